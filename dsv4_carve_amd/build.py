@@ -1,0 +1,72 @@
+"""Builds libexl3_amd.so (gfx950) in-tree with hipcc, one object per bit width in
+parallel, then links.  Usage: python -m dsv4_carve_amd.build [--jobs N]"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT_DIR = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libexl3_amd.so")
+ARCH = os.environ.get("EXL3_OFFLOAD_ARCH", "gfx950")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+COMMON = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    # packed-fp32 instructions are disabled for every HIP object on this target
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+    f"-I{CSRC}",
+]
+
+# (source, extra defines, object name)
+UNITS = [("exl3_capi.hip", [], "exl3_capi.o")]
+UNITS += [("exl3_dense_inst.hip", [f"-DEXL3_BITS={b}"], f"exl3_dense_b{b}.o") for b in range(1, 9)]
+UNITS += [("exl3_moe_capi.hip", [], "exl3_moe_capi.o")]
+# (bit-width mask, codebook) instances of the MoE kernel; keep in sync with
+# EXL3_MOE_INSTANCES in csrc/exl3_moe_capi.hip.
+MOE_UNITS = [(0x004, 1), (0x008, 1), (0x010, 1), (0x040, 1), (0x00C, 1), (0x01C, 1),
+             (0x1FE, 1), (0x1FE, 0), (0x1FE, 2)]
+UNITS += [("exl3_moe_inst.hip", [f"-DEXL3_MOE_MASK=0x{m:03X}u", f"-DEXL3_MOE_CB={c}"],
+           f"exl3_moe_m{m:03x}_c{c}.o") for m, c in MOE_UNITS]
+
+
+def _compile(unit):
+    src, defs, obj = unit
+    out = os.path.join(OUT_DIR, obj)
+    cmd = [HIPCC, *COMMON, *defs, "-c", os.path.join(CSRC, src), "-o", out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "packed-fp32-ops"
+    err = "\n".join(l for l in r.stderr.splitlines() if noise not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src} {defs}:\n{err}")
+    return out
+
+
+def build(jobs: int | None = None, verbose: bool = True) -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    units = [u for u in UNITS if os.path.isfile(os.path.join(CSRC, u[0]))]
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, units))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n" + r.stderr)
+    os.replace(tmp, LIB)
+    if verbose:
+        print(f"built {LIB} from {len(objs)} objects", file=sys.stderr)
+    return LIB
+
+
+if __name__ == "__main__":
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--jobs", type=int, default=None)
+    a = ap.parse_args()
+    build(a.jobs)

@@ -1,0 +1,86 @@
+// C-ABI entry points for the dense path (declared in include/exl3_amd.h):
+//   exl3_dequant            <- dequant_trellis  recipe-lna/lna2/bindings.cpp:118-133
+//                              (raw variant  <- exllamav3 `reconstruct`, recipe-lna/exllamav3/exl3.py.lna:197)
+//   exl3_gemm               <- exl3_gemm        recipe-lna/exllamav3/exl3_gemm.cu.lna:336-364
+//                              (and the exl3_gemv entry, recipe-lna/lna2/bindings.cpp:135-148)
+//   exl3_gemm_scratch_bytes    scratch sizing for exl3_gemm
+//   exl3_last_error            message of the last failed call on this thread
+#include "exl3_dense.hpp"
+
+namespace exl3 {
+// ---------------------------------------------------------------- dispatch tables
+
+#define EXL3_BITS_SWITCH(BITS_VAR, ...)                       \
+    switch (BITS_VAR) {                                        \
+        case 1: { constexpr int B_ = 1; __VA_ARGS__; } break;  \
+        case 2: { constexpr int B_ = 2; __VA_ARGS__; } break;  \
+        case 3: { constexpr int B_ = 3; __VA_ARGS__; } break;  \
+        case 4: { constexpr int B_ = 4; __VA_ARGS__; } break;  \
+        case 5: { constexpr int B_ = 5; __VA_ARGS__; } break;  \
+        case 6: { constexpr int B_ = 6; __VA_ARGS__; } break;  \
+        case 7: { constexpr int B_ = 7; __VA_ARGS__; } break;  \
+        case 8: { constexpr int B_ = 8; __VA_ARGS__; } break;  \
+        default: return fail("bits must be in 1..8");          \
+    }
+
+}  // namespace exl3
+
+using namespace exl3;
+
+extern "C" {
+
+int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int codebook,
+                 const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream) {
+    clear_error();
+    if (!trellis || !out) return fail("null pointer");
+    if (k <= 0 || n <= 0 || k % 16 || n % 16) return fail("k and n must be positive multiples of 16");
+    const bool had = suh != nullptr || svh != nullptr;
+    if (had && (!suh || !svh)) return fail("suh and svh must both be given or both be null");
+    if (had && (k % 128 || n % 128)) return fail("Hadamard-folded dequant needs k, n multiples of 128");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int k16 = (int)(k / 16), n16 = (int)(n / 16);
+    if (codebook < CB_3INST || codebook > CB_MUL1) return fail("codebook must be 0 (3inst), 1 (mcg) or 2 (mul1)");
+    const DequantArgs args{trellis, k16, n16, codebook, had ? suh : nullptr, had ? svh : nullptr, out, s};
+    EXL3_BITS_SWITCH(bits, return launch_dequant<B_>(args));
+    return 0;
+}
+
+int64_t exl3_gemm_scratch_bytes(int64_t m, int64_t k, int64_t n) {
+    clear_error();
+    if (m <= 0 || k <= 0 || n <= 0) return fail("dimensions must be positive");
+    return gemv_scratch_bytes(m, k, n, device_cus());
+}
+
+int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t n, int bits,
+              int codebook, const uint16_t* suh, const uint16_t* svh, void* c, int c_kind,
+              void* scratch, int64_t scratch_bytes, void* stream) {
+    clear_error();
+    if (!a || !b || !c || !suh || !svh || !scratch) return fail("null pointer");
+    if (m <= 0) return fail("m must be positive");
+    if (codebook < CB_3INST || codebook > CB_MUL1) return fail("codebook must be 0 (3inst), 1 (mcg) or 2 (mul1)");
+    if (k <= 0 || k % 128) return fail("k must be a positive multiple of 128");
+    if (n <= 0 || n % 128) return fail("n must be a positive multiple of 128");
+    if (c_kind < OUT_F16 || c_kind > OUT_F32) return fail("c_kind must be 0 (fp16), 1 (bf16) or 2 (fp32)");
+    const int cus = device_cus();
+    if (scratch_bytes < gemv_scratch_bytes(m, k, n, cus)) return fail("scratch too small");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const GemvPlan p = gemv_plan(m, k, n, cus);
+    int* counters = reinterpret_cast<int*>(scratch);
+    float* partials = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) +
+                                               align_up((int64_t)p.n_cb * 4, 256));
+    const size_t c_elem = c_kind == OUT_F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < m; r0 += MAX_ROWS) {
+        const int R = (int)(m - r0 < MAX_ROWS ? m - r0 : MAX_ROWS);
+        const uint16_t* ar = a + r0 * k;
+        void* cr = reinterpret_cast<char*>(c) + (size_t)r0 * n * c_elem;
+        const GemvArgs args{ar, b, suh, svh, cr, c_kind, R, (int)k, (int)n, p, codebook, counters, partials, s};
+        int rc = 0;
+        EXL3_BITS_SWITCH(bits, rc = launch_gemv<B_>(args));
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+}  // extern "C"
+
+extern "C" const char* exl3_last_error(void) { return exl3::g_last_error; }

@@ -1,0 +1,208 @@
+// Dense EXL3 kernels for gfx950: trellis dequant (raw and Hadamard-folded) and
+// the small-row GEMV/GEMM y = had_out(had_in(x) . Wq) * svh.  Templates only;
+// exl3_dense_inst.hip instantiates them once per bit width.
+#pragma once
+
+#include "exl3_gemv.hpp"
+#include "exl3_capi_util.hpp"
+
+namespace exl3 {
+
+// ---------------------------------------------------------------- dequant (raw)
+
+// One lane per tile; writes the 16x16 fp16 block in row-major [K][N].
+template <int BITS, int CB>
+__global__ __launch_bounds__(64) void dequant_raw_kernel(const int16_t* __restrict__ trellis,
+                                                         int k16, int n16, uint16_t* __restrict__ out) {
+    const int tile = blockIdx.x * 64 + threadIdx.x;
+    if (tile >= k16 * n16) return;
+    const int kt = tile / n16, nt = tile - kt * n16;
+    TileRegs<BITS> t;
+    load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) + (size_t)tile * TileRegs<BITS>::NV);
+    const uint32_t* W = t.words();
+    const size_t N = (size_t)n16 * 16;
+    static_for<16>([&](auto KI) {
+        constexpr int k = decltype(KI)::value;
+        u32x4_t row[2];
+        static_for<8>([&](auto PI) {
+            constexpr int p = decltype(PI)::value;
+            const uint32_t lo = decode_half<BITS, CB, tile_t(k, 2 * p)>(W);
+            const uint32_t hi = decode_half<BITS, CB, tile_t(k, 2 * p + 1)>(W);
+            row[p >> 2][p & 3] = lo | (hi << 16);
+        });
+        u32x4_t* o = reinterpret_cast<u32x4_t*>(out + (size_t)(kt * 16 + k) * N + nt * 16);
+        o[0] = row[0];
+        o[1] = row[1];
+    });
+}
+
+// ---------------------------------------------------------------- dequant (Hadamard folded)
+
+// W = diag(suh) H Wq H diag(svh) / 128, one wave per 128x128 block, in the
+// operation order of dequant_cpu (recipe-lna/lna2/bindings.cpp:80-99): row
+// transforms (* 1/sqrt(128)), then column transforms, value = ((v*norm)*su)*sv.
+constexpr int HB_LD = 129;   // padded LDS row (floats)
+
+__device__ __forceinline__ void fwht128_regs(float (&v)[128]) {
+    static_for<7>([&](auto SI) {
+        constexpr int h = 1 << decltype(SI)::value;
+        static_for<64>([&](auto JI) {
+            constexpr int j = decltype(JI)::value;
+            constexpr int i = (j / h) * 2 * h + (j % h);
+            const float a = v[i], b = v[i + h];
+            v[i] = a + b;
+            v[i + h] = a - b;
+        });
+    });
+}
+
+template <int BITS, int CB>
+__global__ __launch_bounds__(64) void dequant_had_kernel(const int16_t* __restrict__ trellis, int k16,
+                                                         int n16, const uint16_t* __restrict__ suh,
+                                                         const uint16_t* __restrict__ svh,
+                                                         uint16_t* __restrict__ out) {
+    __shared__ float mat[128 * HB_LD];
+    const int lane = threadIdx.x;
+    const int nbc = n16 / 8;
+    const int br = blockIdx.x / nbc, bc = blockIdx.x - br * nbc;
+    const size_t N = (size_t)n16 * 16;
+    {
+        const int kt = 8 * br + (lane >> 3), nt = 8 * bc + (lane & 7);
+        TileRegs<BITS> t;
+        load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) +
+                               ((size_t)kt * n16 + nt) * TileRegs<BITS>::NV);
+        const uint32_t* W = t.words();
+        float* base = mat + (16 * (lane >> 3)) * HB_LD + 16 * (lane & 7);
+        static_for<16>([&](auto KI) {
+            constexpr int k = decltype(KI)::value;
+            static_for<16>([&](auto NI) {
+                constexpr int n = decltype(NI)::value;
+                base[k * HB_LD + n] = f16_bits_to_f32(decode_half<BITS, CB, tile_t(k, n)>(W));
+            });
+        });
+    }
+    __syncthreads();
+    for (int rr = lane; rr < 128; rr += 64) {
+        float v[128];
+#pragma unroll
+        for (int c = 0; c < 128; ++c) v[c] = mat[rr * HB_LD + c];
+        fwht128_regs(v);
+#pragma unroll
+        for (int c = 0; c < 128; ++c) mat[rr * HB_LD + c] = v[c] * HAD_NORM;
+    }
+    __syncthreads();
+    for (int cc = lane; cc < 128; cc += 64) {
+        float v[128];
+#pragma unroll
+        for (int r = 0; r < 128; ++r) v[r] = mat[r * HB_LD + cc];
+        fwht128_regs(v);
+        const float sv = f16_bits_to_f32(svh[128 * bc + cc]);
+#pragma unroll
+        for (int r = 0; r < 128; ++r) {
+            float x = v[r] * HAD_NORM;
+            x = x * f16_bits_to_f32(suh[128 * br + r]);
+            x = x * sv;
+            out[(size_t)(128 * br + r) * N + 128 * bc + cc] = f32_to_f16_bits(x);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- dense GEMV
+
+constexpr int GEMV_NSTEP_CAP = 8;   // k rows per item <= 512
+
+struct GemvPlan {
+    int nsteps;   // steps (64 k-rows) per item, even
+    int n_kc;     // k-chunks
+    int n_cb;     // 256-column blocks
+};
+
+inline GemvPlan gemv_plan(int64_t rows, int64_t k, int64_t n, int cus) {
+    GemvPlan p;
+    p.n_cb = (int)((n + COLS - 1) / COLS);
+    const int ksteps = (int)(k / STEP_K);
+    // Aim for >= ~4 waves per CU while keeping the split-K partial traffic
+    // (rows * n * 4 bytes per chunk) small next to the weight bytes.
+    int nsteps = GEMV_NSTEP_CAP;
+    while (nsteps > 2 && (int64_t)p.n_cb * (ksteps / nsteps) < 4LL * cus && rows <= 4) nsteps /= 2;
+    while (ksteps % nsteps) nsteps /= 2;
+    if (nsteps < 2) nsteps = 2;
+    p.nsteps = nsteps;
+    p.n_kc = ksteps / nsteps;
+    return p;
+}
+
+inline int64_t gemv_scratch_bytes(int64_t rows, int64_t k, int64_t n, int cus) {
+    const GemvPlan p = gemv_plan(rows, k, n, cus);
+    const int64_t ctr = align_up((int64_t)p.n_cb * 4, 256);
+    return ctr + (int64_t)p.n_kc * (rows < 16 ? rows : 16) * n * 4;
+}
+
+template <int BITS, int CB>
+__global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x,
+                                                  const int16_t* __restrict__ trellis,
+                                                  const uint16_t* __restrict__ suh,
+                                                  const uint16_t* __restrict__ svh, void* __restrict__ out,
+                                                  int out_kind, int R, int K, int N, int nsteps, int n_kc,
+                                                  int* __restrict__ counters, float* __restrict__ partials) {
+    __shared__ uint16_t xa[MAX_ROWS * GEMV_NSTEP_CAP * STEP_K];
+    const int lane = threadIdx.x;
+    const int cb = blockIdx.x / n_kc, kc = blockIdx.x - cb * n_kc;
+    const int k0 = kc * nsteps * STEP_K;
+
+    for (int m = 0; m < R; ++m)
+        for (int b = 0; b < nsteps * STEP_K; b += 128)
+            had_in_block(x, (size_t)m * K + k0 + b, 0, suh + k0 + b, xa, m, b, GEMV_NSTEP_CAP);
+    __syncthreads();
+
+    float4_t acc[16];
+    mma_steps<BITS, CB>(trellis, N / 16, k0 / 16, nsteps, cb * 16, xa, GEMV_NSTEP_CAP, R, acc);
+
+    const int cols = min(COLS, N - cb * COLS);
+    store_partials(acc, partials + (size_t)kc * R * N + cb * COLS, N, R, cols);
+    __threadfence();
+    int old = 0;
+    if (lane == 0) old = atomicAdd(&counters[cb], 1);
+    old = __shfl(old, 0, 64);
+    if (old != n_kc - 1) return;
+    __threadfence();
+
+    // Last arriver: fixed-order split-K sum, output Hadamard, svh, store.
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    const bool ok = col < N;
+    float sv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (ok)
+        for (int e = 0; e < 4; ++e) sv[e] = f16_bits_to_f32(svh[col + e]);
+    for (int m = 0; m < R; ++m) {
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (ok) {
+            for (int s = 0; s < n_kc; ++s) {
+                const float4_t p = __builtin_nontemporal_load(
+                    reinterpret_cast<const float4_t*>(partials + ((size_t)s * R + m) * N + col));
+                v[0] += p[0]; v[1] += p[1]; v[2] += p[2]; v[3] += p[3];
+            }
+        }
+        fwht128_x4(v);
+        if (ok)
+            for (int e = 0; e < 4; ++e) store_out(out, (size_t)m * N + col + e, out_kind, v[e] * HAD_NORM * sv[e]);
+    }
+    if (lane == 0) counters[cb] = 0;
+}
+
+// ---------------------------------------------------------------- per-bit-width launchers
+
+struct DequantArgs {
+    const int16_t* trellis; int k16, n16; int codebook;
+    const uint16_t* suh; const uint16_t* svh; uint16_t* out; hipStream_t stream;
+};
+struct GemvArgs {
+    const uint16_t* x; const int16_t* trellis; const uint16_t* suh; const uint16_t* svh;
+    void* out; int out_kind; int R, K, N; GemvPlan plan; int codebook;
+    int* counters; float* partials; hipStream_t stream;
+};
+
+// Defined in exl3_dense_inst.hip, one translation unit per BITS.
+template <int BITS> int launch_dequant(const DequantArgs& a);
+template <int BITS> int launch_gemv(const GemvArgs& a);
+
+}  // namespace exl3

@@ -1,0 +1,262 @@
+// Shared GEMV machinery: tile-per-lane trellis decode feeding
+// v_mfma_f32_16x16x32_f16, plus the 128-point Hadamard rotations on wave64.
+//
+// One wave processes a "step" = 4 k-slices x 16 n-tiles = 64 tiles = 64x256
+// weights.  Lane l owns tile (k-slice 4s + l/16, n-tile l%16).  For output
+// column n of the tile and k-group r (k in 2r+{0,1,8,9}) the four windows are
+// t = 32(n&7) + 8r + 4(n>>3) + q, q = 0..3 (consecutive, see the permutation in
+// exl3_decode.hpp).  The MFMA's B operand for lane l is those four weights as
+// (lo, hi) fp16 addend pairs -> 8 K-slots; the A operand for lane l (row l%16,
+// same k-group of k-slice 4s + l/16) is the four matching activations, each
+// duplicated.  One MFMA therefore consumes 256 weights: column n of sixteen
+// n-tiles across four k-slices.  The MFMA k-slot <-> k assignment is a free
+// permutation (a sum is order-free up to fp32 rounding), chosen so every
+// window position is a compile-time constant.
+//
+// Reference counterparts: the small-R GEMV core recipe-lna/lna2/lna_gemv_core.cuh:63-240
+// (register decode + m16n8k16 MMA with fp16 accumulate folded to fp32) and the
+// in/out Hadamard recipe-lna/lna2/lna_moe_ticket.cu:119-144, 342-343.
+#pragma once
+
+#include "exl3_decode.hpp"
+
+namespace exl3 {
+
+constexpr int WAVE = 64;
+constexpr int STEP_K = 64;          // k rows per step (4 k-slices)
+constexpr int COLS = 256;           // output columns per item (16 n-tiles)
+constexpr int MAX_ROWS = 16;        // MFMA M
+
+// LDS layout of the A operand for one item: halves [16 rows][nsteps][4 g][4 r][4 q]
+__device__ __forceinline__ int xa_index(int m, int s, int nsteps_cap, int kk /*0..63*/) {
+    const int g = kk >> 4, k16 = kk & 15;
+    const int r = (k16 & 7) >> 1, q = (k16 & 1) + 2 * (k16 >> 3);
+    return ((m * nsteps_cap + s) * 4 + g) * 16 + r * 4 + q;
+}
+
+// Where the 16-bit window of element T comes from: the low or high half of
+// either a tile word (free) or one funnel shift.  When 16 % BITS == 0 two
+// windows 16 bits apart share one funnel (high half = the earlier window).
+template <int BITS, int T>
+struct WinSel {
+    static constexpr int NB = 256 * BITS;
+    static constexpr int E0 = ((T + 1) * BITS) % NB;
+    static constexpr int E = E0 == 0 ? NB : E0;
+    static constexpr int I1 = (E - 1) >> 5;
+    static constexpr int O = E - 32 * I1;
+    static constexpr bool PAIRED = (16 % BITS == 0) && (O != 16) && (O != 32) &&
+                                   (((T / (16 / BITS)) & 1) == 0);
+    // PAIRED: take window (T + 16/BITS) mod 256's funnel and use its high half.
+    static constexpr int SRC_T = PAIRED ? (T + 16 / BITS) % 256 : T;
+    static constexpr bool HI = PAIRED || (O == 16);
+};
+
+template <int BITS, int T>
+__device__ __forceinline__ uint32_t win_src(const uint32_t* W) {
+    using S = WinSel<BITS, T>;
+    if constexpr (!S::PAIRED && S::O == 16) return W[S::I1];
+    else return win_lo<BITS, S::SRC_T>(W);
+}
+
+template <int BITS, int CB, int T>
+__device__ __forceinline__ uint32_t decode_pair(const uint32_t* W) {
+    return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
+}
+template <int BITS, int CB, int T>
+__device__ __forceinline__ uint16_t decode_half(const uint32_t* W) {
+    return codebook_half<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
+}
+
+// ---------------------------------------------------------------- tile loads
+
+template <int BITS>
+struct TileRegs {
+    static constexpr int NV = 2 * BITS;     // 16-byte vectors per tile (32*BITS bytes)
+    u32x4_t v[NV];
+    __device__ __forceinline__ const uint32_t* words() const {
+        return reinterpret_cast<const uint32_t*>(v);
+    }
+};
+
+template <int BITS>
+__device__ __forceinline__ void load_tile(TileRegs<BITS>& t, const u32x4_t* p) {
+#pragma unroll
+    for (int i = 0; i < TileRegs<BITS>::NV; ++i) t.v[i] = __builtin_nontemporal_load(p + i);
+}
+
+// ---------------------------------------------------------------- MFMA step
+
+// Builds the duplicated A operand for k-group r of this lane from the LDS tile.
+__device__ __forceinline__ half8_t a_operand(const uint16_t* xa, int m, int s, int nsteps_cap,
+                                             int g, int r, bool live) {
+    uint2 v = make_uint2(0u, 0u);
+    if (live) v = *reinterpret_cast<const uint2*>(xa + ((m * nsteps_cap + s) * 4 + g) * 16 + r * 4);
+    u32x4_t d;
+    d[0] = (v.x & 0xffffu) | (v.x << 16);
+    d[1] = (v.x >> 16) | (v.x & 0xffff0000u);
+    d[2] = (v.y & 0xffffu) | (v.y << 16);
+    d[3] = (v.y >> 16) | (v.y & 0xffff0000u);
+    return __builtin_bit_cast(half8_t, d);
+}
+
+// Decodes all 256 weights of the lane's tile and accumulates 64 MFMAs into acc.
+template <int BITS, int CB>
+__device__ __forceinline__ void mma_tile(const uint32_t* W, const half8_t (&A)[4], float4_t (&acc)[16]) {
+    static_for<16>([&](auto NI) {
+        constexpr int n = decltype(NI)::value;
+        static_for<4>([&](auto RI) {
+            constexpr int r = decltype(RI)::value;
+            constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+            u32x4_t b;
+            b[0] = decode_pair<BITS, CB, T0 + 0>(W);
+            b[1] = decode_pair<BITS, CB, T0 + 1>(W);
+            b[2] = decode_pair<BITS, CB, T0 + 2>(W);
+            b[3] = decode_pair<BITS, CB, T0 + 3>(W);
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], __builtin_bit_cast(half8_t, b),
+                                                            acc[n], 0, 0, 0);
+        });
+    });
+}
+
+// Runs `nsteps` (even) steps over k-slices [ks0, ks0 + 4*nsteps) for n-tiles
+// [nt0, nt0+16).  xa: LDS A tile for this item (see xa_index).  Lanes whose
+// n-tile is past the matrix decode a valid tile and their columns are dropped.
+template <int BITS, int CB>
+__device__ __forceinline__ void mma_steps(const int16_t* __restrict__ trellis, int n16, int ks0,
+                                          int nsteps, int nt0, const uint16_t* xa, int nsteps_cap,
+                                          int R, float4_t (&acc)[16]) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int g = lane >> 4, c = lane & 15;
+    const int nt = min(nt0 + c, n16 - 1);
+    constexpr int NV = TileRegs<BITS>::NV;
+    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(trellis) +
+                       ((size_t)(ks0 + g) * n16 + nt) * NV;
+    const size_t step = (size_t)4 * n16 * NV;
+    const bool live = c < R;
+
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    // nsteps is always even: two steps per iteration, ping-ponging the tile registers
+    TileRegs<BITS> buf[2];
+    load_tile<BITS>(buf[0], p);
+    for (int s = 0; s < nsteps; s += 2) {
+        load_tile<BITS>(buf[1], p + (s + 1) * step);
+        {
+            half8_t A[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, c, s, nsteps_cap, g, r, live);
+            mma_tile<BITS, CB>(buf[0].words(), A, acc);
+        }
+        if (s + 2 < nsteps) load_tile<BITS>(buf[0], p + (s + 2) * step);
+        {
+            half8_t A[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, c, s + 1, nsteps_cap, g, r, live);
+            mma_tile<BITS, CB>(buf[1].words(), A, acc);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- Hadamard (wave64)
+
+// In-place natural-order 128-point FWHT of a block held as 2 consecutive
+// elements per lane (element 2l+e in lane l), fp32, same add/sub sequence per
+// element as the scalar loop in orders/F1-ref/exl3_dequant.cuh:136-147.
+__device__ __forceinline__ void fwht128_x2(float& v0, float& v1) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    {
+        const float a = v0, b = v1;
+        v0 = a + b;
+        v1 = a - b;
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const float p0 = shfl_xor(v0, m), p1 = shfl_xor(v1, m);
+        const bool upper = (lane & m) != 0;
+        v0 = upper ? p0 - v0 : v0 + p0;
+        v1 = upper ? p1 - v1 : v1 + p1;
+    }
+}
+
+// Same transform for two independent 128-blocks, 4 consecutive elements per
+// lane: lanes 0-31 hold block 0, lanes 32-63 block 1 (element 4j+e of the block
+// in lane j of the half-wave).
+__device__ __forceinline__ void fwht128_x4(float (&v)[4]) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    {
+        float a = v[0], b = v[1];
+        v[0] = a + b; v[1] = a - b;
+        a = v[2]; b = v[3];
+        v[2] = a + b; v[3] = a - b;
+        a = v[0]; b = v[2];
+        v[0] = a + b; v[2] = a - b;
+        a = v[1]; b = v[3];
+        v[1] = a + b; v[3] = a - b;
+    }
+#pragma unroll
+    for (int m = 1; m < 32; m <<= 1) {
+        const bool upper = (lane & m) != 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float p = shfl_xor(v[e], m);
+            v[e] = upper ? p - v[e] : v[e] + p;
+        }
+    }
+}
+
+// Input rotation of one 128-element block into the LDS A tile:
+// xh = half( H (half(x * suh)) / sqrt(128) ), lna_moe_ticket.cu:119-144.
+// x_kind: 0 = fp16, 1 = bf16 (converted to fp16 with RNE first).
+__device__ __forceinline__ void had_in_block(const void* x, size_t x_off, int x_kind,
+                                             const uint16_t* suh, uint16_t* xa, int m,
+                                             int kblock_local /* multiple of 128 */, int nsteps_cap) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    uint32_t xx;
+    if (x_kind == 0) {
+        xx = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + x_off + 2 * lane);
+    } else {
+        const uint32_t b = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + x_off + 2 * lane);
+        xx = (uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(b & 0xffffu))) |
+             ((uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(b >> 16))) << 16);
+    }
+    const uint32_t ss = *reinterpret_cast<const uint32_t*>(suh + 2 * lane);
+    // half(x*suh): the fp32 product of two halves is exact, so one RNE cast = half mul
+    float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(xx & 0xffffu) * f16_bits_to_f32(ss & 0xffffu)));
+    float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(xx >> 16) * f16_bits_to_f32(ss >> 16)));
+    fwht128_x2(v0, v1);
+    const int k0 = kblock_local + 2 * lane;
+    xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = f32_to_f16_bits(v0 * HAD_NORM);
+    xa[xa_index(m, (k0 + 1) >> 6, nsteps_cap, (k0 + 1) & 63)] = f32_to_f16_bits(v1 * HAD_NORM);
+}
+
+// Copies an already-rotated fp16 block (128 elements) into the LDS A tile.
+__device__ __forceinline__ void copy_block(const uint16_t* src, uint16_t* xa, int m, int kblock_local,
+                                           int nsteps_cap) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(src + 2 * lane);
+    const int k0 = kblock_local + 2 * lane;
+    xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = (uint16_t)(v & 0xffffu);
+    xa[xa_index(m, (k0 + 1) >> 6, nsteps_cap, (k0 + 1) & 63)] = (uint16_t)(v >> 16);
+}
+
+// Writes the 16 accumulators of one item (rows < R) as fp32 partials
+// dst[row * ld + col], col = 16 * (n-tile) + n within the 256-column block.
+__device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float* dst, size_t ld,
+                                               int R, int cols_valid) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int c = lane & 15, rg = lane >> 4;
+    if (16 * c >= cols_valid) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = 4 * rg + i;
+        if (row < R) {
+            float4_t* o = reinterpret_cast<float4_t*>(dst + (size_t)row * ld + 16 * c);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                o[q] = float4_t{acc[4 * q][i], acc[4 * q + 1][i], acc[4 * q + 2][i], acc[4 * q + 3][i]};
+        }
+    }
+}
+
+}  // namespace exl3

@@ -1,0 +1,426 @@
+// Routed-MoE decode layer for gfx950: one launch computes, for up to 16 rows,
+//   out[r] = sum_j w[r][j] * down_e(half(silu(min(gate_e(x_r), L)) * clamp(up_e(x_r), -L, L)))
+// over the top-k experts e of each row (precision boundaries of the lna2 canon,
+// recipe-lna/lna2/lna_moe_ticket.cu:5-12).
+//
+// Scheduler (re-derived for 256 CUs, no grid barrier, no co-residency assumption):
+//   * Persistent single-wave workgroups draw tickets from one atomic counter.
+//   * Ticket order: every gate/up item of every active expert, then every
+//     down item.  Item = (expert group, projection, 256-column block, k-chunk).
+//   * gate/up items write fp32 partials; the last arriver of a (group, column
+//     block) sums them in fixed order, applies the output Hadamard + svh, the
+//     clamped SwiGLU, the down projection's suh + input Hadamard, stores the
+//     fp16 down input and publishes an epoch flag.
+//   * A down item spins on the flags of the column blocks it reads.  Those were
+//     ticketed earlier and never wait, so every wait ends whatever the number
+//     of resident waves.
+//   * down items write partials; the last arriver of a (group, H-block) applies
+//     the output Hadamard + svh; the last group to finish an H-block gathers the
+//     block of `out` in top-k slot order (fp32) and casts once.
+//   * Counters are reset by whoever consumes them; flags compare against an
+//     epoch the last retiring wave advances, so the control block is zeroed once.
+// Reference counterpart: lna2_kernel<K> (lna_moe_ticket.cu:240-429), whose expert
+// teams need co-resident CTAs and a team barrier (lna_moe_ticket.cu:459-466).
+#pragma once
+
+#include "exl3_gemv.hpp"
+#include "exl3_capi_util.hpp"
+
+namespace exl3 {
+namespace moe {
+
+constexpr int MAX_M = 16;
+constexpr int MAX_TOPK = 8;
+constexpr int MAX_SLOTS = MAX_M * MAX_TOPK;   // also the bound on groups and pairs
+constexpr int MAX_EXPERTS = 2048;             // route-plan bitmask capacity
+constexpr int NSTEP_CAP = 8;
+
+// Steps (64 k-rows each) per item: the largest even divisor of k/64 that is <= 8.
+__host__ __device__ inline int item_steps(int k) {
+    const int ks = k / STEP_K;
+    int s = NSTEP_CAP;
+    while (s > 2 && ks % s) s -= 2;
+    return s;
+}
+
+struct Layout {
+    int nI, nH, SA, SB, stepsA, stepsB;
+    int64_t ctrl, cntA, doneA, cntB, cntG, PA, DI, PB, DC, total;
+};
+
+__host__ __device__ inline int64_t al(int64_t v) { return (v + 255) / 256 * 256; }
+
+__host__ __device__ inline Layout layout(int H, int I, int topk) {
+    Layout L;
+    L.nI = I / COLS;
+    L.nH = H / COLS;
+    L.stepsA = item_steps(H);
+    L.stepsB = item_steps(I);
+    L.SA = H / STEP_K / L.stepsA;
+    L.SB = I / STEP_K / L.stepsB;
+    const int64_t P = (int64_t)MAX_M * topk;      // max pairs = max groups
+    int64_t o = 0;
+    L.ctrl = o;  o += 256;
+    L.cntA = o;  o = al(o + P * L.nI * 4);
+    L.doneA = o; o = al(o + P * L.nI * 4);
+    L.cntB = o;  o = al(o + P * L.nH * 4);
+    L.cntG = o;  o = al(o + (int64_t)L.nH * 4);
+    L.PA = o;    o = al(o + P * 2 * L.SA * I * 4);
+    L.DI = o;    o = al(o + P * I * 2);
+    L.PB = o;    o = al(o + P * L.SB * H * 4);
+    L.DC = o;    o = al(o + P * H * 4);
+    L.total = o;
+    return L;
+}
+
+// Control words at the head of the scratch buffer.
+struct Ctrl {
+    int ticket;
+    int retire;
+    int epoch;
+    int error;
+};
+
+struct Params {
+    const void* x; int x_kind;
+    void* out; int out_kind;
+    int m, H, I, E, topk;
+    const int64_t* gt; const int64_t* gsu; const int64_t* gsv;
+    const int64_t* ut; const int64_t* usu; const int64_t* usv;
+    const int64_t* dt; const int64_t* dsu; const int64_t* dsv;
+    const int32_t* ids; const float* w;
+    const int8_t* ebits; int bits;
+    float limit;
+    char* scratch;
+    Layout L;
+};
+
+template <typename T>
+__device__ __forceinline__ T* at(char* base, int64_t off) { return reinterpret_cast<T*>(base + off); }
+
+// ---------------------------------------------------------------- route plan
+
+struct Plan {
+    int U;                       // active expert groups (ascending expert id)
+    int gexp[MAX_SLOTS];
+    int gpair[MAX_SLOTS];        // first pair index of the group
+    uint32_t gmask[MAX_SLOTS];   // row bitmask
+    int8_t gbits[MAX_SLOTS];
+    int16_t slotpair[MAX_SLOTS]; // pair of slot (row*topk + j), -1 if invalid
+};
+
+// Expert-major row bitmask, then a wave-wide exclusive scan over experts
+// (lna_moe_ticket.cu:167-214 computes the same plan with block scans).
+// `tmp` (>= E*6 bytes of LDS) is only used during planning.
+__device__ inline void build_plan(const Params& P, Plan& pl, char* tmp) {
+    const int lane = threadIdx.x;
+    uint32_t* rowmask = reinterpret_cast<uint32_t*>(tmp);
+    int16_t* epair = reinterpret_cast<int16_t*>(tmp + 4 * MAX_EXPERTS);
+    for (int e = lane; e < P.E; e += WAVE) rowmask[e] = 0u;
+    __syncthreads();
+    const int slots = P.m * P.topk;
+    for (int s = lane; s < slots; s += WAVE) {
+        const int id = P.ids[s];
+        if (id >= 0 && id < P.E) atomicOr(&rowmask[id], 1u << (s / P.topk));
+    }
+    __syncthreads();
+    const int chunk = (P.E + WAVE - 1) / WAVE;
+    const int e0 = lane * chunk, e1 = min(P.E, e0 + chunk);
+    int ng = 0, np = 0;
+    for (int e = e0; e < e1; ++e) {
+        const uint32_t mk = rowmask[e];
+        ng += mk != 0u;
+        np += __popc(mk);
+    }
+    int sg = ng, sp = np;   // inclusive scans
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const int a = __shfl_up(sg, d, WAVE), b = __shfl_up(sp, d, WAVE);
+        if (lane >= d) { sg += a; sp += b; }
+    }
+    int gx = sg - ng, px = sp - np;
+    for (int e = e0; e < e1; ++e) {
+        const uint32_t mk = rowmask[e];
+        epair[e] = (int16_t)px;
+        if (mk) {
+            pl.gexp[gx] = e;
+            pl.gpair[gx] = px;
+            pl.gmask[gx] = mk;
+            pl.gbits[gx] = (int8_t)(P.ebits ? P.ebits[e] : P.bits);
+            ++gx;
+            px += __popc(mk);
+        }
+    }
+    if (lane == WAVE - 1) pl.U = sg;
+    __syncthreads();
+    for (int s = lane; s < slots; s += WAVE) {
+        const int id = P.ids[s];
+        int16_t pr = -1;
+        if (id >= 0 && id < P.E) {
+            const int row = s / P.topk;
+            pr = (int16_t)(epair[id] + __popc(rowmask[id] & ((1u << row) - 1u)));
+        }
+        pl.slotpair[s] = pr;
+    }
+    __syncthreads();
+}
+
+// Row index of the i-th set bit of mask.
+__device__ __forceinline__ int nth_row(uint32_t mask, int i) {
+    for (int k = 0; k < i; ++k) mask &= mask - 1u;
+    return __ffs((int)mask) - 1;
+}
+
+// ---------------------------------------------------------------- device sync helpers
+
+__device__ __forceinline__ int wave_atomic_add(int* p, int v) {
+    int old = 0;
+    if (threadIdx.x == 0) old = atomicAdd(p, v);
+    return __shfl(old, 0, WAVE);
+}
+
+__device__ __forceinline__ void wait_flag(int* flag, int target) {
+    if (threadIdx.x == 0) {
+        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target)
+            __builtin_amdgcn_s_sleep(2);
+    }
+    __syncthreads();
+    __threadfence();
+}
+
+__device__ __forceinline__ float silu_clamped(float g, float u, float limit) {
+    // comparisons leave NaN untouched, as in lna_moe_ticket.cu:350-352
+    if (g > limit) g = limit;
+    if (u < -limit) u = -limit;
+    if (u > limit) u = limit;
+    return (g / (1.0f + expf(-g))) * u;
+}
+
+// ---------------------------------------------------------------- items
+
+template <uint32_t MASK, int CB>
+__device__ __forceinline__ void run_mma(int bits, const int16_t* trellis, int n16, int ks0, int nsteps,
+                                        int nt0, const uint16_t* xa, int R, float4_t (&acc)[16],
+                                        int* err) {
+    bool done = false;
+    static_for<8>([&](auto BI) {
+        constexpr int B = decltype(BI)::value + 1;
+        if constexpr ((MASK >> B) & 1u) {
+            if (!done && bits == B) {
+                mma_steps<B, CB>(trellis, n16, ks0, nsteps, nt0, xa, NSTEP_CAP, R, acc);
+                done = true;
+            }
+        }
+    });
+    if (!done) {
+        if (threadIdx.x == 0) atomicOr(err, 1);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
+    }
+}
+
+// gate/up item
+template <uint32_t MASK, int CB>
+__device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch) {
+    const Layout& L = P.L;
+    const int per_g = 2 * L.nI * L.SA;
+    const int g = t / per_g;
+    int rem = t - g * per_g;
+    const int p = rem / (L.nI * L.SA);
+    rem -= p * L.nI * L.SA;
+    const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
+    const int e = pl.gexp[g], pb = pl.gpair[g];
+    const uint32_t mask = pl.gmask[g];
+    const int R = __popc(mask);
+    const int kchunk = L.stepsA * STEP_K;
+    const int k0 = kc * kchunk;
+
+    const uint16_t* suh = reinterpret_cast<const uint16_t*>((p ? P.usu : P.gsu)[e]);
+    for (int r = 0; r < R; ++r) {
+        const int row = nth_row(mask, r);
+        for (int b = 0; b < kchunk; b += 128)
+            had_in_block(P.x, (size_t)row * P.H + k0 + b, P.x_kind, suh + k0 + b, xa, r, b, NSTEP_CAP);
+    }
+    __syncthreads();
+
+    float4_t acc[16];
+    const int16_t* tr = reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]);
+    Ctrl* ctrl = at<Ctrl>(P.scratch, L.ctrl);
+    run_mma<MASK, CB>(pl.gbits[g], tr, P.I / 16, k0 / 16, L.stepsA, cb * 16, xa, R, acc, &ctrl->error);
+
+    float* PA = at<float>(P.scratch, L.PA);
+    const size_t ld = (size_t)2 * L.SA * P.I;
+    store_partials(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, ld, R, COLS);
+    __threadfence();
+    int* cnt = at<int>(P.scratch, L.cntA) + g * L.nI + cb;
+    if (wave_atomic_add(cnt, 1) != 2 * L.SA - 1) return;
+    __threadfence();
+
+    // Last arriver: gate/up epilogue for (group g, column block cb).
+    const int lane = threadIdx.x;
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    const uint16_t* gsv = reinterpret_cast<const uint16_t*>(P.gsv[e]);
+    const uint16_t* usv = reinterpret_cast<const uint16_t*>(P.usv[e]);
+    const uint16_t* dsu = reinterpret_cast<const uint16_t*>(P.dsu[e]);
+    uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
+    for (int r = 0; r < R; ++r) {
+        const int pair = pb + r;
+        float gv[4] = {0.f, 0.f, 0.f, 0.f}, uv[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < L.SA; ++s) {
+            const float4_t a = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(
+                PA + ((size_t)(pair * 2 + 0) * L.SA + s) * P.I + col));
+            const float4_t b = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(
+                PA + ((size_t)(pair * 2 + 1) * L.SA + s) * P.I + col));
+            gv[0] += a[0]; gv[1] += a[1]; gv[2] += a[2]; gv[3] += a[3];
+            uv[0] += b[0]; uv[1] += b[1]; uv[2] += b[2]; uv[3] += b[3];
+        }
+        fwht128_x4(gv);
+        fwht128_x4(uv);
+        float dv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float gg = gv[i] * HAD_NORM * f16_bits_to_f32(gsv[col + i]);
+            const float uu = uv[i] * HAD_NORM * f16_bits_to_f32(usv[col + i]);
+            const uint16_t act = f32_to_f16_bits(silu_clamped(gg, uu, P.limit));
+            // down input rotation: half(act * down_suh), fp32 butterflies
+            dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[col + i])));
+        }
+        fwht128_x4(dv);
+        uint2 packed;
+        packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
+        packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
+        *reinterpret_cast<uint2*>(DI + (size_t)pair * P.I + col) = packed;
+    }
+    if (lane == 0) *cnt = 0;
+    __threadfence();
+    if (lane == 0)
+        __hip_atomic_store(at<int>(P.scratch, L.doneA) + g * L.nI + cb, epoch + 1, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// down item
+template <uint32_t MASK, int CB>
+__device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch) {
+    const Layout& L = P.L;
+    const int per_g = L.nH * L.SB;
+    const int g = t / per_g;
+    const int rem = t - g * per_g;
+    const int cb = rem / L.SB, kc = rem - (rem / L.SB) * L.SB;
+    const int e = pl.gexp[g], pb = pl.gpair[g];
+    const uint32_t mask = pl.gmask[g];
+    const int R = __popc(mask);
+    const int kchunk = L.stepsB * STEP_K;
+    const int k0 = kc * kchunk;
+
+    // wait for the gate/up column blocks this chunk reads
+    int* doneA = at<int>(P.scratch, L.doneA) + g * L.nI;
+    for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c) wait_flag(doneA + c, epoch + 1);
+
+    const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
+    for (int r = 0; r < R; ++r)
+        for (int b = 0; b < kchunk; b += 128)
+            copy_block(DI + (size_t)(pb + r) * P.I + k0 + b, xa, r, b, NSTEP_CAP);
+    __syncthreads();
+
+    float4_t acc[16];
+    const int16_t* tr = reinterpret_cast<const int16_t*>(P.dt[e]);
+    Ctrl* ctrl = at<Ctrl>(P.scratch, L.ctrl);
+    run_mma<MASK, CB>(pl.gbits[g], tr, P.H / 16, k0 / 16, L.stepsB, cb * 16, xa, R, acc, &ctrl->error);
+
+    float* PB = at<float>(P.scratch, L.PB);
+    store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS);
+    __threadfence();
+    int* cnt = at<int>(P.scratch, L.cntB) + g * L.nH + cb;
+    if (wave_atomic_add(cnt, 1) != L.SB - 1) return;
+    __threadfence();
+
+    // Last arriver for (group, H block): output rotation + svh.
+    const int lane = threadIdx.x;
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    const uint16_t* dsv = reinterpret_cast<const uint16_t*>(P.dsv[e]);
+    float* DC = at<float>(P.scratch, L.DC);
+    for (int r = 0; r < R; ++r) {
+        const int pair = pb + r;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < L.SB; ++s) {
+            const float4_t a = __builtin_nontemporal_load(
+                reinterpret_cast<const float4_t*>(PB + ((size_t)pair * L.SB + s) * P.H + col));
+            v[0] += a[0]; v[1] += a[1]; v[2] += a[2]; v[3] += a[3];
+        }
+        fwht128_x4(v);
+        float4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = v[i] * HAD_NORM * f16_bits_to_f32(dsv[col + i]);
+        *reinterpret_cast<float4_t*>(DC + (size_t)pair * P.H + col) = o;
+    }
+    if (lane == 0) *cnt = 0;
+    __threadfence();
+    int* cg = at<int>(P.scratch, L.cntG) + cb;
+    if (wave_atomic_add(cg, 1) != pl.U - 1) return;
+    __threadfence();
+
+    // Last group to finish this H block: fixed-order gather over the top-k slots.
+    for (int row = 0; row < P.m; ++row) {
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < P.topk; ++j) {
+            const int pair = pl.slotpair[row * P.topk + j];
+            if (pair < 0) continue;
+            const float wt = P.w[row * P.topk + j];
+            const float4_t d = __builtin_nontemporal_load(
+                reinterpret_cast<const float4_t*>(DC + (size_t)pair * P.H + col));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt * d[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
+    }
+    if (lane == 0) *cg = 0;
+}
+
+template <uint32_t MASK, int CB>
+__global__ __launch_bounds__(64) void moe_kernel(Params P) {
+    __shared__ uint16_t xa[MAX_M * NSTEP_CAP * STEP_K];     // also route-plan workspace
+    __shared__ Plan pl;
+    static_assert(sizeof(xa) >= 6 * MAX_EXPERTS, "plan workspace");
+    const Layout& L = P.L;
+    Ctrl* ctrl = at<Ctrl>(P.scratch, L.ctrl);
+    const int epoch = __hip_atomic_load(&ctrl->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    build_plan(P, pl, reinterpret_cast<char*>(xa));
+    const int U = pl.U;
+    const int nA = U * 2 * L.nI * L.SA;
+    const int total = nA + U * L.nH * L.SB;
+
+    if (U == 0 && blockIdx.x == 0) {   // nothing routed: the layer output is zero
+        for (int i = threadIdx.x; i < P.m * P.H; i += WAVE) store_out(P.out, i, P.out_kind, 0.f);
+    }
+
+    for (;;) {
+        const int t = wave_atomic_add(&ctrl->ticket, 1);
+        if (t >= total) break;
+        if (t < nA) item_a<MASK, CB>(P, pl, xa, t, epoch);
+        else item_b<MASK, CB>(P, pl, xa, t - nA, epoch);
+        __syncthreads();   // xa is rewritten by the next item
+    }
+
+    // Retire; the last wave out resets the queue and advances the epoch.
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const int r = atomicAdd(&ctrl->retire, 1);
+        if (r == (int)gridDim.x - 1) {
+            __hip_atomic_store(&ctrl->ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ctrl->retire, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ctrl->epoch, epoch + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Launcher for one (bit-width mask, codebook) instantiation; defined in exl3_moe_inst.hip.
+template <uint32_t MASK, int CB>
+int launch_moe(const Params& P, int waves, hipStream_t stream);
+
+template <uint32_t MASK, int CB>
+int moe_waves_per_cu();
+
+}  // namespace moe
+}  // namespace exl3

@@ -1,0 +1,134 @@
+// C-ABI entry points of the routed-MoE decode (declared in include/exl3_amd.h):
+//   exl3_moe_decode         <- lna2_moe_decode   recipe-lna/lna2/lna_moe_ticket.cu:507-581
+//   exl3_moe_scratch_bytes  <- lna2_moe_scratch_bytes  :481
+//   exl3_moe_max_rows       <- lna2_moe_max_rows       :484
+//   exl3_moe_info           <- lna2_moe_info           :494-505
+#include <math.h>
+
+#include "exl3_moe.hpp"
+
+namespace exl3 {
+namespace moe {
+
+// Instantiated (mask, codebook) pairs; the first whose mask covers the
+// requested widths is used.  Keep in sync with MOE_UNITS in build.py.
+#define EXL3_MOE_INSTANCES(X)                 \
+    X(0x004u, 1) X(0x008u, 1) X(0x010u, 1)    \
+    X(0x040u, 1) X(0x00Cu, 1) X(0x01Cu, 1)    \
+    X(0x1FEu, 1) X(0x1FEu, 0) X(0x1FEu, 2)
+
+#define EXL3_DECL(M, C)                                                          \
+    template <> int launch_moe<M, C>(const Params&, int, hipStream_t);          \
+    template <> int moe_waves_per_cu<M, C>();
+EXL3_MOE_INSTANCES(EXL3_DECL)
+#undef EXL3_DECL
+
+struct Instance {
+    uint32_t mask;
+    int cb;
+    int (*launch)(const Params&, int, hipStream_t);
+    int (*waves)();
+};
+
+#define EXL3_ENTRY(M, C) {M, C, &launch_moe<M, C>, &moe_waves_per_cu<M, C>},
+static const Instance kInstances[] = {EXL3_MOE_INSTANCES(EXL3_ENTRY)};
+#undef EXL3_ENTRY
+
+static int cached_waves(int idx) {
+    static int cache[MAX_DEVICES][sizeof(kInstances) / sizeof(kInstances[0])] = {};
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) dev = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!cache[dev][idx]) cache[dev][idx] = kInstances[idx].waves();
+    return cache[dev][idx];
+}
+
+}  // namespace moe
+}  // namespace exl3
+
+using namespace exl3;
+using namespace exl3::moe;
+
+extern "C" {
+
+int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk) {
+    clear_error();
+    if (hidden <= 0 || hidden % COLS || intermediate <= 0 || intermediate % COLS)
+        return fail("hidden and intermediate must be positive multiples of 256");
+    if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..8");
+    return layout((int)hidden, (int)intermediate, (int)topk).total;
+}
+
+int exl3_moe_max_rows(void) { return MAX_M; }
+
+int exl3_moe_info(int64_t* out, int n) {
+    clear_error();
+    if (!out || n < 0) return fail("bad output buffer");
+    const int cus = device_cus();
+    const int64_t v[] = {cus, (int64_t)cus * cached_waves(4), WAVE, MAX_M, MAX_SLOTS, STEP_K, COLS,
+                         (int64_t)sizeof(Ctrl)};
+    const int k = n < 8 ? n : 8;
+    for (int i = 0; i < k; ++i) out[i] = v[i];
+    return k;
+}
+
+int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                    int64_t intermediate, int64_t n_experts, int64_t topk,
+                    const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                    const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                    const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                    const int32_t* expert_ids, const float* routing_weights,
+                    const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                    float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    clear_error();
+    if (!x || !out || !expert_ids || !routing_weights || !scratch) return fail("null pointer");
+    if (!gate_trellis || !gate_suh || !gate_svh || !up_trellis || !up_suh || !up_svh || !down_trellis ||
+        !down_suh || !down_svh)
+        return fail("null pointer table");
+    if (x_kind != 0 && x_kind != 1) return fail("x must be fp16 or bf16");
+    if (out_kind < OUT_F16 || out_kind > OUT_F32) return fail("out must be fp16, bf16 or fp32");
+    if (m < 1 || m > MAX_M) return fail("row count out of range (1 <= m <= exl3_moe_max_rows())");
+    if (hidden <= 0 || hidden % COLS || intermediate <= 0 || intermediate % COLS)
+        return fail("hidden and intermediate must be positive multiples of 256");
+    if (n_experts < 1 || n_experts > MAX_EXPERTS) return fail("expert count out of range (1..2048)");
+    if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..8");
+    if (!(swiglu_limit > 0.0f) || !isfinite(swiglu_limit)) return fail("requires a finite positive SwiGLU limit");
+    if (codebook < CB_3INST || codebook > CB_MUL1) return fail("codebook must be 0, 1 or 2");
+    uint32_t mask;
+    if (expert_bits) {
+        mask = (uint32_t)bits_mask;
+        if (mask == 0 || (mask & ~0x1FEu)) return fail("bits_mask must name widths in 1..8");
+    } else {
+        if (bits < 1 || bits > 8) return fail("bits must be in 1..8");
+        mask = 1u << bits;
+    }
+    const Layout L = layout((int)hidden, (int)intermediate, (int)topk);
+    if (scratch_bytes < L.total) return fail("scratch too small (see exl3_moe_scratch_bytes)");
+
+    int idx = -1;
+    const int ninst = (int)(sizeof(kInstances) / sizeof(kInstances[0]));
+    for (int i = 0; i < ninst; ++i)
+        if (kInstances[i].cb == codebook && (kInstances[i].mask & mask) == mask) { idx = i; break; }
+    if (idx < 0) return fail("no kernel instance for this bit-width set / codebook");
+
+    Params P;
+    P.x = x; P.x_kind = x_kind; P.out = out; P.out_kind = out_kind;
+    P.m = (int)m; P.H = (int)hidden; P.I = (int)intermediate; P.E = (int)n_experts; P.topk = (int)topk;
+    P.gt = gate_trellis; P.gsu = gate_suh; P.gsv = gate_svh;
+    P.ut = up_trellis; P.usu = up_suh; P.usv = up_svh;
+    P.dt = down_trellis; P.dsu = down_suh; P.dsv = down_svh;
+    P.ids = expert_ids; P.w = routing_weights;
+    P.ebits = expert_bits; P.bits = bits;
+    P.limit = swiglu_limit;
+    P.scratch = reinterpret_cast<char*>(scratch);
+    P.L = L;
+
+    const int64_t groups = n_experts < m * topk ? n_experts : m * topk;
+    const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB);
+    const int64_t resident = (int64_t)device_cus() * cached_waves(idx);
+    const int waves = (int)(items < resident ? items : resident);
+    return kInstances[idx].launch(P, waves, reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,33 @@
+// Instantiates the routed-MoE kernel for one (bit-width mask, codebook) pair,
+// set by the build: EXL3_MOE_MASK (bit b set = b-bit experts supported) and
+// EXL3_MOE_CB (0 = 3INST, 1 = MCG, 2 = MUL1).
+#include "exl3_moe.hpp"
+
+#ifndef EXL3_MOE_MASK
+#error "EXL3_MOE_MASK must be defined"
+#endif
+#ifndef EXL3_MOE_CB
+#error "EXL3_MOE_CB must be defined"
+#endif
+
+namespace exl3 {
+namespace moe {
+
+template <>
+int launch_moe<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int waves, hipStream_t stream) {
+    hipLaunchKernelGGL((moe_kernel<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(waves), dim3(WAVE), 0, stream, P);
+    return check_launch();
+}
+
+template <>
+int moe_waves_per_cu<EXL3_MOE_MASK, EXL3_MOE_CB>() {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, reinterpret_cast<const void*>(moe_kernel<EXL3_MOE_MASK, EXL3_MOE_CB>), WAVE, 0) != hipSuccess ||
+        n < 1)
+        n = 1;
+    return n;
+}
+
+}  // namespace moe
+}  // namespace exl3

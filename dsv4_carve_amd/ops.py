@@ -1,0 +1,365 @@
+"""Torch custom ops over the C ABI (include/exl3_amd.h).
+
+Every op is registered in the ``exl3_amd`` torch.library namespace with a CUDA
+(= HIP on ROCm) implementation only, so a CPU tensor fails in the dispatcher and
+a missing ``libexl3_amd.so`` fails at the first call: there is no fallback.
+Launches go to torch's current stream and never allocate, so they are
+capturable with ``torch.cuda.graph`` once the shared scratch exists.
+
+Reference call surfaces mirrored here:
+  * ``dequant_trellis``  -- vllm_exl3_c, recipe-lna/lna2/bindings.cpp:118-133
+  * ``reconstruct``      -- exllamav3_ext, used at recipe-lna/exllamav3/exl3.py.lna:197
+  * ``exl3_gemm``        -- exllamav3_ext, recipe-lna/exllamav3/exl3_gemm.cu.lna:336-364
+  * ``exl3_gemv``        -- vllm_exl3_c, recipe-lna/lna2/bindings.cpp:135-148
+  * ``lna2_moe_decode`` and its helpers -- vllm_exl3_c,
+    recipe-lna/lna2/lna_moe_ticket.cu:481-581, bindings.cpp:212-219
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+
+CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
+OUT_KIND = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+X_KIND = {torch.float16: 0, torch.bfloat16: 1}
+
+
+def codebook_id(mcg: bool, mul1: bool) -> int:
+    """Codebook selection of exl3_gemm_gr (exl3_gemm.cu.lna:186-189)."""
+    if mcg and mul1:
+        raise RuntimeError("Specified both mcg and mul1")
+    return CB_MCG if mcg else (CB_MUL1 if mul1 else CB_3INST)
+
+
+def _stream(device: torch.device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else int(t.data_ptr())
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+# ------------------------------------------------------------------ shared scratch
+
+class _ScratchPool:
+    """One zeroed scratch buffer per (device, purpose), grown outside capture.
+
+    The kernels' counters must be zero before the first launch and are left
+    zero by every launch (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296 is the
+    same contract), so a buffer is zeroed exactly once, when it is created."""
+
+    def __init__(self):
+        self._bufs: dict[tuple[int, str], torch.Tensor] = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        key = (int(idx), purpose)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                if torch.cuda.is_current_stream_capturing():
+                    raise RuntimeError(
+                        f"exl3 {purpose} scratch was not prewarmed for device {idx} "
+                        f"(need {nbytes} bytes during graph capture)")
+                torch.cuda.synchronize(device)     # the old buffer may still be in use
+                buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+    def resident_bytes(self) -> int:
+        return sum(int(b.numel()) for b in self._bufs.values())
+
+
+SCRATCH = _ScratchPool()
+
+# ------------------------------------------------------------------ op registration
+
+_LIB = torch.library.Library("exl3_amd", "DEF")
+_LIB.define("dequant(Tensor trellis, Tensor? suh, Tensor? svh, int bits, int codebook, Tensor(a!) out) -> ()")
+_LIB.define("gemm(Tensor a, Tensor b, Tensor(a!) c, Tensor suh, Tensor svh, int codebook, "
+            "Tensor(b!) scratch) -> ()")
+_LIB.define("moe_decode(Tensor x, Tensor(a!) out, Tensor gate_trellis, Tensor gate_suh, Tensor gate_svh, "
+            "Tensor up_trellis, Tensor up_suh, Tensor up_svh, Tensor down_trellis, Tensor down_suh, "
+            "Tensor down_svh, Tensor expert_ids, Tensor routing_weights, Tensor? expert_bits, int bits, "
+            "int bits_mask, int codebook, float swiglu_limit, int hidden, int intermediate, "
+            "Tensor(b!) scratch) -> ()")
+
+
+def _dequant_impl(trellis, suh, svh, bits, codebook, out):
+    L = _lib.load()
+    k = trellis.shape[0] * 16
+    n = trellis.shape[1] * 16
+    _lib.check(L.exl3_dequant(_ptr(trellis), k, n, int(bits), int(codebook), _ptr(suh), _ptr(svh),
+                              _ptr(out), _stream(trellis.device)))
+
+
+def _gemm_impl(a, b, c, suh, svh, codebook, scratch):
+    L = _lib.load()
+    m, k = a.shape
+    n = b.shape[1] * 16
+    bits = b.shape[2] // 16
+    _lib.check(L.exl3_gemm(_ptr(a), m, k, _ptr(b), n, bits, int(codebook), _ptr(suh), _ptr(svh),
+                           _ptr(c), OUT_KIND[c.dtype], _ptr(scratch), scratch.numel(), _stream(a.device)))
+
+
+def _moe_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, expert_bits, bits, bits_mask,
+              codebook, limit, hidden, intermediate, scratch):
+    L = _lib.load()
+    m = x.shape[0]
+    _lib.check(L.exl3_moe_decode(
+        _ptr(x), X_KIND[x.dtype], _ptr(out), OUT_KIND[out.dtype], m, int(hidden), int(intermediate),
+        gt.numel(), ids.shape[1],
+        _ptr(gt), _ptr(gsu), _ptr(gsv), _ptr(ut), _ptr(usu), _ptr(usv), _ptr(dt), _ptr(dsu), _ptr(dsv),
+        _ptr(ids), _ptr(w), _ptr(expert_bits), int(bits), int(bits_mask), int(codebook), float(limit),
+        _ptr(scratch), scratch.numel(), _stream(x.device)))
+
+
+_LIB.impl("dequant", _dequant_impl, "CUDA")
+_LIB.impl("gemm", _gemm_impl, "CUDA")
+_LIB.impl("moe_decode", _moe_impl, "CUDA")
+
+# ------------------------------------------------------------------ dequant
+
+
+def _check_trellis(trellis: torch.Tensor, bits: int | None = None) -> int:
+    _check(trellis.dim() == 3 and trellis.dtype == torch.int16,
+           "trellis must be int16 [rows/16, cols/16, 16*K]")
+    _check(trellis.is_contiguous(), "trellis must be contiguous")
+    _check(trellis.shape[2] % 16 == 0 and 1 <= trellis.shape[2] // 16 <= 8,
+           "trellis last dimension must be 16*K with 1 <= K <= 8")
+    k = trellis.shape[2] // 16
+    if bits is not None:
+        _check(k == bits, "trellis last dimension must be 16*K")
+    _check(trellis.shape[0] > 0 and trellis.shape[1] > 0, "trellis dimensions must be positive")
+    return k
+
+
+def reconstruct_weight(trellis: torch.Tensor, codebook: int = CB_MCG) -> torch.Tensor:
+    """Raw codebook matrix Wq fp16 [in, out] (no rotations)."""
+    bits = _check_trellis(trellis)
+    out = torch.empty((trellis.shape[0] * 16, trellis.shape[1] * 16), dtype=torch.float16,
+                      device=trellis.device)
+    torch.ops.exl3_amd.dequant(trellis, None, None, bits, codebook, out)
+    return out
+
+
+def reconstruct(w: torch.Tensor, trellis: torch.Tensor, K: int, mcg: bool, mul1: bool) -> None:
+    """exllamav3_ext.reconstruct(w, trellis, K, mcg, mul1): fills w with Wq."""
+    _check_trellis(trellis, K)
+    _check(w.dtype == torch.float16 and w.is_contiguous() and
+           tuple(w.shape) == (trellis.shape[0] * 16, trellis.shape[1] * 16), "w must be fp16 [in, out]")
+    torch.ops.exl3_amd.dequant(trellis, None, None, K, codebook_id(mcg, mul1), w)
+
+
+def dequant_trellis(trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int,
+                    mcg: bool = True, mul1: bool = False) -> torch.Tensor:
+    """vllm_exl3_c.dequant_trellis: W = diag(suh) H Wq H diag(svh)/128, fp16 [in, out]
+    (bindings.cpp:118-133; bit widths 1..8 instead of {2,3,4,8})."""
+    _check_trellis(trellis, K)
+    _check(suh.dtype == torch.float16 and svh.dtype == torch.float16, "suh and svh must be float16")
+    _check(suh.numel() >= trellis.shape[0] * 16 and svh.numel() >= trellis.shape[1] * 16,
+           "suh/svh are too short")
+    _check(trellis.shape[0] % 8 == 0 and trellis.shape[1] % 8 == 0,
+           "trellis dimensions must reconstruct whole 128-element Hadamard blocks")
+    out = torch.empty((trellis.shape[0] * 16, trellis.shape[1] * 16), dtype=torch.float16,
+                      device=trellis.device)
+    torch.ops.exl3_amd.dequant(trellis, suh.contiguous(), svh.contiguous(), K, codebook_id(mcg, mul1), out)
+    return out
+
+# ------------------------------------------------------------------ dense GEMV / GEMM
+
+
+def gemm_scratch(device: torch.device, m: int, k: int, n: int) -> torch.Tensor:
+    nbytes = _lib.check(_lib.load().exl3_gemm_scratch_bytes(m, k, n))
+    return SCRATCH.get(device, "gemm", nbytes)
+
+
+def prepare_gemm(device: torch.device, max_rows: int, k: int, n: int) -> None:
+    """Reserve the shared dense scratch before any graph capture (the role of
+    LNA_EXL3_PREWARM_ROWS, recipe-lna/vllm_exl3_exl3.py.lna:2718-2742)."""
+    for m in range(1, max_rows + 1):
+        gemm_scratch(device, m, k, n)
+
+
+def gemm_into(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+              c: torch.Tensor, codebook: int = CB_MCG) -> torch.Tensor:
+    """c = had_out(had_in(x*suh) @ Wq) * svh for x fp16 [m, k]; c fp16/bf16/fp32 [m, n]."""
+    bits = _check_trellis(trellis)
+    _check(x.dim() == 2 and x.dtype == torch.float16 and x.is_contiguous(), "x must be contiguous fp16 [m, k]")
+    m, k = x.shape
+    n = trellis.shape[1] * 16
+    _check(k == trellis.shape[0] * 16, "x feature dimension does not match trellis")
+    _check(k % 128 == 0 and n % 128 == 0, "in and out features must be multiples of 128")
+    _check(c.dtype in OUT_KIND and c.is_contiguous() and tuple(c.shape) == (m, n), "c must be [m, n] contiguous")
+    _check(suh.dtype == torch.float16 and suh.numel() == k and suh.is_contiguous(), "suh must be fp16 [k]")
+    _check(svh.dtype == torch.float16 and svh.numel() == n and svh.is_contiguous(), "svh must be fp16 [n]")
+    for t in (trellis, suh, svh, c):
+        _check(t.device == x.device, "all tensors must be on the same device")
+    scratch = gemm_scratch(x.device, m, k, n)
+    torch.ops.exl3_amd.gemm(x, trellis, c, suh, svh, codebook, scratch)
+    return c
+
+
+def gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+         codebook: int = CB_MCG, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    c = torch.empty((x.shape[0], trellis.shape[1] * 16), dtype=out_dtype, device=x.device)
+    return gemm_into(x, trellis, suh, svh, c, codebook)
+
+
+def exl3_gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tensor | None,
+              A_had: torch.Tensor | None, svh: torch.Tensor | None, force_shape_idx: int = -1,
+              mcg: bool = False, mul1: bool = False, force_num_sms: int = 0) -> int:
+    """exllamav3_ext.exl3_gemm(A, B, C, suh, A_had, svh, force_shape_idx, mcg, mul1,
+    force_num_sms) -> shape tag (exl3_gemm.cu.lna:336-364).  A is [..., k] fp16,
+    C [..., n] fp16 or fp32.  A_had, force_shape_idx and force_num_sms only steer
+    the reference's tile autotuner and are accepted for drop-in compatibility."""
+    del A_had, force_shape_idx, force_num_sms
+    _check(suh is not None and svh is not None, "suh and svh are required")
+    _check(A.dtype == torch.float16, "A must be float16")
+    _check(C.dtype in (torch.float16, torch.float32), "C must be float16 or float32")
+    a2 = A.reshape(-1, A.shape[-1])
+    c2 = C.view(-1, C.shape[-1])
+    gemm_into(a2, B, suh, svh, c2, codebook_id(mcg, mul1))
+    return 0
+
+
+def exl3_gemv(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
+              K: int, mcg: bool = True, mmode: int = 1) -> torch.Tensor:
+    """vllm_exl3_c.exl3_gemv(x, trellis, suh, svh, K, mcg, mmode), bindings.cpp:135-148:
+    output in x's dtype; m is not limited to 8 here."""
+    _check(x.dim() >= 2, "x must have shape [..., in_features]")
+    _check(mmode in (0, 1), "mmode must be 0 or 1")
+    _check_trellis(trellis, K)
+    _check(x.shape[-1] == trellis.shape[0] * 16, "x feature dimension does not match trellis")
+    x2 = x.contiguous().view(-1, x.shape[-1]).to(torch.float16)
+    out = gemm(x2, trellis, suh, svh, CB_MCG if mcg else CB_MUL1, torch.float32)
+    return out.to(x.dtype).view(*x.shape[:-1], -1)
+
+# ------------------------------------------------------------------ routed MoE decode
+
+MOE_TABLE_KEYS = ("gate_trellis", "gate_suh", "gate_svh", "up_trellis", "up_suh", "up_svh",
+                  "down_trellis", "down_suh", "down_svh")
+
+
+def moe_max_rows() -> int:
+    return int(_lib.load().exl3_moe_max_rows())
+
+
+def moe_scratch_bytes(hidden: int, intermediate: int, topk: int) -> int:
+    return int(_lib.check(_lib.load().exl3_moe_scratch_bytes(hidden, intermediate, topk)))
+
+
+def moe_scratch(device: torch.device, hidden: int, intermediate: int, topk: int) -> torch.Tensor:
+    """The shared per-device MoE scratch (zeroed once, self-resetting afterwards)."""
+    return SCRATCH.get(device, "moe", moe_scratch_bytes(hidden, intermediate, topk))
+
+
+def moe_info() -> list[int]:
+    import ctypes
+
+    buf = (ctypes.c_int64 * 8)()
+    n = _lib.check(_lib.load().exl3_moe_info(buf, 8))
+    return [int(buf[i]) for i in range(n)]
+
+
+def bits_mask_of(bits) -> int:
+    return sum(1 << int(b) for b in set(int(b) for b in bits))
+
+
+def moe_decode(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Tensor,
+               routing_weights: torch.Tensor, *, intermediate: int, bits: int | None = None,
+               expert_bits: torch.Tensor | None = None, bits_mask: int | None = None,
+               codebook: int = CB_MCG, swiglu_limit: float = 10.0,
+               scratch: torch.Tensor | None = None) -> torch.Tensor:
+    """One-launch routed-expert decode of x [m, hidden] into out [m, hidden].
+
+    tables: the nine int64 device pointer tables (dict keyed by MOE_TABLE_KEYS,
+    or a sequence in that order).  Either `bits` (every expert) or
+    `expert_bits` (int8 [E] device tensor) with `bits_mask` (set of widths)."""
+    if isinstance(tables, dict):
+        tabs = [tables[k] for k in MOE_TABLE_KEYS]
+    else:
+        tabs = list(tables)
+    _check(len(tabs) == 9, "nine pointer tables are required")
+    _check(x.is_cuda and x.dtype in X_KIND, "input must be HIP fp16 or bf16")
+    _check(x.dim() == 2 and x.is_contiguous(), "input must be contiguous [m, hidden]")
+    m, hidden = x.shape
+    _check(1 <= m <= moe_max_rows(), "row count out of range (1 <= m <= moe_max_rows())")
+    _check(out.is_cuda and out.device == x.device and tuple(out.shape) == tuple(x.shape) and out.is_contiguous(),
+           "output must match x shape/device and be contiguous")
+    _check(out.dtype in OUT_KIND, "output must be fp16/bf16/fp32")
+    _check(expert_ids.is_cuda and expert_ids.dtype == torch.int32 and expert_ids.is_contiguous() and
+           expert_ids.dim() == 2 and expert_ids.shape[0] == m, "expert_ids must be contiguous int32 [m, topk]")
+    _check(routing_weights.is_cuda and routing_weights.dtype == torch.float32 and
+           routing_weights.is_contiguous() and routing_weights.shape == expert_ids.shape,
+           "routing_weights must be contiguous fp32 [m, topk]")
+    n_experts = tabs[0].numel()
+    for t in tabs:
+        _check(t.is_cuda and t.device == x.device and t.dtype == torch.int64 and t.is_contiguous() and
+               t.numel() == n_experts, "pointer tables must be contiguous int64 [experts] on the input device")
+    if expert_bits is not None:
+        _check(expert_bits.is_cuda and expert_bits.dtype == torch.int8 and expert_bits.numel() == n_experts,
+               "expert_bits must be int8 [experts] on the device")
+        _check(bits_mask is not None and bits_mask > 0, "bits_mask is required with expert_bits")
+        b, mask = 0, int(bits_mask)
+    else:
+        _check(bits is not None and 1 <= int(bits) <= 8, "bits must be in 1..8")
+        b, mask = int(bits), 0
+    if scratch is None:
+        scratch = moe_scratch(x.device, hidden, intermediate, expert_ids.shape[1])
+    torch.ops.exl3_amd.moe_decode(x, out, *tabs, expert_ids, routing_weights, expert_bits, b, mask,
+                                  int(codebook), float(swiglu_limit), int(hidden), int(intermediate), scratch)
+    return out
+
+
+# vllm_exl3_c names (recipe-lna/lna2/bindings.cpp:212-219, lna_moe_ticket.cu:481-581).
+# The reference kernel is fixed at hidden=4096, intermediate=256, top-6 and one
+# width per launch; here intermediate is a keyword (default: that geometry),
+# top-k comes from the ids' shape and `bits` may be a per-expert int8 table.
+
+def lna2_moe_decode(x, out, gate_trellis, gate_suh, gate_svh, up_trellis, up_suh, up_svh,
+                    down_trellis, down_suh, down_svh, expert_ids, routing_weights, bits,
+                    swiglu_limit, scratch, *, intermediate: int = 256, bits_mask: int | None = None,
+                    codebook: int = CB_MCG):
+    tabs = (gate_trellis, gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh)
+    limit = float(swiglu_limit)
+    _check(limit > 0.0 and limit == limit and limit != float("inf"), "requires a finite positive SwiGLU limit")
+    _check(scratch.is_cuda and scratch.dtype == torch.uint8 and scratch.is_contiguous() and
+           scratch.numel() >= moe_scratch_bytes(x.shape[1], intermediate, expert_ids.shape[1]),
+           "scratch too small")
+    if isinstance(bits, torch.Tensor):
+        mask = bits_mask if bits_mask is not None else bits_mask_of(bits.cpu().tolist())
+        return moe_decode(x, out, tabs, expert_ids, routing_weights, intermediate=intermediate,
+                          expert_bits=bits, bits_mask=mask, codebook=codebook, swiglu_limit=limit,
+                          scratch=scratch)
+    return moe_decode(x, out, tabs, expert_ids, routing_weights, intermediate=intermediate, bits=int(bits),
+                      codebook=codebook, swiglu_limit=limit, scratch=scratch)
+
+
+def lna2_moe_scratch_bytes(hidden: int = 4096, intermediate: int = 256, topk: int = 6) -> int:
+    return moe_scratch_bytes(hidden, intermediate, topk)
+
+
+def lna2_moe_max_rows() -> int:
+    return moe_max_rows()
+
+
+def lna2_moe_prepare(bits: int) -> None:
+    _check(1 <= int(bits) <= 8, "bits must be in 1..8")
+    moe_info()
+
+
+def lna2_moe_info(bits: int) -> list[int]:
+    """[cus, waves per launch, threads per wave, max rows, max pairs, step k, cols, ctrl bytes]."""
+    lna2_moe_prepare(bits)
+    return moe_info()

@@ -1,0 +1,103 @@
+/*
+ * exl3_amd.h -- C ABI of libexl3_amd.so, the MI355X (gfx950) EXL3 decode path.
+ *
+ * Plain pointers, sizes and an opaque stream (a hipStream_t passed as void*;
+ * NULL = the default stream).  Every device pointer is HBM memory on the
+ * current HIP device.  Functions return 0 (or a non-negative size) on success
+ * and a negative value on an argument or launch error; exl3_last_error()
+ * returns the message of the last failure on the calling thread.  No call
+ * allocates device memory, synchronises the stream or queries the clock, so
+ * every launch can be captured into a HIP graph.
+ *
+ * Element kinds: x_kind 0 = fp16, 1 = bf16; out_kind 0 = fp16, 1 = bf16, 2 = fp32.
+ * Codebooks: 0 = 3INST, 1 = MCG (production), 2 = MUL1.
+ * Weight ABI per projection (recipe-lna/vllm_exl3_exl3.py.lna:50-54, 2083-2122):
+ *   trellis int16 [in/16][out/16][16*bits], suh fp16 [in], svh fp16 [out].
+ */
+#ifndef EXL3_AMD_H
+#define EXL3_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* exl3_last_error(void);
+
+/*
+ * Trellis -> fp16 weight matrix [k][n] (row-major).
+ * suh == svh == NULL: the raw codebook matrix Wq (exllamav3 `reconstruct`,
+ *   called at recipe-lna/exllamav3/exl3.py.lna:197); k, n multiples of 16.
+ * suh, svh given: W = diag(suh) H Wq H diag(svh) / 128 with 128-blocks
+ *   (replaces vllm_exl3_c.dequant_trellis, recipe-lna/lna2/bindings.cpp:118-133,
+ *   computed on the GPU instead of bindings.cpp:16-101); k, n multiples of 128.
+ * Bit-exact with the round-to-nearest-even decode canon.
+ */
+int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int codebook,
+                 const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream);
+
+/*
+ * c[m][n] = had_out(had_in(a . suh) . Wq) . svh, fp32 accumulation.
+ * Replaces exllamav3 `exl3_gemm` (recipe-lna/exllamav3/exl3_gemm.cu.lna:336-364,
+ * limits k % 16, n % 128 at :35-37) as used by LinearEXL3.forward for rows <= 144
+ * (recipe-lna/exllamav3/exl3.py.lna:114-139), and vllm_exl3_c.exl3_gemv
+ * (recipe-lna/lna2/bindings.cpp:135-148).  a: fp16 [m][k]; k % 128 == 0,
+ * n % 128 == 0; any m (processed in blocks of 16 rows).  scratch: device
+ * buffer of at least exl3_gemm_scratch_bytes(m, k, n) bytes, zeroed once
+ * before its first use; the kernels leave its counters zero again, so one
+ * buffer serves every later call on the same stream (one call at a time).
+ */
+int64_t exl3_gemm_scratch_bytes(int64_t m, int64_t k, int64_t n);
+int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t n, int bits,
+              int codebook, const uint16_t* suh, const uint16_t* svh, void* c, int c_kind,
+              void* scratch, int64_t scratch_bytes, void* stream);
+
+/*
+ * Routed-MoE decode layer, one launch: for every row r and top-k slot j with a
+ * valid expert e = expert_ids[r][j] (0 <= e < n_experts; others are skipped):
+ *   g = had_out(had_in(x[r] . gate_suh[e]) . Wgate[e]) . gate_svh[e]   (fp32)
+ *   u = same with up;  act = half(silu(min(g, L)) * clamp(u, -L, L))
+ *   d = had_out(had_in(act . down_suh[e]) . Wdown[e]) . down_svh[e]    (fp32)
+ *   out[r] = sum_j routing_weights[r][j] * d   (fp32, slot order), one cast.
+ * Replaces vllm_exl3_c.lna2_moe_decode (recipe-lna/lna2/lna_moe_ticket.cu:507-581)
+ * and generalises its fixed geometry (H=4096, I=256, top-6, one K per launch,
+ * :34-36, 532) to any hidden % 256 == 0, intermediate % 256 == 0, topk <= 8 and
+ * a per-expert bit width.
+ *   x: [m][hidden] (x_kind), out: [m][hidden] (out_kind), 1 <= m <= exl3_moe_max_rows().
+ *   Pointer tables: device int64 [n_experts] of data pointers (as built by
+ *     build_exl3_fused_state, recipe-lna/vllm_exl3_exl3.py.lna:1543-1569).
+ *   expert_ids int32 [m][topk], routing_weights fp32 [m][topk] (already scaled).
+ *   expert_bits: device int8 [n_experts] bit widths, or NULL when every expert
+ *     uses `bits`.  bits_mask: bit b set for every width b present (ignored
+ *     when expert_bits is NULL).
+ *   swiglu_limit: finite and > 0 (lna_moe_ticket.cu:552-553).
+ *   scratch: >= exl3_moe_scratch_bytes(hidden, intermediate, topk) bytes, zeroed
+ *     once before first use; self-resetting afterwards.  One launch at a time
+ *     per scratch buffer.
+ */
+int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk);
+int exl3_moe_max_rows(void);
+int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                    int64_t intermediate, int64_t n_experts, int64_t topk,
+                    const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                    const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                    const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                    const int32_t* expert_ids, const float* routing_weights,
+                    const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                    float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
+
+/*
+ * Launch geometry for diagnostics (replaces lna2_moe_info,
+ * recipe-lna/lna2/lna_moe_ticket.cu:494-505): writes up to n values
+ * {cus, waves_per_launch, threads_per_wave, max_rows, max_pairs, step_k, cols,
+ *  ctrl_bytes} and returns how many were written.
+ */
+int exl3_moe_info(int64_t* out, int n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EXL3_AMD_H */

@@ -1,0 +1,155 @@
+"""GPU parity of the dense path through the C ABI: dequant bit-exact against the
+oracle, GEMV/GEMM within the fp tolerance, bitwise repeatable."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from dsv4_carve_amd import synth
+from oracle import oracle as O
+from tests.helpers import assert_close, to_dev
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ops(dev):
+    from dsv4_carve_amd import ops as _ops
+    return _ops
+
+
+@pytest.mark.parametrize("bits", list(range(1, 9)))
+@pytest.mark.parametrize("cb", [O.CB_MCG, O.CB_3INST, O.CB_MUL1])
+def test_reconstruct_bit_exact(ops, dev, bits, cb):
+    print(f"reconstruct bits={bits} cb={cb}", flush=True)
+    rng = np.random.default_rng(1000 + 10 * bits + cb)
+    tr = rng.integers(0, 1 << 16, (16, 24, 16 * bits), dtype=np.uint16).view(np.int16)
+    got = ops.reconstruct_weight(to_dev(tr, dev), cb).cpu().numpy().view(np.uint16)
+    ref = O.reconstruct_fast(tr, bits, cb).view(np.uint16)
+    bad = np.argwhere(got != ref)
+    assert bad.size == 0, f"{len(bad)} mismatches, first at {bad[:4].tolist()}"
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
+def test_reconstruct_primitive_streams(ops, dev, bits):
+    """The four primitive-gate streams (primitive_gate.cu:107-121) as tiles."""
+    from tests.test_oracle import primitive_streams
+
+    tiles = primitive_streams(bits).view(np.int16).reshape(1, 4, 16 * bits)
+    got = ops.reconstruct_weight(to_dev(tiles, dev)).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, O.reconstruct_c(tiles, bits).view(np.uint16))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
+def test_dequant_trellis_bit_exact(ops, dev, bits):
+    print(f"dequant_trellis bits={bits}", flush=True)
+    L = synth.dense(256, 384, bits, seed=bits)
+    got = ops.dequant_trellis(to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev), bits)
+    ref = O.dequant_full_c(L["trellis"], L["suh"], L["svh"], bits)
+    g = got.cpu().numpy()
+    bad = np.argwhere(g.view(np.uint16) != ref.view(np.uint16))
+    if bad.size:
+        d = np.abs(g.view(np.int16).astype(np.int32) - ref.view(np.int16).astype(np.int32))
+        k, n = bad[0]
+        raise AssertionError(f"{len(bad)} of {g.size} differ, max {d.max()} ulp; first ({k},{n}) "
+                             f"got {g[k, n]!r} ref {ref[k, n]!r}; rows {sorted(set(bad[:, 0] % 128))[:8]} "
+                             f"cols {sorted(set(bad[:, 1] % 128))[:8]}")
+
+
+def _gemm_case(ops, dev, k, n, bits, rows, out_dtype, seed=0, cb=O.CB_MCG):
+    import torch
+
+    print(f"gemm k={k} n={n} bits={bits} rows={rows} out={out_dtype} cb={cb}", flush=True)
+    L = synth.dense(k, n, bits, seed=seed + bits)
+    x = synth.activations(rows, k, seed=seed + rows)
+    tr, su, sv = to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev)
+    xd = to_dev(x, dev)
+    y = ops.gemm(xd, tr, su, sv, cb, out_dtype)
+    y2 = ops.gemm(xd, tr, su, sv, cb, out_dtype)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y2), "not bitwise repeatable"
+    ref = O.linear(x, L["trellis"], L["suh"], L["svh"], bits, cb)
+    return y.float().cpu().numpy(), ref
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 6])
+@pytest.mark.parametrize("rows", [1, 2, 4, 8, 16])
+def test_gemm_small(ops, dev, bits, rows):
+    import torch
+
+    got, ref = _gemm_case(ops, dev, 512, 768, bits, rows, torch.float32)
+    assert_close(got, ref, what=f"K{bits} rows={rows}")
+
+
+@pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 1536), (1536, 4096), (4096, 12288)])
+def test_gemm_baseline_shapes(ops, dev, k, n):
+    import torch
+
+    for bits, rows in ((6, 1), (2, 16), (3, 4), (4, 8)):
+        got, ref = _gemm_case(ops, dev, k, n, bits, rows, torch.float32, seed=k + n)
+        assert_close(got, ref, what=f"{k}x{n} K{bits} rows={rows}")
+
+
+def test_gemm_c0_config(ops, dev):
+    """K=N=4096, 6 bits, 1 row: the CPU-reference configuration."""
+    import torch
+
+    got, ref = _gemm_case(ops, dev, 4096, 4096, 6, 1, torch.float32, seed=2026)
+    assert_close(got, ref, what="C0")
+
+
+@pytest.mark.parametrize("rows", [17, 40])
+def test_gemm_many_rows(ops, dev, rows):
+    import torch
+
+    got, ref = _gemm_case(ops, dev, 256, 512, 3, rows, torch.float32)
+    assert_close(got, ref, what=f"rows={rows}")
+
+
+@pytest.mark.parametrize("out_dtype", ["float16", "bfloat16"])
+def test_gemm_out_dtypes(ops, dev, out_dtype):
+    import torch
+
+    dt = getattr(torch, out_dtype)
+    got, ref = _gemm_case(ops, dev, 512, 256, 4, 3, dt)
+    tol = 4e-3 if out_dtype == "bfloat16" else 1e-3
+    assert_close(got, ref, rel=tol, what=out_dtype)
+
+
+@pytest.mark.parametrize("cb", [O.CB_3INST, O.CB_MUL1])
+def test_gemm_other_codebooks(ops, dev, cb):
+    import torch
+
+    got, ref = _gemm_case(ops, dev, 512, 512, 3, 2, torch.float32, cb=cb)
+    assert_close(got, ref, what=f"cb={cb}")
+
+
+def test_reference_call_surfaces(ops, dev):
+    """exllamav3-style exl3_gemm and vllm_exl3_c-style exl3_gemv entry points."""
+    import torch
+
+    L = synth.dense(256, 256, 3, seed=77)
+    x = synth.activations(5, 256, seed=77)
+    tr, su, sv = to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev)
+    ref = O.linear(x, L["trellis"], L["suh"], L["svh"], 3)
+    C = torch.empty((5, 256), dtype=torch.float32, device=dev)
+    assert ops.exl3_gemm(to_dev(x, dev), tr, C, su, None, sv, -1, True, False, 0) == 0
+    assert_close(C.cpu().numpy(), ref)
+    y = ops.exl3_gemv(to_dev(x, dev), tr, su, sv, 3, True)
+    assert y.dtype == torch.float16
+    assert_close(y.float().cpu().numpy(), ref, rel=2e-3)
+
+
+def test_argument_errors(ops, dev):
+    import torch
+
+    L = synth.dense(256, 256, 3, seed=1)
+    tr, su, sv = to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev)
+    with pytest.raises(RuntimeError):
+        ops.gemm(torch.zeros((1, 128), dtype=torch.float16, device=dev), tr, su, sv)
+    with pytest.raises(RuntimeError):
+        ops.gemm(torch.zeros((1, 256), dtype=torch.float32, device=dev), tr, su, sv)
+    with pytest.raises(RuntimeError):
+        ops.exl3_gemm(torch.zeros((1, 256), dtype=torch.float16, device=dev), tr,
+                      torch.empty((1, 256), device=dev), su, None, sv, -1, True, True, 0)

@@ -1,0 +1,267 @@
+"""GPU parity of the routed-MoE decode through the C ABI.
+
+Cases follow the reference's desk-parity gate (recipe-lna/lna2/parity_native.py):
+route profiles unique/hot/zipf/boundary/within-row-dup/R_e16/cancel (:184-206),
+weights normal/zero/cancel (:209-216), inputs zero/real/amplified/clamp/large
+(:219-233), every row count, bitwise repeat (:296-298), a transposed-ids ABI
+check (:347-366) and a scratch-reuse replay (:369-393).  Tolerance is the fp
+bar (max-abs 2e-2, rel-L2 1e-3) against the oracle."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from dsv4_carve_amd import synth
+from oracle import oracle as O
+from tests.helpers import assert_close, rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+
+LIMIT = 10.0
+
+
+class Layer:
+    """Device copy of synthetic experts plus their pointer tables."""
+
+    def __init__(self, dev, E, H, I, bits_list, seed, scale_svh=1.0):
+        import torch
+        from dsv4_carve_amd.ops import MOE_TABLE_KEYS
+
+        self.E, self.H, self.I = E, H, I
+        self.bits = list(bits_list)
+        self.experts = [synth.expert(e, H, I, self.bits[e], seed) for e in range(E)]
+        if scale_svh != 1.0:
+            for ex in self.experts:
+                for p in ("gate", "up", "down"):
+                    ex[p]["svh"] = (ex[p]["svh"].astype(np.float32) * scale_svh).astype(np.float16)
+        self.keep = []
+        cols = {k: [] for k in MOE_TABLE_KEYS}
+        for ex in self.experts:
+            for p in ("gate", "up", "down"):
+                for part in ("trellis", "suh", "svh"):
+                    t = to_dev(ex[p][part], dev)
+                    self.keep.append(t)
+                    cols[f"{p}_{part}"].append(int(t.data_ptr()))
+        self.tables = {k: torch.tensor(v, dtype=torch.int64, device=dev) for k, v in cols.items()}
+        self.ebits = torch.tensor(self.bits, dtype=torch.int8, device=dev)
+        self.mask = sum(1 << b for b in set(self.bits))
+        self.cache = {}
+
+    def run(self, x, ids, w, out_dtype=None, limit=LIMIT):
+        import torch
+        from dsv4_carve_amd import ops
+
+        dev = self.ebits.device
+        xd = x if isinstance(x, torch.Tensor) else to_dev(x, dev)
+        out = torch.empty(xd.shape, dtype=out_dtype or torch.float32, device=dev)
+        ops.moe_decode(xd, out, self.tables, to_dev(ids.astype(np.int32), dev), to_dev(w.astype(np.float32), dev),
+                       intermediate=self.I, expert_bits=self.ebits, bits_mask=self.mask, swiglu_limit=limit)
+        return out
+
+    def ref(self, x16, ids, w, limit=LIMIT):
+        return O.moe(x16, ids, w, self.experts, limit, cache=self.cache)
+
+
+@pytest.fixture(scope="module")
+def small(dev):
+    # 16 experts, mixed 2/3/4-bit, hidden 512, intermediate 256, top-6
+    bits = [3, 2, 4, 3, 2, 2, 3, 4, 2, 3, 3, 2, 4, 2, 3, 2]
+    return Layer(dev, 16, 512, 256, bits, seed=17)
+
+
+def route_ids(m, profile, E=16, topk=6):
+    if profile == "unique":
+        return (np.arange(m * topk) % E).reshape(m, topk).astype(np.int32)
+    if profile == "hot":
+        return np.zeros((m, topk), np.int32)
+    if profile in ("zipf", "cancel"):
+        return np.tile(np.array([0, 0, 1, 1, 2, 3]), (m, 1)).astype(np.int32)
+    if profile == "boundary":
+        return np.tile(np.array([0, E - 1, 0, E - 1, 1, E - 2]), (m, 1)).astype(np.int32)
+    if profile == "within-row-dup":
+        return np.stack([[(r + j) % E for j in (0, 0, 1, 2, 3, 4)] for r in range(m)]).astype(np.int32)
+    if profile == "R_e16":
+        return np.stack([np.full(topk, r % 16) for r in range(m)]).astype(np.int32)
+    if profile == "invalid":
+        return np.tile(np.array([-1, 3, E, 5, 10 ** 6, -7]), (m, 1)).astype(np.int32)
+    if profile == "random":
+        return synth.routing(m, E, topk, seed=m)[0]
+    raise ValueError(profile)
+
+
+def route_weights(m, profile, topk=6):
+    if profile == "zero":
+        return np.zeros((m, topk), np.float32)
+    if profile == "cancel":
+        return np.tile(np.array([1.0, -1.0, 0.25, -0.25, 0.125, -0.125], np.float32), (m, 1))
+    return np.tile(np.array([0.5, 0.25, 0.125, 0.0625, 0.03125, 0.015625], np.float32), (m, 1))
+
+
+def inputs(m, name, H=512):
+    if name == "zero":
+        return np.zeros((m, H), np.float16)
+    if name == "real":
+        return synth.activations(m, H, seed=9100 + m)
+    if name == "amplified":
+        return (synth.activations(m, H, seed=9200 + m).astype(np.float32) * 8).astype(np.float16)
+    if name.startswith("clamp-"):
+        return np.full((m, H), float(name.split("-", 1)[1]), np.float16)
+    raise ValueError(name)
+
+
+def check(layer, x16, ids, w, what, **kw):
+    got = layer.run(x16, ids, w, **kw).cpu().numpy()
+    ref = layer.ref(x16, ids, w)
+    scale = max(1.0, float(np.abs(ref).max()))
+    assert_close(got / scale, ref / scale, what=what)
+    return got, ref
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 15, 16])
+def test_rows_random_routes(small, m):
+    print(f"moe m={m}", flush=True)
+    ids, w = synth.routing(m, 16, 6, seed=100 + m)
+    check(small, inputs(m, "real"), ids, w, f"m={m}")
+
+
+@pytest.mark.parametrize("profile", ["unique", "hot", "zipf", "boundary", "within-row-dup", "R_e16", "invalid"])
+def test_route_profiles(small, profile):
+    print(f"moe profile={profile}", flush=True)
+    for m in (1, 4, 16):
+        ids = route_ids(m, profile)
+        check(small, inputs(m, "real"), ids, route_weights(m, "normal"), f"{profile} m={m}")
+
+
+def test_cancel_and_zero_weights(small):
+    """Fully cancelling slots (each expert twice with +w and -w) leave a
+    degenerate row, judged on absolute error as in parity_native.py:54-58;
+    the partly cancelling profile of :184-216 is judged on the fp tolerance."""
+    m = 8
+    ids = np.tile(np.array([0, 0, 1, 1, 2, 2], np.int32), (m, 1))
+    w = np.tile(np.array([1.0, -1.0, 0.25, -0.25, 0.125, -0.125], np.float32), (m, 1))
+    got = small.run(inputs(m, "real"), ids, w).cpu().numpy()
+    assert np.abs(got).max() <= 1e-4
+    check(small, inputs(m, "real"), route_ids(m, "cancel"), route_weights(m, "cancel"), "cancel")
+    got0 = small.run(inputs(m, "real"), route_ids(m, "cancel"), route_weights(m, "zero")).cpu().numpy()
+    assert np.all(got0 == 0.0)
+
+
+@pytest.mark.parametrize("name", ["zero", "amplified", "clamp-9.99", "clamp-10.0", "clamp-10.01"])
+def test_inputs(small, name):
+    m = 4
+    ids, w = synth.routing(m, 16, 6, seed=7)
+    x = inputs(m, name)
+    got = small.run(x, ids, w).cpu().numpy()
+    ref = small.ref(x, ids, w)
+    if name == "zero":
+        assert np.all(got == 0.0)
+    else:
+        scale = max(1.0, float(np.abs(ref).max()))
+        assert_close(got / scale, ref / scale, what=name)
+
+
+@pytest.mark.parametrize("out_dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("x_dtype", ["float16", "bfloat16"])
+def test_dtypes(small, dev, out_dtype, x_dtype):
+    import torch
+
+    m = 5
+    ids, w = synth.routing(m, 16, 6, seed=31)
+    x32 = synth.activations(m, 512, seed=31, dtype=np.float32)
+    xt = torch.from_numpy(x32).to(dev).to(getattr(torch, x_dtype))
+    got = small.run(xt, ids, w, out_dtype=getattr(torch, out_dtype)).float().cpu().numpy()
+    x16 = xt.float().cpu().numpy().astype(np.float16)        # the kernel's bf16 -> fp16 rounding
+    ref = small.ref(x16, ids, w)
+    tol = 6e-3 if "bfloat16" in (out_dtype,) else 2e-3
+    assert rel_l2(got, ref) <= tol
+
+
+def test_bitwise_repeat_and_scratch_reuse(small):
+    """Alternating row counts reuse the self-resetting scratch (parity_native.py:369-393)."""
+    import torch
+
+    outs = {}
+    for rep in range(3):
+        for m in (16, 1, 7, 3):
+            ids, w = synth.routing(m, 16, 6, seed=500 + m)
+            o = small.run(inputs(m, "real"), ids, w)
+            torch.cuda.synchronize()
+            if m in outs:
+                assert torch.equal(o, outs[m]), f"m={m} not bitwise repeatable"
+            outs[m] = o
+    ids, w = synth.routing(16, 16, 6, seed=516)
+    ref = small.ref(inputs(16, "real"), ids, w)
+    assert rel_l2(outs[16].cpu().numpy(), ref) < 1e-3
+
+
+def test_transposed_ids_changes_output(small):
+    """The historical flat/transposed-id bug (docs/PLAN.md:107): [m, k] must be read row-major."""
+    m = 6
+    ids, w = synth.routing(m, 16, 6, seed=3)
+    a = small.run(inputs(m, "real"), ids, w).cpu().numpy()
+    idt = np.ascontiguousarray(ids.T.reshape(m, 6))
+    b = small.run(inputs(m, "real"), idt, w).cpu().numpy()
+    assert not np.allclose(a, b)
+
+
+def test_argument_errors(small, dev):
+    import torch
+    from dsv4_carve_amd import ops
+
+    x = torch.zeros((2, 512), dtype=torch.float16, device=dev)
+    out = torch.empty((2, 512), dtype=torch.float32, device=dev)
+    ids = torch.zeros((2, 6), dtype=torch.int32, device=dev)
+    w = torch.zeros((2, 6), dtype=torch.float32, device=dev)
+    kw = dict(intermediate=256, expert_bits=small.ebits, bits_mask=small.mask)
+    with pytest.raises(RuntimeError):      # too many rows
+        ops.moe_decode(torch.zeros((17, 512), dtype=torch.float16, device=dev),
+                       torch.empty((17, 512), device=dev), small.tables,
+                       torch.zeros((17, 6), dtype=torch.int32, device=dev),
+                       torch.zeros((17, 6), device=dev), **kw)
+    with pytest.raises(RuntimeError):      # int64 ids
+        ops.moe_decode(x, out, small.tables, ids.long(), w, **kw)
+    with pytest.raises(RuntimeError):      # non-finite limit
+        ops.moe_decode(x, out, small.tables, ids, w, swiglu_limit=float("inf"), **kw)
+    with pytest.raises(RuntimeError):      # a 0-bit width is not a width
+        ops.moe_decode(x, out, small.tables, ids, w, intermediate=256, expert_bits=small.ebits,
+                       bits_mask=(1 << 0) | (1 << 3))
+
+
+# ---------------------------------------------------------------- full MoE layer shape
+
+@pytest.fixture(scope="module")
+def c2(dev):
+    """256 experts, top-8, hidden 4096, intermediate 2048, 3-bit for the first
+    128 experts and 2-bit for the rest."""
+    return Layer(dev, 256, 4096, 2048, synth.mixed_bits(256), seed=2)
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_c2_against_oracle(c2, m):
+    print(f"c2 m={m}", flush=True)
+    ids, w = synth.routing(m, 256, 8, seed=1000 + m)
+    x = synth.activations(m, 4096, seed=1000 + m)
+    got = c2.run(x, ids, w).cpu().numpy()
+    ref = c2.ref(x, ids, w)
+    assert_close(got, ref, what=f"C2 m={m}")
+
+
+def test_c2_size_independent_properties(c2, dev):
+    """At m=16: bitwise repeat; row-permutation equivariance; every row equals
+    the same row computed alone (rows never interact)."""
+    import torch
+
+    m = 16
+    ids, w = synth.routing(m, 256, 8, seed=77)
+    x = synth.activations(m, 4096, seed=77)
+    a = c2.run(x, ids, w)
+    b = c2.run(x, ids, w)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    perm = np.random.default_rng(5).permutation(m)
+    p = c2.run(x[perm], ids[perm], w[perm])
+    assert torch.equal(p, a[torch.as_tensor(perm, device=dev)])
+    for r in (0, 9, 15):
+        single = c2.run(x[r:r + 1], ids[r:r + 1], w[r:r + 1])
+        assert torch.equal(single[0], a[r]), f"row {r} differs when computed alone"
