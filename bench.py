@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Routed-MoE decode layer benchmark (one MI355X).
+
+Workload: 256 experts, top-8 routing, hidden 4096, expert intermediate 2048
+(gate+up 4096 -> 2x2048, clamped SiLU*mul, down 2048 -> 4096); experts 0-127 at
+3 bits, 128-255 at 2 bits (EXL3 MCG trellis); seeded synthetic weights, N(0,1)
+router logits, fp16 activations.  One step = one layer decode over a batch of
+`--rows` rows (default 16).  Every step of a run uses a different routing from a
+seeded pool, so consecutive steps read different experts (no reuse through the
+256 MB MALL), and the steps are replayed from a HIP graph.
+
+Prints ONE JSON line; `value` is microseconds per layer at --rows (lower is
+better), `roofline` the achieved HBM bandwidth on the algorithmic bytes of the
+experts actually read, `cpu_baseline` the CPU restatement of the reference's
+CPU path timed on a bounded sample on this host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HIDDEN, INTER, EXPERTS, TOPK = 4096, 2048, 256, 8
+HBM_PEAK_GBS = 8000.0
+POOL = 64
+
+
+def expert_bytes(hidden: int, inter: int, bits: int) -> int:
+    """Algorithmic bytes of one expert: packed trellis + suh + svh of gate, up, down."""
+    per = 3 * hidden * inter * bits // 8
+    return per + 2 * 2 * (hidden + inter) + 2 * (inter + hidden)
+
+
+def step_bytes(ids: np.ndarray, bits: list[int], hidden: int, inter: int, x_bytes=2, out_bytes=4) -> int:
+    m = ids.shape[0]
+    active = sorted({int(e) for e in ids.reshape(-1) if 0 <= e < len(bits)})
+    return sum(expert_bytes(hidden, inter, bits[e]) for e in active) + m * hidden * (x_bytes + out_bytes)
+
+
+class DeviceLayer:
+    def __init__(self, dev, n_experts, hidden, inter, bits, seed):
+        import torch
+        from dsv4_carve_amd import synth
+        from dsv4_carve_amd.ops import MOE_TABLE_KEYS
+
+        self.hidden, self.inter, self.bits = hidden, inter, list(bits)
+        self.keep = []
+        cols = {k: [] for k in MOE_TABLE_KEYS}
+        for e in range(n_experts):
+            ex = synth.expert(e, hidden, inter, self.bits[e], seed)
+            for p in ("gate", "up", "down"):
+                for part in ("trellis", "suh", "svh"):
+                    t = torch.from_numpy(ex[p][part]).to(dev)
+                    self.keep.append(t)
+                    cols[f"{p}_{part}"].append(int(t.data_ptr()))
+        self.tables = {k: torch.tensor(v, dtype=torch.int64, device=dev) for k, v in cols.items()}
+        self.ebits = torch.tensor(self.bits, dtype=torch.int8, device=dev)
+        self.mask = sum(1 << b for b in set(self.bits))
+
+
+def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False):
+    """Returns (us per step, mean algorithmic bytes per step)."""
+    import torch
+    from dsv4_carve_amd import ops, synth
+
+    n_exp = len(layer.bits)
+    pool = [synth.routing(rows, n_exp, topk, seed=seed * 1000 + (0 if same_routing else i)) for i in range(POOL)]
+    ids = torch.tensor(np.stack([p[0] for p in pool]), dtype=torch.int32, device=dev)
+    wts = torch.tensor(np.stack([p[1] for p in pool]), dtype=torch.float32, device=dev)
+    x = torch.from_numpy(synth.activations(rows, layer.hidden, seed=seed)).to(dev)
+    out = torch.empty((rows, layer.hidden), dtype=torch.float32, device=dev)
+    scratch = ops.moe_scratch(dev, layer.hidden, layer.inter, topk)
+
+    def launch(i):
+        ops.moe_decode(x, out, layer.tables, ids[i % POOL], wts[i % POOL], intermediate=layer.inter,
+                       expert_bits=layer.ebits, bits_mask=layer.mask, scratch=scratch)
+
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            launch(i)
+    torch.cuda.synchronize()
+    graph.replay()                       # one untimed replay (graph upload)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1000.0 / steps
+    nbytes = float(np.mean([step_bytes(pool[i % POOL][0], layer.bits, layer.hidden, layer.inter)
+                            for i in range(steps)]))
+    return us, nbytes
+
+
+def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> dict:
+    """CPU restatement timed on one 3-bit and one 2-bit expert, scaled to the
+    mean set of distinct experts per step at this row count."""
+    import torch
+    from dsv4_carve_amd import synth
+    from oracle import cpu_baseline as CB
+
+    t3 = CB.time_expert(synth.expert(0, HIDDEN, INTER, 3, seed), rows)
+    t2 = CB.time_expert(synth.expert(200, HIDDEN, INTER, 2, seed), rows)
+    n3 = n2 = 0.0
+    for ids in us_ids:
+        act = {int(e) for e in ids.reshape(-1)}
+        n3 += sum(1 for e in act if bits[e] == 3)
+        n2 += sum(1 for e in act if bits[e] == 2)
+    n3 /= len(us_ids)
+    n2 /= len(us_ids)
+    return {
+        "value": round((n3 * t3 + n2 * t2) * 1e6, 1),
+        "unit": "us/layer",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"one 3-bit and one 2-bit expert ({rows} rows, gate+up+down, dequant per call + fp32 "
+                   f"matmul, median of 3 after 1 warm-up: {t3 * 1e3:.0f} ms and {t2 * 1e3:.0f} ms), scaled by the "
+                   f"mean distinct experts per step ({n3:.1f} 3-bit + {n2:.1f} 2-bit)"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--rows", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extra", action="store_true", help="only the headline measurement")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
+              "the layer fits one MI355X and value is that GPU's throughput.", file=sys.stderr)
+        return 2
+    import torch
+    from dsv4_carve_amd import ops, synth
+
+    if not torch.cuda.is_available():
+        print("no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    t0 = time.time()
+    bits = synth.mixed_bits(EXPERTS)
+    layer = DeviceLayer(dev, EXPERTS, HIDDEN, INTER, bits, seed=1)
+    print(f"[bench] layer built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+
+    us, nbytes = time_layer(layer, dev, a.rows, TOPK, a.steps, a.warmup, seed=a.rows)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    print(f"[bench] rows={a.rows}: {us:.1f} us/layer, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+
+    extra = {}
+    if not a.no_extra:
+        sweep = {}
+        for m in (1, 2, 4, 8, 16):
+            u, b = time_layer(layer, dev, m, TOPK, 40, 3, seed=m)
+            uw, bw = time_layer(layer, dev, m, TOPK, 40, 3, seed=m, same_routing=True)
+            sweep[str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1),
+                             "frac": round(b / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(b),
+                             "warm_us": round(uw, 2), "warm_GBps": round(bw / (uw * 1e-6) / 1e9, 1)}
+            print(f"[bench] sweep m={m}: {sweep[str(m)]}", file=sys.stderr, flush=True)
+        extra["rows_sweep"] = sweep
+        # The reference's own geometry: one GPU's share of the layer under TP8
+        # (hidden 4096, intermediate 256, top-6, all experts at one width).
+        tp = {}
+        for kb in (2, 3):
+            tl = DeviceLayer(dev, EXPERTS, HIDDEN, 256, [kb] * EXPERTS, seed=7 + kb)
+            tp[f"K{kb}"] = {}
+            for m in (1, 2, 4, 8, 16):
+                u, b = time_layer(tl, dev, m, 6, 40, 3, seed=100 + m)
+                tp[f"K{kb}"][str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1)}
+            del tl
+            torch.cuda.empty_cache()
+        extra["tp8_slice_h4096_i256_top6"] = tp
+        print(f"[bench] tp8 slice: {tp}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not a.no_cpu:
+        pool_ids = [synth.routing(a.rows, EXPERTS, TOPK, seed=a.rows * 1000 + i)[0] for i in range(POOL)]
+        cpu = cpu_baseline(a.rows, bits, seed=1, us_ids=pool_ids)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    traffic = None
+    prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_c2_m16_traffic.json")
+    if os.path.isfile(prof):
+        with open(prof) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": "routed-MoE decode us/layer + achieved HBM GB/s (% of 8 TB/s), rows 1-16",
+        "value": round(us, 2),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(us / 1000.0, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded EXL3 trellis weights, N(0,1) router logits and activations)",
+        "config": {"workload": "routed-MoE decode layer: 256 experts, top-8, hidden 4096, intermediate 2048, "
+                               "experts 0-127 3-bit / 128-255 2-bit EXL3 MCG, fresh routing each step",
+                   "rows": a.rows, "experts": EXPERTS, "topk": TOPK, "hidden": HIDDEN, "intermediate": INTER},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "bytes_per_launch": int(nbytes)},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

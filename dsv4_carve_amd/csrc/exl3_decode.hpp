@@ -33,6 +33,17 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
+// Global-address-space views.  Pointers that reach a kernel through a device
+// table (the MoE weight tables) are generic to the compiler, which would emit
+// flat loads (these also count against the LDS counter and force broader
+// waits); casting them to address space 1 keeps the loads on the vector memory path.
+template <typename T>
+using gptr_t = const __attribute__((address_space(1))) T*;
+template <typename T>
+__device__ __forceinline__ gptr_t<T> as_global(const T* p) {
+    return (gptr_t<T>)p;
+}
+
 // ---------------------------------------------------------------- compile-time loops
 
 template <typename F, int... I>

@@ -18,7 +18,7 @@ __global__ __launch_bounds__(64) void dequant_raw_kernel(const int16_t* __restri
     if (tile >= k16 * n16) return;
     const int kt = tile / n16, nt = tile - kt * n16;
     TileRegs<BITS> t;
-    load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) + (size_t)tile * TileRegs<BITS>::NV);
+    load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) + (size_t)tile * tile_vecs<BITS>());
     const uint32_t* W = t.words();
     const size_t N = (size_t)n16 * 16;
     static_for<16>([&](auto KI) {
@@ -70,7 +70,7 @@ __global__ __launch_bounds__(64) void dequant_had_kernel(const int16_t* __restri
         const int kt = 8 * br + (lane >> 3), nt = 8 * bc + (lane & 7);
         TileRegs<BITS> t;
         load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) +
-                               ((size_t)kt * n16 + nt) * TileRegs<BITS>::NV);
+                               ((size_t)kt * n16 + nt) * tile_vecs<BITS>());
         const uint32_t* W = t.words();
         float* base = mat + (16 * (lane >> 3)) * HB_LD + 16 * (lane & 7);
         static_for<16>([&](auto KI) {
@@ -150,22 +150,24 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     const int cb = blockIdx.x / n_kc, kc = blockIdx.x - cb * n_kc;
     const int k0 = kc * nsteps * STEP_K;
 
+    // weights for step 0 are in flight while the input rotation runs
+    const u32x4_t* tp = tile_ptr<BITS>(trellis, N / 16, k0 / 16, cb * 16);
+    TileRegs<BITS> first;
+    load_tile<BITS>(first, tp);
     for (int m = 0; m < R; ++m)
-        for (int b = 0; b < nsteps * STEP_K; b += 128)
-            had_in_block(x, (size_t)m * K + k0 + b, 0, suh + k0 + b, xa, m, b, GEMV_NSTEP_CAP);
+        had_in_row(x, (size_t)m * K + k0, 0, suh + k0, xa, m, nsteps * STEP_K / 128, GEMV_NSTEP_CAP);
     __syncthreads();
 
     float4_t acc[16];
-    mma_steps<BITS, CB>(trellis, N / 16, k0 / 16, nsteps, cb * 16, xa, GEMV_NSTEP_CAP, R, acc);
+    mma_steps<BITS, CB>(first, tp, N / 16, nsteps, xa, GEMV_NSTEP_CAP, R, acc);
 
     const int cols = min(COLS, N - cb * COLS);
     store_partials(acc, partials + (size_t)kc * R * N + cb * COLS, N, R, cols);
-    __threadfence();
+    publish_fence();
     int old = 0;
     if (lane == 0) old = atomicAdd(&counters[cb], 1);
     old = __shfl(old, 0, 64);
     if (old != n_kc - 1) return;
-    __threadfence();
 
     // Last arriver: fixed-order split-K sum, output Hadamard, svh, store.
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
@@ -176,17 +178,14 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     for (int m = 0; m < R; ++m) {
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         if (ok) {
-            for (int s = 0; s < n_kc; ++s) {
-                const float4_t p = __builtin_nontemporal_load(
-                    reinterpret_cast<const float4_t*>(partials + ((size_t)s * R + m) * N + col));
-                v[0] += p[0]; v[1] += p[1]; v[2] += p[2]; v[3] += p[3];
-            }
+            const float4_t t = sum_partials(partials + (size_t)m * N + col, (size_t)R * N, n_kc);
+            v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
         }
         fwht128_x4(v);
         if (ok)
             for (int e = 0; e < 4; ++e) store_out(out, (size_t)m * N + col + e, out_kind, v[e] * HAD_NORM * sv[e]);
     }
-    if (lane == 0) counters[cb] = 0;
+    if (lane == 0) __hip_atomic_store(&counters[cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- per-bit-width launchers

@@ -69,19 +69,27 @@ __device__ __forceinline__ uint16_t decode_half(const uint32_t* W) {
 
 // ---------------------------------------------------------------- tile loads
 
-template <int BITS>
-struct TileRegs {
-    static constexpr int NV = 2 * BITS;     // 16-byte vectors per tile (32*BITS bytes)
-    u32x4_t v[NV];
+// Register buffer for one tile.  CAP (16-byte vectors) may exceed the 2*BITS a
+// tile needs so kernels serving several widths share one buffer; only the
+// first 2*BITS vectors are loaded and decoded.
+template <int CAP>
+struct TileBuf {
+    u32x4_t v[CAP];
     __device__ __forceinline__ const uint32_t* words() const {
         return reinterpret_cast<const uint32_t*>(v);
     }
 };
-
 template <int BITS>
-__device__ __forceinline__ void load_tile(TileRegs<BITS>& t, const u32x4_t* p) {
+using TileRegs = TileBuf<2 * BITS>;
+template <int BITS>
+constexpr int tile_vecs() { return 2 * BITS; }      // 32*BITS bytes per tile
+
+template <int BITS, int CAP>
+__device__ __forceinline__ void load_tile(TileBuf<CAP>& t, const u32x4_t* p) {
+    static_assert(CAP >= 2 * BITS, "tile buffer too small");
+    gptr_t<u32x4_t> q = as_global(p);
 #pragma unroll
-    for (int i = 0; i < TileRegs<BITS>::NV; ++i) t.v[i] = __builtin_nontemporal_load(p + i);
+    for (int i = 0; i < 2 * BITS; ++i) t.v[i] = __builtin_nontemporal_load(q + i);
 }
 
 // ---------------------------------------------------------------- MFMA step
@@ -118,44 +126,104 @@ __device__ __forceinline__ void mma_tile(const uint32_t* W, const half8_t (&A)[4
     });
 }
 
-// Runs `nsteps` (even) steps over k-slices [ks0, ks0 + 4*nsteps) for n-tiles
-// [nt0, nt0+16).  xa: LDS A tile for this item (see xa_index).  Lanes whose
-// n-tile is past the matrix decode a valid tile and their columns are dropped.
-template <int BITS, int CB>
-__device__ __forceinline__ void mma_steps(const int16_t* __restrict__ trellis, int n16, int ks0,
-                                          int nsteps, int nt0, const uint16_t* xa, int nsteps_cap,
-                                          int R, float4_t (&acc)[16]) {
+// Address of this lane's tile for the first step of an item, and the stride
+// between steps (in 16-byte vectors).
+template <int BITS>
+__device__ __forceinline__ const u32x4_t* tile_ptr(const int16_t* trellis, int n16, int ks0, int nt0) {
     const int lane = threadIdx.x & (WAVE - 1);
     const int g = lane >> 4, c = lane & 15;
     const int nt = min(nt0 + c, n16 - 1);
-    constexpr int NV = TileRegs<BITS>::NV;
-    const u32x4_t* p = reinterpret_cast<const u32x4_t*>(trellis) +
-                       ((size_t)(ks0 + g) * n16 + nt) * NV;
-    const size_t step = (size_t)4 * n16 * NV;
+    return reinterpret_cast<const u32x4_t*>(trellis) + ((size_t)(ks0 + g) * n16 + nt) * tile_vecs<BITS>();
+}
+
+// Runs `nsteps` (even) steps over k-slices [ks0, ks0 + 4*nsteps) for n-tiles
+// [nt0, nt0+16).  `first` must already hold the step-0 tile (issued by the
+// caller with load_tile(first, tile_ptr(...)) so the loads overlap whatever the
+// caller does meanwhile).  xa: LDS A tile for this item (see xa_index).  Lanes
+// whose n-tile is past the matrix decode a valid tile; their columns are dropped.
+template <int BITS, int CB, int CAP>
+__device__ __forceinline__ void mma_steps(TileBuf<CAP>& first, const u32x4_t* p, int n16, int nsteps,
+                                          const uint16_t* xa, int nsteps_cap, int R, float4_t (&acc)[16]) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int g = lane >> 4, c = lane & 15;
+    const size_t step = (size_t)4 * n16 * tile_vecs<BITS>();
     const bool live = c < R;
 
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 
     // nsteps is always even: two steps per iteration, ping-ponging the tile registers
-    TileRegs<BITS> buf[2];
-    load_tile<BITS>(buf[0], p);
+    TileBuf<CAP> second;
     for (int s = 0; s < nsteps; s += 2) {
-        load_tile<BITS>(buf[1], p + (s + 1) * step);
+        load_tile<BITS>(second, p + (s + 1) * step);
         {
             half8_t A[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, c, s, nsteps_cap, g, r, live);
-            mma_tile<BITS, CB>(buf[0].words(), A, acc);
+            mma_tile<BITS, CB>(first.words(), A, acc);
         }
-        if (s + 2 < nsteps) load_tile<BITS>(buf[0], p + (s + 2) * step);
+        if (s + 2 < nsteps) load_tile<BITS>(first, p + (s + 2) * step);
         {
             half8_t A[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, c, s + 1, nsteps_cap, g, r, live);
-            mma_tile<BITS, CB>(buf[1].words(), A, acc);
+            mma_tile<BITS, CB>(second.words(), A, acc);
         }
     }
+}
+
+// ---------------------------------------------------------------- cross-wave data
+//
+// Data handed from one wave to another (split-K partials, the MoE down input
+// and down output) moves with device-scope relaxed atomic stores and loads.
+// On gfx950 those are sc1 accesses that write through / bypass the per-XCD L2,
+// so they are coherent across XCDs without a full-L2 writeback + invalidate
+// (__threadfence at device scope costs one of each per call, which dominated
+// every item).  A producer orders its data before the counter or flag that
+// publishes it with publish_fence(); a consumer reads only after it observed
+// that counter or flag through a device-scope atomic.
+
+__device__ __forceinline__ void st_dev(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev4(float* p, float4_t v) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st_dev(p + i, v[i]);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float4_t ld_dev4(const float* p) {
+    return float4_t{ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3)};
+}
+
+// Completes this wave's outstanding memory operations (its device-scope data
+// stores included) before anything that follows, e.g. the counter or flag
+// update that hands the data to another wave.
+__device__ __forceinline__ void publish_fence() {
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+}
+
+// Sums `count` fp32 partial vectors p[i * stride] (float4 per lane) in index
+// order; loads are issued in batches of 8 so their latencies overlap.
+__device__ __forceinline__ float4_t sum_partials(const float* p, size_t stride, int count) {
+    float4_t acc = {0.f, 0.f, 0.f, 0.f};
+    for (int i0 = 0; i0 < count; i0 += 8) {
+        float4_t v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j < count) v[j] = ld_dev4(p + (size_t)(i0 + j) * stride);
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j < count) acc += v[j];
+    }
+    return acc;
 }
 
 // ---------------------------------------------------------------- Hadamard (wave64)
@@ -205,43 +273,62 @@ __device__ __forceinline__ void fwht128_x4(float (&v)[4]) {
     }
 }
 
-// Input rotation of one 128-element block into the LDS A tile:
-// xh = half( H (half(x * suh)) / sqrt(128) ), lna_moe_ticket.cu:119-144.
+// Input rotation of `nblocks` (<= 4) consecutive 128-element blocks of one row
+// into the LDS A tile: xh = half( H (half(x * suh)) / sqrt(128) ),
+// lna_moe_ticket.cu:119-144.  All global loads are issued before any math.
 // x_kind: 0 = fp16, 1 = bf16 (converted to fp16 with RNE first).
-__device__ __forceinline__ void had_in_block(const void* x, size_t x_off, int x_kind,
-                                             const uint16_t* suh, uint16_t* xa, int m,
-                                             int kblock_local /* multiple of 128 */, int nsteps_cap) {
+constexpr int HAD_MAX_BLOCKS = 4;
+
+__device__ __forceinline__ void had_in_row(const void* x, size_t x_off, int x_kind, const uint16_t* suh,
+                                           uint16_t* xa, int m, int nblocks, int nsteps_cap) {
     const int lane = threadIdx.x & (WAVE - 1);
-    uint32_t xx;
-    if (x_kind == 0) {
-        xx = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + x_off + 2 * lane);
-    } else {
-        const uint32_t b = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + x_off + 2 * lane);
-        xx = (uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(b & 0xffffu))) |
-             ((uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(b >> 16))) << 16);
+    uint32_t xx[HAD_MAX_BLOCKS], ss[HAD_MAX_BLOCKS];
+    gptr_t<uint32_t> xp = as_global(reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + x_off) + lane);
+    gptr_t<uint32_t> sp = as_global(reinterpret_cast<const uint32_t*>(suh) + lane);
+#pragma unroll
+    for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
+        if (b < nblocks) {
+            xx[b] = xp[64 * b];
+            ss[b] = sp[64 * b];
+        }
+#pragma unroll
+    for (int b = 0; b < HAD_MAX_BLOCKS; ++b) {
+        if (b >= nblocks) break;
+        uint32_t v2 = xx[b];
+        if (x_kind != 0)
+            v2 = (uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 & 0xffffu))) |
+                 ((uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 >> 16))) << 16);
+        // half(x*suh): the fp32 product of two halves is exact, so one RNE cast = half mul
+        float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 & 0xffffu) * f16_bits_to_f32(ss[b] & 0xffffu)));
+        float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 >> 16) * f16_bits_to_f32(ss[b] >> 16)));
+        fwht128_x2(v0, v1);
+        const int k0 = 128 * b + 2 * lane;
+        xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = f32_to_f16_bits(v0 * HAD_NORM);
+        xa[xa_index(m, (k0 + 1) >> 6, nsteps_cap, (k0 + 1) & 63)] = f32_to_f16_bits(v1 * HAD_NORM);
     }
-    const uint32_t ss = *reinterpret_cast<const uint32_t*>(suh + 2 * lane);
-    // half(x*suh): the fp32 product of two halves is exact, so one RNE cast = half mul
-    float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(xx & 0xffffu) * f16_bits_to_f32(ss & 0xffffu)));
-    float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(xx >> 16) * f16_bits_to_f32(ss >> 16)));
-    fwht128_x2(v0, v1);
-    const int k0 = kblock_local + 2 * lane;
-    xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = f32_to_f16_bits(v0 * HAD_NORM);
-    xa[xa_index(m, (k0 + 1) >> 6, nsteps_cap, (k0 + 1) & 63)] = f32_to_f16_bits(v1 * HAD_NORM);
 }
 
-// Copies an already-rotated fp16 block (128 elements) into the LDS A tile.
-__device__ __forceinline__ void copy_block(const uint16_t* src, uint16_t* xa, int m, int kblock_local,
-                                           int nsteps_cap) {
+// Copies `nblocks` (<= 4) already-rotated fp16 blocks of one row, written by
+// other waves, into the LDS A tile.
+__device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int m, int nblocks, int nsteps_cap) {
     const int lane = threadIdx.x & (WAVE - 1);
-    const uint32_t v = *reinterpret_cast<const uint32_t*>(src + 2 * lane);
-    const int k0 = kblock_local + 2 * lane;
-    xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = (uint16_t)(v & 0xffffu);
-    xa[xa_index(m, (k0 + 1) >> 6, nsteps_cap, (k0 + 1) & 63)] = (uint16_t)(v >> 16);
+    uint32_t v[HAD_MAX_BLOCKS];
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(src) + lane;
+#pragma unroll
+    for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
+        if (b < nblocks) v[b] = ld_dev(sp + 64 * b);
+#pragma unroll
+    for (int b = 0; b < HAD_MAX_BLOCKS; ++b) {
+        if (b >= nblocks) break;
+        const int k0 = 128 * b + 2 * lane;
+        xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = (uint16_t)(v[b] & 0xffffu);
+        xa[xa_index(m, (k0 + 1) >> 6, nsteps_cap, (k0 + 1) & 63)] = (uint16_t)(v[b] >> 16);
+    }
 }
 
 // Writes the 16 accumulators of one item (rows < R) as fp32 partials
-// dst[row * ld + col], col = 16 * (n-tile) + n within the 256-column block.
+// dst[row * ld + col], col = 16 * (n-tile) + n within the 256-column block,
+// with device-scope stores (another wave reduces them).
 __device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float* dst, size_t ld,
                                                int R, int cols_valid) {
     const int lane = threadIdx.x & (WAVE - 1);
@@ -251,10 +338,10 @@ __device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float*
     for (int i = 0; i < 4; ++i) {
         const int row = 4 * rg + i;
         if (row < R) {
-            float4_t* o = reinterpret_cast<float4_t*>(dst + (size_t)row * ld + 16 * c);
+            float* o = dst + (size_t)row * ld + 16 * c;
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                o[q] = float4_t{acc[4 * q][i], acc[4 * q + 1][i], acc[4 * q + 2][i], acc[4 * q + 3][i]};
+                st_dev4(o + 4 * q, float4_t{acc[4 * q][i], acc[4 * q + 1][i], acc[4 * q + 2][i], acc[4 * q + 3][i]});
         }
     }
 }

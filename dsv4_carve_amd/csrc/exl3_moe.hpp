@@ -165,12 +165,6 @@ __device__ inline void build_plan(const Params& P, Plan& pl, char* tmp) {
     __syncthreads();
 }
 
-// Row index of the i-th set bit of mask.
-__device__ __forceinline__ int nth_row(uint32_t mask, int i) {
-    for (int k = 0; k < i; ++k) mask &= mask - 1u;
-    return __ffs((int)mask) - 1;
-}
-
 // ---------------------------------------------------------------- device sync helpers
 
 __device__ __forceinline__ int wave_atomic_add(int* p, int v) {
@@ -179,13 +173,19 @@ __device__ __forceinline__ int wave_atomic_add(int* p, int v) {
     return __shfl(old, 0, WAVE);
 }
 
+// Spins until a device-scope flag reaches `target`.  The producer set it after
+// completing the device-scope stores it publishes, so reads that follow (also
+// device-scope) see that data.
 __device__ __forceinline__ void wait_flag(int* flag, int target) {
     if (threadIdx.x == 0) {
         while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target)
             __builtin_amdgcn_s_sleep(2);
     }
     __syncthreads();
-    __threadfence();
+}
+
+__device__ __forceinline__ void reset_counter(int* p) {
+    if (threadIdx.x == 0) __hip_atomic_store(p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ float silu_clamped(float g, float u, float limit) {
@@ -198,82 +198,56 @@ __device__ __forceinline__ float silu_clamped(float g, float u, float limit) {
 
 // ---------------------------------------------------------------- items
 
-template <uint32_t MASK, int CB>
-__device__ __forceinline__ void run_mma(int bits, const int16_t* trellis, int n16, int ks0, int nsteps,
-                                        int nt0, const uint16_t* xa, int R, float4_t (&acc)[16],
-                                        int* err) {
-    bool done = false;
-    static_for<8>([&](auto BI) {
-        constexpr int B = decltype(BI)::value + 1;
-        if constexpr ((MASK >> B) & 1u) {
-            if (!done && bits == B) {
-                mma_steps<B, CB>(trellis, n16, ks0, nsteps, nt0, xa, NSTEP_CAP, R, acc);
-                done = true;
-            }
-        }
-    });
-    if (!done) {
-        if (threadIdx.x == 0) atomicOr(err, 1);
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
-    }
-}
+// Item bodies are instantiated once per bit width; the kernel dispatches on the
+// expert's width at item granularity (a uniform branch per wave).
 
-// gate/up item
-template <uint32_t MASK, int CB>
-__device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch) {
+// gate/up item: (group g, projection p, 256-column block cb, k-chunk kc)
+template <int B, int CB>
+__device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int p, int cb, int kc,
+                            int epoch) {
     const Layout& L = P.L;
-    const int per_g = 2 * L.nI * L.SA;
-    const int g = t / per_g;
-    int rem = t - g * per_g;
-    const int p = rem / (L.nI * L.SA);
-    rem -= p * L.nI * L.SA;
-    const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
     const int e = pl.gexp[g], pb = pl.gpair[g];
     const uint32_t mask = pl.gmask[g];
     const int R = __popc(mask);
     const int kchunk = L.stepsA * STEP_K;
     const int k0 = kc * kchunk;
 
+    // step-0 weights are in flight while the input rotation runs
+    const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]), P.I / 16, k0 / 16,
+                                    cb * 16);
+    TileRegs<B> first;
+    load_tile<B>(first, tp);
     const uint16_t* suh = reinterpret_cast<const uint16_t*>((p ? P.usu : P.gsu)[e]);
+    uint32_t rest = mask;
     for (int r = 0; r < R; ++r) {
-        const int row = nth_row(mask, r);
-        for (int b = 0; b < kchunk; b += 128)
-            had_in_block(P.x, (size_t)row * P.H + k0 + b, P.x_kind, suh + k0 + b, xa, r, b, NSTEP_CAP);
+        const int row = __ffs((int)rest) - 1;
+        rest &= rest - 1u;
+        had_in_row(P.x, (size_t)row * P.H + k0, P.x_kind, suh + k0, xa, r, kchunk / 128, NSTEP_CAP);
     }
     __syncthreads();
 
     float4_t acc[16];
-    const int16_t* tr = reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]);
-    Ctrl* ctrl = at<Ctrl>(P.scratch, L.ctrl);
-    run_mma<MASK, CB>(pl.gbits[g], tr, P.I / 16, k0 / 16, L.stepsA, cb * 16, xa, R, acc, &ctrl->error);
+    mma_steps<B, CB>(first, tp, P.I / 16, L.stepsA, xa, NSTEP_CAP, R, acc);
 
     float* PA = at<float>(P.scratch, L.PA);
     const size_t ld = (size_t)2 * L.SA * P.I;
     store_partials(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, ld, R, COLS);
-    __threadfence();
+    publish_fence();
     int* cnt = at<int>(P.scratch, L.cntA) + g * L.nI + cb;
     if (wave_atomic_add(cnt, 1) != 2 * L.SA - 1) return;
-    __threadfence();
 
     // Last arriver: gate/up epilogue for (group g, column block cb).
     const int lane = threadIdx.x;
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    const uint16_t* gsv = reinterpret_cast<const uint16_t*>(P.gsv[e]);
-    const uint16_t* usv = reinterpret_cast<const uint16_t*>(P.usv[e]);
-    const uint16_t* dsu = reinterpret_cast<const uint16_t*>(P.dsu[e]);
+    gptr_t<uint16_t> gsv = as_global(reinterpret_cast<const uint16_t*>(P.gsv[e]));
+    gptr_t<uint16_t> usv = as_global(reinterpret_cast<const uint16_t*>(P.usv[e]));
+    gptr_t<uint16_t> dsu = as_global(reinterpret_cast<const uint16_t*>(P.dsu[e]));
     uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
     for (int r = 0; r < R; ++r) {
         const int pair = pb + r;
-        float gv[4] = {0.f, 0.f, 0.f, 0.f}, uv[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < L.SA; ++s) {
-            const float4_t a = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(
-                PA + ((size_t)(pair * 2 + 0) * L.SA + s) * P.I + col));
-            const float4_t b = __builtin_nontemporal_load(reinterpret_cast<const float4_t*>(
-                PA + ((size_t)(pair * 2 + 1) * L.SA + s) * P.I + col));
-            gv[0] += a[0]; gv[1] += a[1]; gv[2] += a[2]; gv[3] += a[3];
-            uv[0] += b[0]; uv[1] += b[1]; uv[2] += b[2]; uv[3] += b[3];
-        }
+        const float4_t ga = sum_partials(PA + (size_t)(pair * 2 + 0) * L.SA * P.I + col, P.I, L.SA);
+        const float4_t ua = sum_partials(PA + (size_t)(pair * 2 + 1) * L.SA * P.I + col, P.I, L.SA);
+        float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
         fwht128_x4(gv);
         fwht128_x4(uv);
         float dv[4];
@@ -289,16 +263,122 @@ __device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int
         uint2 packed;
         packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
         packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
-        *reinterpret_cast<uint2*>(DI + (size_t)pair * P.I + col) = packed;
+        uint32_t* di = reinterpret_cast<uint32_t*>(DI + (size_t)pair * P.I + col);
+        st_dev(di, packed.x);
+        st_dev(di + 1, packed.y);
     }
-    if (lane == 0) *cnt = 0;
-    __threadfence();
+    reset_counter(cnt);
+    publish_fence();
     if (lane == 0)
-        __hip_atomic_store(at<int>(P.scratch, L.doneA) + g * L.nI + cb, epoch + 1, __ATOMIC_RELEASE,
+        __hip_atomic_store(at<int>(P.scratch, L.doneA) + g * L.nI + cb, epoch + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// down item
+// down item: (group g, 256-column block cb of hidden, k-chunk kc of intermediate)
+template <int B, int CB>
+__device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int cb, int kc, int epoch) {
+    const Layout& L = P.L;
+    const int e = pl.gexp[g], pb = pl.gpair[g];
+    const uint32_t mask = pl.gmask[g];
+    const int R = __popc(mask);
+    const int kchunk = L.stepsB * STEP_K;
+    const int k0 = kc * kchunk;
+
+    const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[e]), P.H / 16, k0 / 16, cb * 16);
+    TileRegs<B> first;
+    load_tile<B>(first, tp);
+
+    // wait for the gate/up column blocks this chunk reads
+    int* doneA = at<int>(P.scratch, L.doneA) + g * L.nI;
+    for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c) wait_flag(doneA + c, epoch + 1);
+
+    const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
+    for (int r = 0; r < R; ++r) copy_row(DI + (size_t)(pb + r) * P.I + k0, xa, r, kchunk / 128, NSTEP_CAP);
+    __syncthreads();
+
+    float4_t acc[16];
+    mma_steps<B, CB>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
+
+    float* PB = at<float>(P.scratch, L.PB);
+    store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS);
+    publish_fence();
+    int* cnt = at<int>(P.scratch, L.cntB) + g * L.nH + cb;
+    if (wave_atomic_add(cnt, 1) != L.SB - 1) return;
+
+    // Last arriver for (group, H block): output rotation + svh.
+    const int lane = threadIdx.x;
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    gptr_t<uint16_t> dsv = as_global(reinterpret_cast<const uint16_t*>(P.dsv[e]));
+    float* DC = at<float>(P.scratch, L.DC);
+    for (int r = 0; r < R; ++r) {
+        const int pair = pb + r;
+        const float4_t t = sum_partials(PB + (size_t)pair * L.SB * P.H + col, P.H, L.SB);
+        float v[4] = {t[0], t[1], t[2], t[3]};
+        fwht128_x4(v);
+        float4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = v[i] * HAD_NORM * f16_bits_to_f32(dsv[col + i]);
+        st_dev4(DC + (size_t)pair * P.H + col, o);
+    }
+    reset_counter(cnt);
+    publish_fence();
+    int* cg = at<int>(P.scratch, L.cntG) + cb;
+    if (wave_atomic_add(cg, 1) != pl.U - 1) return;
+
+    // Last group to finish this H block: fixed-order gather over the top-k slots.
+    for (int row = 0; row < P.m; ++row) {
+        float4_t d[MAX_TOPK];
+        float wt[MAX_TOPK];
+#pragma unroll
+        for (int j = 0; j < MAX_TOPK; ++j) {       // issue every slot's load first
+            const int pair = j < P.topk ? pl.slotpair[row * P.topk + j] : -1;
+            wt[j] = pair >= 0 ? P.w[row * P.topk + j] : 0.f;
+            d[j] = pair >= 0 ? ld_dev4(DC + (size_t)pair * P.H + col) : float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+        float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < MAX_TOPK; ++j) {       // fp32 sum in top-k slot order
+            if (j >= P.topk || pl.slotpair[row * P.topk + j] < 0) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[j][i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
+    }
+    reset_counter(cg);
+}
+
+// Width dispatch: runs body<B> for the instantiated width B == bits; a width
+// outside MASK (the host checks against it) sets the error word and skips.
+template <uint32_t MASK, typename F>
+__device__ __forceinline__ void dispatch_bits(int bits, int* err, F&& body) {
+    bool done = false;
+    static_for<8>([&](auto BI) {
+        constexpr int B = decltype(BI)::value + 1;
+        if constexpr ((MASK >> B) & 1u) {
+            if (!done && bits == B) {
+                body(std::integral_constant<int, B>{});
+                done = true;
+            }
+        }
+    });
+    if (!done && threadIdx.x == 0) atomicOr(err, 1);
+}
+
+template <uint32_t MASK, int CB>
+__device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch) {
+    const Layout& L = P.L;
+    const int per_g = 2 * L.nI * L.SA;
+    const int g = t / per_g;
+    int rem = t - g * per_g;
+    const int p = rem / (L.nI * L.SA);
+    rem -= p * L.nI * L.SA;
+    const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
+    dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
+        item_a_body<decltype(BI)::value, CB>(P, pl, xa, g, p, cb, kc, epoch);
+    });
+}
+
 template <uint32_t MASK, int CB>
 __device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch) {
     const Layout& L = P.L;
@@ -306,75 +386,9 @@ __device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int
     const int g = t / per_g;
     const int rem = t - g * per_g;
     const int cb = rem / L.SB, kc = rem - (rem / L.SB) * L.SB;
-    const int e = pl.gexp[g], pb = pl.gpair[g];
-    const uint32_t mask = pl.gmask[g];
-    const int R = __popc(mask);
-    const int kchunk = L.stepsB * STEP_K;
-    const int k0 = kc * kchunk;
-
-    // wait for the gate/up column blocks this chunk reads
-    int* doneA = at<int>(P.scratch, L.doneA) + g * L.nI;
-    for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c) wait_flag(doneA + c, epoch + 1);
-
-    const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
-    for (int r = 0; r < R; ++r)
-        for (int b = 0; b < kchunk; b += 128)
-            copy_block(DI + (size_t)(pb + r) * P.I + k0 + b, xa, r, b, NSTEP_CAP);
-    __syncthreads();
-
-    float4_t acc[16];
-    const int16_t* tr = reinterpret_cast<const int16_t*>(P.dt[e]);
-    Ctrl* ctrl = at<Ctrl>(P.scratch, L.ctrl);
-    run_mma<MASK, CB>(pl.gbits[g], tr, P.H / 16, k0 / 16, L.stepsB, cb * 16, xa, R, acc, &ctrl->error);
-
-    float* PB = at<float>(P.scratch, L.PB);
-    store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS);
-    __threadfence();
-    int* cnt = at<int>(P.scratch, L.cntB) + g * L.nH + cb;
-    if (wave_atomic_add(cnt, 1) != L.SB - 1) return;
-    __threadfence();
-
-    // Last arriver for (group, H block): output rotation + svh.
-    const int lane = threadIdx.x;
-    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    const uint16_t* dsv = reinterpret_cast<const uint16_t*>(P.dsv[e]);
-    float* DC = at<float>(P.scratch, L.DC);
-    for (int r = 0; r < R; ++r) {
-        const int pair = pb + r;
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int s = 0; s < L.SB; ++s) {
-            const float4_t a = __builtin_nontemporal_load(
-                reinterpret_cast<const float4_t*>(PB + ((size_t)pair * L.SB + s) * P.H + col));
-            v[0] += a[0]; v[1] += a[1]; v[2] += a[2]; v[3] += a[3];
-        }
-        fwht128_x4(v);
-        float4_t o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = v[i] * HAD_NORM * f16_bits_to_f32(dsv[col + i]);
-        *reinterpret_cast<float4_t*>(DC + (size_t)pair * P.H + col) = o;
-    }
-    if (lane == 0) *cnt = 0;
-    __threadfence();
-    int* cg = at<int>(P.scratch, L.cntG) + cb;
-    if (wave_atomic_add(cg, 1) != pl.U - 1) return;
-    __threadfence();
-
-    // Last group to finish this H block: fixed-order gather over the top-k slots.
-    for (int row = 0; row < P.m; ++row) {
-        float s4[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int j = 0; j < P.topk; ++j) {
-            const int pair = pl.slotpair[row * P.topk + j];
-            if (pair < 0) continue;
-            const float wt = P.w[row * P.topk + j];
-            const float4_t d = __builtin_nontemporal_load(
-                reinterpret_cast<const float4_t*>(DC + (size_t)pair * P.H + col));
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt * d[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
-    }
-    if (lane == 0) *cg = 0;
+    dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
+        item_b_body<decltype(BI)::value, CB>(P, pl, xa, g, cb, kc, epoch);
+    });
 }
 
 template <uint32_t MASK, int CB>
@@ -404,13 +418,13 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
     }
 
     // Retire; the last wave out resets the queue and advances the epoch.
+    publish_fence();
     if (threadIdx.x == 0) {
-        __threadfence();
         const int r = atomicAdd(&ctrl->retire, 1);
         if (r == (int)gridDim.x - 1) {
             __hip_atomic_store(&ctrl->ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&ctrl->retire, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&ctrl->epoch, epoch + 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ctrl->epoch, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
 }
