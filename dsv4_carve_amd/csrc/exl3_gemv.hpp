@@ -183,24 +183,33 @@ __device__ __forceinline__ void mma_steps(TileBuf<CAP>& first, const u32x4_t* p,
 // publishes it with publish_fence(); a consumer reads only after it observed
 // that counter or flag through a device-scope atomic.
 
-__device__ __forceinline__ void st_dev(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ void st_dev(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_dev4(float* p, float4_t v) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) st_dev(p + i, v[i]);
-}
-__device__ __forceinline__ float ld_dev(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float4_t ld_dev4(const float* p) {
-    return float4_t{ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3)};
+// 16-byte device-scope store (one instruction; consecutive lanes should write
+// consecutive 16-byte chunks so the write-through traffic is whole lines).
+__device__ __forceinline__ void st_dev4(float* p, float4_t v) {
+    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+__device__ __forceinline__ void st_dev2(uint32_t* p, uint2 v) {
+    asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+}
+// Up to 8 16-byte device-scope loads issued back to back, then one wait.  The
+// wait lists every destination as read-write so no use can be scheduled
+// before it.
+template <int N>
+__device__ __forceinline__ void ld_dev4_batch(float4_t (&v)[8], const float* const (&p)[8]) {
+    static_assert(N >= 1 && N <= 8, "batch of 1..8");
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+        asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[j]) : "v"(p[j]) : "memory");
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
+                 :
+                 : "memory");
 }
 
 // Completes this wave's outstanding memory operations (its device-scope data
@@ -210,15 +219,46 @@ __device__ __forceinline__ void publish_fence() {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 }
 
+// Sums two independent sets of `count` partials (a and b) in index order with
+// up to 16 loads in flight (8 of each per batch).
+__device__ __forceinline__ void sum_partials2(const float* a, const float* b, size_t stride, int count,
+                                              float4_t& sa, float4_t& sb) {
+    sa = float4_t{0.f, 0.f, 0.f, 0.f};
+    sb = sa;
+    for (int i0 = 0; i0 < count; i0 += 8) {
+        float4_t va[8], vb[8];
+        const float* qa[8];
+        const float* qb[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            qa[j] = a + (size_t)min(i0 + j, count - 1) * stride;
+            qb[j] = b + (size_t)min(i0 + j, count - 1) * stride;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(va[j]) : "v"(qa[j]) : "memory");
+        ld_dev4_batch<8>(vb, qb);      // its wait covers the eight loads above too
+        asm volatile("" : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]), "+v"(va[4]), "+v"(va[5]),
+                          "+v"(va[6]), "+v"(va[7]));
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            if (i0 + j < count) {
+                sa += va[j];
+                sb += vb[j];
+            }
+    }
+}
+
 // Sums `count` fp32 partial vectors p[i * stride] (float4 per lane) in index
 // order; loads are issued in batches of 8 so their latencies overlap.
 __device__ __forceinline__ float4_t sum_partials(const float* p, size_t stride, int count) {
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
     for (int i0 = 0; i0 < count; i0 += 8) {
         float4_t v[8];
+        const float* q[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            if (i0 + j < count) v[j] = ld_dev4(p + (size_t)(i0 + j) * stride);
+        for (int j = 0; j < 8; ++j) q[j] = p + (size_t)min(i0 + j, count - 1) * stride;
+        ld_dev4_batch<8>(v, q);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             if (i0 + j < count) acc += v[j];
@@ -328,22 +368,29 @@ __device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int 
 
 // Writes the 16 accumulators of one item (rows < R) as fp32 partials
 // dst[row * ld + col], col = 16 * (n-tile) + n within the 256-column block,
-// with device-scope stores (another wave reduces them).
-__device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float* dst, size_t ld,
-                                               int R, int cols_valid) {
+// with device-scope stores (another wave reduces them).  The MFMA result
+// layout (lane = n-tile + 16 * row group, register = column in the tile) is
+// transposed through LDS (`tbuf`, >= R KB, free at this point) so every store
+// instruction writes one contiguous 1 KB row.
+__device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float* dst, size_t ld, int R,
+                                               int cols_valid, float* tbuf) {
     const int lane = threadIdx.x & (WAVE - 1);
     const int c = lane & 15, rg = lane >> 4;
-    if (16 * c >= cols_valid) return;
+    __syncthreads();
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int row = 4 * rg + i;
         if (row < R) {
-            float* o = dst + (size_t)row * ld + 16 * c;
+            float4_t* t = reinterpret_cast<float4_t*>(tbuf + row * COLS + 16 * c);
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                st_dev4(o + 4 * q, float4_t{acc[4 * q][i], acc[4 * q + 1][i], acc[4 * q + 2][i], acc[4 * q + 3][i]});
+                t[q] = float4_t{acc[4 * q][i], acc[4 * q + 1][i], acc[4 * q + 2][i], acc[4 * q + 3][i]};
         }
     }
+    __syncthreads();
+    if (4 * lane < cols_valid)
+        for (int row = 0; row < R; ++row)
+            st_dev4(dst + (size_t)row * ld + 4 * lane, reinterpret_cast<const float4_t*>(tbuf + row * COLS)[lane]);
 }
 
 }  // namespace exl3

@@ -35,27 +35,32 @@ constexpr int MAX_SLOTS = MAX_M * MAX_TOPK;   // also the bound on groups and pa
 constexpr int MAX_EXPERTS = 2048;             // route-plan bitmask capacity
 constexpr int NSTEP_CAP = 8;
 
-// Steps (64 k-rows each) per item: the largest even divisor of k/64 that is <= 8.
-__host__ __device__ inline int item_steps(int k) {
+// Steps (64 k-rows each) per item: a power of two in 2..8 dividing k/64.  The
+// host starts from 8 and halves while the items would not give every resident
+// wave at least one (small batches read few experts and need short items to
+// spread them over the whole GPU).
+__host__ __device__ inline int item_steps(int k, int64_t units, int64_t waves) {
     const int ks = k / STEP_K;
     int s = NSTEP_CAP;
-    while (s > 2 && ks % s) s -= 2;
+    while (s > 2 && (ks % s != 0 || units * (ks / s) < waves)) s /= 2;
     return s;
 }
 
 struct Layout {
     int nI, nH, SA, SB, stepsA, stepsB;
-    int64_t ctrl, cntA, doneA, cntB, cntG, PA, DI, PB, DC, total;
+    int64_t ctrl, cntA, doneA, cntB, cntG, doneB, PA, DI, PB, DC, total;
 };
 
 __host__ __device__ inline int64_t al(int64_t v) { return (v + 255) / 256 * 256; }
 
-__host__ __device__ inline Layout layout(int H, int I, int topk) {
+// stepsA/stepsB: steps per gate/up and per down item (2, 4 or 8; the scratch
+// size is taken at 2, the most partials).
+__host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2, int stepsB = 2) {
     Layout L;
     L.nI = I / COLS;
     L.nH = H / COLS;
-    L.stepsA = item_steps(H);
-    L.stepsB = item_steps(I);
+    L.stepsA = stepsA;
+    L.stepsB = stepsB;
     L.SA = H / STEP_K / L.stepsA;
     L.SB = I / STEP_K / L.stepsB;
     const int64_t P = (int64_t)MAX_M * topk;      // max pairs = max groups
@@ -65,6 +70,7 @@ __host__ __device__ inline Layout layout(int H, int I, int topk) {
     L.doneA = o; o = al(o + P * L.nI * 4);
     L.cntB = o;  o = al(o + P * L.nH * 4);
     L.cntG = o;  o = al(o + (int64_t)L.nH * 4);
+    L.doneB = o; o = al(o + (int64_t)L.nH * 4);
     L.PA = o;    o = al(o + P * 2 * L.SA * I * 4);
     L.DI = o;    o = al(o + P * I * 2);
     L.PB = o;    o = al(o + P * L.SB * H * 4);
@@ -93,10 +99,48 @@ struct Params {
     float limit;
     char* scratch;
     Layout L;
+    int64_t trace_off;   // start of the phase-trace region (EXL3_TRACE builds)
 };
 
 template <typename T>
 __device__ __forceinline__ T* at(char* base, int64_t off) { return reinterpret_cast<T*>(base + off); }
+
+// ---------------------------------------------------------------- phase tracing
+//
+// Built with -DEXL3_TRACE=1, every wave appends (event, argument, time) records
+// to a region after the scratch layout (TRACE_EVENTS per wave, TRACE_WAVES
+// waves); time is s_memrealtime (100 MHz).  Off by default: no code, no bytes.
+#ifndef EXL3_TRACE
+#define EXL3_TRACE 0
+#endif
+constexpr int TRACE_EVENTS = 128;
+constexpr int TRACE_WAVES = 4096;
+enum TraceEvent : uint32_t {
+    EV_START = 1, EV_PLAN, EV_A_BEGIN, EV_A_MMA, EV_A_END, EV_EPI_A_END, EV_B_BEGIN, EV_B_WAITED,
+    EV_B_MMA, EV_B_END, EV_EPI_B_END, EV_GATHER_END, EV_RETIRE
+};
+inline int64_t trace_bytes() { return EXL3_TRACE ? (int64_t)TRACE_WAVES * TRACE_EVENTS * 8 + 256 : 0; }
+
+struct Tracer {
+#if EXL3_TRACE
+    uint2* buf = nullptr;
+    int n = 0;
+    __device__ void init(char* base) {
+        if (blockIdx.x < TRACE_WAVES) buf = reinterpret_cast<uint2*>(base) + (size_t)blockIdx.x * TRACE_EVENTS;
+    }
+    __device__ void operator()(uint32_t ev, uint32_t arg = 0) {
+        if (buf && n < TRACE_EVENTS - 1 && threadIdx.x == 0) {
+            const uint64_t t = __builtin_amdgcn_s_memrealtime();
+            buf[n] = make_uint2((ev << 24) | (arg & 0xffffffu), (uint32_t)t);
+            buf[n + 1] = make_uint2(0u, 0u);
+        }
+        ++n;
+    }
+#else
+    __device__ void init(char*) {}
+    __device__ void operator()(uint32_t, uint32_t = 0) {}
+#endif
+};
 
 // ---------------------------------------------------------------- route plan
 
@@ -196,6 +240,17 @@ __device__ __forceinline__ float silu_clamped(float g, float u, float limit) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
+// Four consecutive fp16 scale values starting at element `col` of the vector
+// whose address is `addr` (col is a multiple of 4, so one 8-byte load).
+__device__ __forceinline__ void load_half4(uint16_t (&v)[4], int64_t addr, int col) {
+    gptr_t<uint32_t> p = as_global(reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(addr) + col));
+    const uint32_t a = p[0], b = p[1];
+    v[0] = (uint16_t)a;
+    v[1] = (uint16_t)(a >> 16);
+    v[2] = (uint16_t)b;
+    v[3] = (uint16_t)(b >> 16);
+}
+
 // ---------------------------------------------------------------- items
 
 // Item bodies are instantiated once per bit width; the kernel dispatches on the
@@ -204,7 +259,7 @@ __device__ __forceinline__ float silu_clamped(float g, float u, float limit) {
 // gate/up item: (group g, projection p, 256-column block cb, k-chunk kc)
 template <int B, int CB>
 __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int p, int cb, int kc,
-                            int epoch) {
+                            int epoch, Tracer& tr) {
     const Layout& L = P.L;
     const int e = pl.gexp[g], pb = pl.gpair[g];
     const uint32_t mask = pl.gmask[g];
@@ -228,55 +283,62 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
 
     float4_t acc[16];
     mma_steps<B, CB>(first, tp, P.I / 16, L.stepsA, xa, NSTEP_CAP, R, acc);
+    tr(EV_A_MMA);
 
     float* PA = at<float>(P.scratch, L.PA);
     const size_t ld = (size_t)2 * L.SA * P.I;
-    store_partials(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, ld, R, COLS);
+    store_partials(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, ld, R, COLS,
+                   reinterpret_cast<float*>(xa));
     publish_fence();
     int* cnt = at<int>(P.scratch, L.cntA) + g * L.nI + cb;
-    if (wave_atomic_add(cnt, 1) != 2 * L.SA - 1) return;
+    const bool last = wave_atomic_add(cnt, 1) == 2 * L.SA - 1;
+    tr(EV_A_END, last);
+    if (!last) return;
 
     // Last arriver: gate/up epilogue for (group g, column block cb).
     const int lane = threadIdx.x;
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    gptr_t<uint16_t> gsv = as_global(reinterpret_cast<const uint16_t*>(P.gsv[e]));
-    gptr_t<uint16_t> usv = as_global(reinterpret_cast<const uint16_t*>(P.usv[e]));
-    gptr_t<uint16_t> dsu = as_global(reinterpret_cast<const uint16_t*>(P.dsu[e]));
+    // scales first: their loads are in flight during the partial sums
+    uint16_t gsv[4], usv[4], dsu[4];
+    load_half4(gsv, P.gsv[e], col);
+    load_half4(usv, P.usv[e], col);
+    load_half4(dsu, P.dsu[e], col);
     uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
     for (int r = 0; r < R; ++r) {
         const int pair = pb + r;
-        const float4_t ga = sum_partials(PA + (size_t)(pair * 2 + 0) * L.SA * P.I + col, P.I, L.SA);
-        const float4_t ua = sum_partials(PA + (size_t)(pair * 2 + 1) * L.SA * P.I + col, P.I, L.SA);
+        float4_t ga, ua;
+        sum_partials2(PA + (size_t)(pair * 2 + 0) * L.SA * P.I + col, PA + (size_t)(pair * 2 + 1) * L.SA * P.I + col,
+                      P.I, L.SA, ga, ua);
         float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
         fwht128_x4(gv);
         fwht128_x4(uv);
         float dv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float gg = gv[i] * HAD_NORM * f16_bits_to_f32(gsv[col + i]);
-            const float uu = uv[i] * HAD_NORM * f16_bits_to_f32(usv[col + i]);
+            const float gg = gv[i] * HAD_NORM * f16_bits_to_f32(gsv[i]);
+            const float uu = uv[i] * HAD_NORM * f16_bits_to_f32(usv[i]);
             const uint16_t act = f32_to_f16_bits(silu_clamped(gg, uu, P.limit));
             // down input rotation: half(act * down_suh), fp32 butterflies
-            dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[col + i])));
+            dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[i])));
         }
         fwht128_x4(dv);
         uint2 packed;
         packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
         packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
-        uint32_t* di = reinterpret_cast<uint32_t*>(DI + (size_t)pair * P.I + col);
-        st_dev(di, packed.x);
-        st_dev(di + 1, packed.y);
+        st_dev2(reinterpret_cast<uint32_t*>(DI + (size_t)pair * P.I + col), packed);
     }
     reset_counter(cnt);
     publish_fence();
     if (lane == 0)
         __hip_atomic_store(at<int>(P.scratch, L.doneA) + g * L.nI + cb, epoch + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
+    tr(EV_EPI_A_END);
 }
 
 // down item: (group g, 256-column block cb of hidden, k-chunk kc of intermediate)
 template <int B, int CB>
-__device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int cb, int kc, int epoch) {
+__device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int cb, int kc, int epoch,
+                            Tracer& tr) {
     const Layout& L = P.L;
     const int e = pl.gexp[g], pb = pl.gpair[g];
     const uint32_t mask = pl.gmask[g];
@@ -291,6 +353,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     // wait for the gate/up column blocks this chunk reads
     int* doneA = at<int>(P.scratch, L.doneA) + g * L.nI;
     for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c) wait_flag(doneA + c, epoch + 1);
+    tr(EV_B_WAITED);
 
     const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
     for (int r = 0; r < R; ++r) copy_row(DI + (size_t)(pb + r) * P.I + k0, xa, r, kchunk / 128, NSTEP_CAP);
@@ -298,17 +361,22 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
 
     float4_t acc[16];
     mma_steps<B, CB>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
+    tr(EV_B_MMA);
 
     float* PB = at<float>(P.scratch, L.PB);
-    store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS);
+    store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS,
+                   reinterpret_cast<float*>(xa));
     publish_fence();
     int* cnt = at<int>(P.scratch, L.cntB) + g * L.nH + cb;
-    if (wave_atomic_add(cnt, 1) != L.SB - 1) return;
+    const bool last = wave_atomic_add(cnt, 1) == L.SB - 1;
+    tr(EV_B_END, last);
+    if (!last) return;
 
     // Last arriver for (group, H block): output rotation + svh.
     const int lane = threadIdx.x;
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    gptr_t<uint16_t> dsv = as_global(reinterpret_cast<const uint16_t*>(P.dsv[e]));
+    uint16_t dsv[4];
+    load_half4(dsv, P.dsv[e], col);
     float* DC = at<float>(P.scratch, L.DC);
     for (int r = 0; r < R; ++r) {
         const int pair = pb + r;
@@ -317,35 +385,51 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
         fwht128_x4(v);
         float4_t o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = v[i] * HAD_NORM * f16_bits_to_f32(dsv[col + i]);
+        for (int i = 0; i < 4; ++i) o[i] = v[i] * HAD_NORM * f16_bits_to_f32(dsv[i]);
         st_dev4(DC + (size_t)pair * P.H + col, o);
     }
     reset_counter(cnt);
     publish_fence();
     int* cg = at<int>(P.scratch, L.cntG) + cb;
-    if (wave_atomic_add(cg, 1) != pl.U - 1) return;
-
-    // Last group to finish this H block: fixed-order gather over the top-k slots.
-    for (int row = 0; row < P.m; ++row) {
-        float4_t d[MAX_TOPK];
-        float wt[MAX_TOPK];
-#pragma unroll
-        for (int j = 0; j < MAX_TOPK; ++j) {       // issue every slot's load first
-            const int pair = j < P.topk ? pl.slotpair[row * P.topk + j] : -1;
-            wt[j] = pair >= 0 ? P.w[row * P.topk + j] : 0.f;
-            d[j] = pair >= 0 ? ld_dev4(DC + (size_t)pair * P.H + col) : float4_t{0.f, 0.f, 0.f, 0.f};
-        }
-        float s4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < MAX_TOPK; ++j) {       // fp32 sum in top-k slot order
-            if (j >= P.topk || pl.slotpair[row * P.topk + j] < 0) continue;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[j][i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
-    }
+    const bool done = wave_atomic_add(cg, 1) == pl.U - 1;
+    tr(EV_EPI_B_END, done);
+    if (!done) return;
+    // Every group has finished this H block: publish it to the gather items.
     reset_counter(cg);
+    publish_fence();
+    if (lane == 0)
+        __hip_atomic_store(at<int>(P.scratch, L.doneB) + cb, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// gather item: (H block cb, row) -- out[row][block] = sum over the row's top-k
+// slots, in slot order, of weight * down output (fp32), one cast.
+__device__ void item_g(const Params& P, const Plan& pl, int t, int epoch, Tracer& tr) {
+    const Layout& L = P.L;
+    const int cb = t / P.m, row = t - (t / P.m) * P.m;
+    wait_flag(at<int>(P.scratch, L.doneB) + cb, epoch + 1);
+    const int lane = threadIdx.x;
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    const float* DC = at<float>(P.scratch, L.DC);
+    float4_t d[MAX_TOPK];
+    float wt[MAX_TOPK];
+    const float* q[MAX_TOPK];
+#pragma unroll
+    for (int j = 0; j < MAX_TOPK; ++j) {       // issue every slot's load first
+        const int pair = j < P.topk ? pl.slotpair[row * P.topk + j] : -1;
+        wt[j] = pair >= 0 ? P.w[row * P.topk + j] : 0.f;
+        q[j] = DC + (size_t)(pair >= 0 ? pair : 0) * P.H + col;
+    }
+    ld_dev4_batch<MAX_TOPK>(d, q);
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < MAX_TOPK; ++j) {       // fp32 sum in top-k slot order
+        if (j >= P.topk || pl.slotpair[row * P.topk + j] < 0) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[j][i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
+    tr(EV_GATHER_END);
 }
 
 // Width dispatch: runs body<B> for the instantiated width B == bits; a width
@@ -366,7 +450,7 @@ __device__ __forceinline__ void dispatch_bits(int bits, int* err, F&& body) {
 }
 
 template <uint32_t MASK, int CB>
-__device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch) {
+__device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch, Tracer& tr) {
     const Layout& L = P.L;
     const int per_g = 2 * L.nI * L.SA;
     const int g = t / per_g;
@@ -375,19 +459,19 @@ __device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int
     rem -= p * L.nI * L.SA;
     const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
     dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
-        item_a_body<decltype(BI)::value, CB>(P, pl, xa, g, p, cb, kc, epoch);
+        item_a_body<decltype(BI)::value, CB>(P, pl, xa, g, p, cb, kc, epoch, tr);
     });
 }
 
 template <uint32_t MASK, int CB>
-__device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch) {
+__device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch, Tracer& tr) {
     const Layout& L = P.L;
     const int per_g = L.nH * L.SB;
     const int g = t / per_g;
     const int rem = t - g * per_g;
     const int cb = rem / L.SB, kc = rem - (rem / L.SB) * L.SB;
     dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
-        item_b_body<decltype(BI)::value, CB>(P, pl, xa, g, cb, kc, epoch);
+        item_b_body<decltype(BI)::value, CB>(P, pl, xa, g, cb, kc, epoch, tr);
     });
 }
 
@@ -397,27 +481,41 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
     __shared__ Plan pl;
     static_assert(sizeof(xa) >= 6 * MAX_EXPERTS, "plan workspace");
     const Layout& L = P.L;
+    Tracer tr;
+    tr.init(P.scratch + P.trace_off);
+    tr(EV_START);
     Ctrl* ctrl = at<Ctrl>(P.scratch, L.ctrl);
     const int epoch = __hip_atomic_load(&ctrl->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
     build_plan(P, pl, reinterpret_cast<char*>(xa));
+    tr(EV_PLAN);
     const int U = pl.U;
     const int nA = U * 2 * L.nI * L.SA;
-    const int total = nA + U * L.nH * L.SB;
+    const int nAB = nA + U * L.nH * L.SB;
+    const int total = U ? nAB + L.nH * P.m : 0;
 
     if (U == 0 && blockIdx.x == 0) {   // nothing routed: the layer output is zero
         for (int i = threadIdx.x; i < P.m * P.H; i += WAVE) store_out(P.out, i, P.out_kind, 0.f);
     }
 
-    for (;;) {
-        const int t = wave_atomic_add(&ctrl->ticket, 1);
-        if (t >= total) break;
-        if (t < nA) item_a<MASK, CB>(P, pl, xa, t, epoch);
-        else item_b<MASK, CB>(P, pl, xa, t - nA, epoch);
+    // Ticket order: gate/up items, down items, gather items.  A wave's first
+    // ticket is its own index (no burst on the counter at launch); later ones
+    // come from the counter, offset by the grid size.
+    for (int t = blockIdx.x; t < total; t = (int)gridDim.x + wave_atomic_add(&ctrl->ticket, 1)) {
+        if (t < nA) {
+            tr(EV_A_BEGIN, t);
+            item_a<MASK, CB>(P, pl, xa, t, epoch, tr);
+        } else if (t < nAB) {
+            tr(EV_B_BEGIN, t - nA);
+            item_b<MASK, CB>(P, pl, xa, t - nA, epoch, tr);
+        } else {
+            item_g(P, pl, t - nAB, epoch, tr);
+        }
         __syncthreads();   // xa is rewritten by the next item
     }
 
     // Retire; the last wave out resets the queue and advances the epoch.
+    tr(EV_RETIRE);
     publish_fence();
     if (threadIdx.x == 0) {
         const int r = atomicAdd(&ctrl->retire, 1);

@@ -57,7 +57,7 @@ int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t top
     if (hidden <= 0 || hidden % COLS || intermediate <= 0 || intermediate % COLS)
         return fail("hidden and intermediate must be positive multiples of 256");
     if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..8");
-    return layout((int)hidden, (int)intermediate, (int)topk).total;
+    return layout((int)hidden, (int)intermediate, (int)topk).total + trace_bytes();
 }
 
 int exl3_moe_max_rows(void) { return MAX_M; }
@@ -103,14 +103,21 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
         if (bits < 1 || bits > 8) return fail("bits must be in 1..8");
         mask = 1u << bits;
     }
-    const Layout L = layout((int)hidden, (int)intermediate, (int)topk);
-    if (scratch_bytes < L.total) return fail("scratch too small (see exl3_moe_scratch_bytes)");
+    const int64_t trace_off = layout((int)hidden, (int)intermediate, (int)topk).total;
+    if (scratch_bytes < trace_off + trace_bytes()) return fail("scratch too small (see exl3_moe_scratch_bytes)");
 
     int idx = -1;
     const int ninst = (int)(sizeof(kInstances) / sizeof(kInstances[0]));
     for (int i = 0; i < ninst; ++i)
         if (kInstances[i].cb == codebook && (kInstances[i].mask & mask) == mask) { idx = i; break; }
     if (idx < 0) return fail("no kernel instance for this bit-width set / codebook");
+
+    // Distinct experts are at most min(E, m * topk); size the items for that.
+    const int64_t groups = n_experts < m * topk ? n_experts : m * topk;
+    const int64_t resident = (int64_t)device_cus() * cached_waves(idx);
+    const int stepsA = item_steps((int)hidden, groups * 2 * (intermediate / COLS), resident);
+    const int stepsB = item_steps((int)intermediate, groups * (hidden / COLS), resident);
+    const Layout L = layout((int)hidden, (int)intermediate, (int)topk, stepsA, stepsB);
 
     Params P;
     P.x = x; P.x_kind = x_kind; P.out = out; P.out_kind = out_kind;
@@ -123,10 +130,9 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
     P.limit = swiglu_limit;
     P.scratch = reinterpret_cast<char*>(scratch);
     P.L = L;
+    P.trace_off = trace_off;
 
-    const int64_t groups = n_experts < m * topk ? n_experts : m * topk;
-    const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB);
-    const int64_t resident = (int64_t)device_cus() * cached_waves(idx);
+    const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB) + (int64_t)L.nH * m;
     const int waves = (int)(items < resident ? items : resident);
     return kInstances[idx].launch(P, waves, reinterpret_cast<hipStream_t>(stream));
 }

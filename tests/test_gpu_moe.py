@@ -248,8 +248,11 @@ def test_c2_against_oracle(c2, m):
 
 
 def test_c2_size_independent_properties(c2, dev):
-    """At m=16: bitwise repeat; row-permutation equivariance; every row equals
-    the same row computed alone (rows never interact)."""
+    """At m=16: bitwise repeat; row-permutation equivariance (bit-exact); every
+    row equals the same row computed alone up to fp32 reassociation (the split-K
+    chunking adapts to the batch size, so the summation tree may differ and an
+    fp16 rounding of the activation can flip: rel-L2 1e-4, ten times inside the
+    parity bar)."""
     import torch
 
     m = 16
@@ -263,5 +266,5 @@ def test_c2_size_independent_properties(c2, dev):
     p = c2.run(x[perm], ids[perm], w[perm])
     assert torch.equal(p, a[torch.as_tensor(perm, device=dev)])
     for r in (0, 9, 15):
-        single = c2.run(x[r:r + 1], ids[r:r + 1], w[r:r + 1])
-        assert torch.equal(single[0], a[r]), f"row {r} differs when computed alone"
+        single = c2.run(x[r:r + 1], ids[r:r + 1], w[r:r + 1])[0].cpu().numpy()
+        assert rel_l2(single, a[r].cpu().numpy()) < 1e-4, f"row {r} differs when computed alone"
