@@ -1,0 +1,677 @@
+"""The vllm-exl3 plugin's EXL3 linear / routed-MoE call surface, over libexl3_amd.
+
+Mirrors what vLLM calls on this path, with the same names, argument meaning and
+error behaviour, so the plugin's dispatch code can switch to this package:
+
+  * ``LinearEXL3`` / ``make_linear_exl3`` / ``execute_exl3_linear`` -- the
+    exllamav3 linear (recipe-lna/exllamav3/exl3.py.lna:16-218,
+    recipe-lna/vllm_exl3_exl3.py.lna:889-926).  Up to AUTO_RECONSTRUCT_THRESHOLD
+    rows run the trellis-decode GEMV kernel; more rows reconstruct the
+    Hadamard-folded fp16 weight on the GPU and run one hgemm.
+  * ``apply_exl3_experts`` and its helpers -- routed experts
+    (recipe-lna/vllm_exl3_exl3.py.lna:951-1296, 1543-1569, 1707-1779): backend
+    selection by VLLM_EXL3_MOE_KERNEL, strict levels by VLLM_EXL3_MOE_STRICT,
+    one-shot decline logging, per-backend call counters, the shared zeroed
+    scratch, and the unique-expert LinearEXL3 loop.
+  * ``Exl3MoEMethod`` / ``Exl3LinearMethod`` -- create_weights /
+    process_weights_after_loading / apply (recipe-lna/vllm_exl3_exl3.py.lna:2045-2307,
+    2310-2853), importable without vLLM.
+
+Backends here: ``lna2`` is the gfx950 routed-MoE decode kernel (default under
+``auto``); ``loop`` is the unique-expert loop over LinearEXL3, whose every
+matrix product is the same library's GEMV/GEMM.  Both run on the GPU only: a
+CPU tensor fails in the op dispatcher, and there is no CPU fallback.
+
+Beyond the reference's kernel ABI the routed kernel accepts one bit width per
+expert (the experts of a layer may mix widths), top-k up to 8 and any hidden /
+intermediate size that is a multiple of 256.
+"""
+
+from __future__ import annotations
+
+import logging
+import os
+from typing import Any
+
+import torch
+import torch.nn.functional as F
+from torch.nn import Parameter
+
+from . import ops
+
+logger = logging.getLogger("vllm." + __name__)
+
+MCG_MULTIPLIER = 0xCBAC1FED
+MCG_MARKER_SIGNED_INT32 = -877912083
+MUL1_MULTIPLIER = 0x83DCD12D
+MUL1_MARKER_SIGNED_INT32 = -2082680531
+EXL3_SUFFIXES = ("trellis", "suh", "svh", "mcg", "mul1")
+SWIGLU_LIMIT_DEFAULT = 10.0
+AUTO_RECONSTRUCT_THRESHOLD = 144
+MAX_RECONSTRUCT_SLICE_N = 32768
+MOE_TABLE_KEYS = ops.MOE_TABLE_KEYS
+
+
+# ---------------------------------------------------------------- linear
+
+
+class NullConfig:
+    """Stand-in for exllamav3's config when a linear is built without a model."""
+
+    class infer_params:
+        no_reconstruct = False
+
+
+class LinearEXL3:
+    """One EXL3 linear: y = had_out(had_in(x * suh) @ Wq) * svh (+ bias).
+
+    Constructor checks and forward semantics follow
+    recipe-lna/exllamav3/exl3.py.lna:18-99, 114-139."""
+
+    quant_type: str = "exl3"
+
+    def __init__(self, config, in_features: int, out_features: int, scale=None, su=None, sv=None,
+                 suh=None, svh=None, trellis=None, mcg=None, mul1=None, bias=None, out_dtype=None,
+                 transformers_fix: bool = False, key: str | None = None):
+        assert scale is None, "scale is no longer used"
+        assert su is not None or suh is not None, "either su (packed) or suh (unpacked) is required"
+        assert sv is not None or svh is not None, "either sv (packed) or svh (unpacked) is required"
+        assert trellis is not None, "trellis is required"
+        if su is not None:
+            assert su.dtype == torch.int16, "su is wrong datatype"
+        if sv is not None:
+            assert sv.dtype == torch.int16, "sv is wrong datatype"
+        if suh is not None:
+            assert suh.dtype == torch.half, "suh is wrong datatype"
+        if svh is not None:
+            assert svh.dtype == torch.half, "svh is wrong datatype"
+        assert trellis.dtype == torch.int16, "trellis is wrong datatype"
+        assert len(trellis.shape) == 3, "trellis must have dim = 3"
+        if bias is not None and bias.dtype == torch.float:
+            bias = bias.to(torch.half)
+        self.config = config if config is not None else NullConfig()
+        self.transformers_fix = transformers_fix
+        self.key = key
+        self.suh = (suh if suh is not None else self.unpack_bf(su)).contiguous()
+        self.svh = (svh if svh is not None else self.unpack_bf(sv)).contiguous()
+        self.trellis = trellis.contiguous()
+        self.K = trellis.shape[-1] // 16
+        self.in_features = in_features
+        self.out_features = out_features
+        assert self.trellis.shape[0] * 16 == in_features and self.trellis.shape[1] * 16 == out_features, \
+            "trellis shape does not match in/out features"
+        self.bias = bias
+        self.out_dtype = out_dtype
+        self.default_out_dtype = out_dtype or torch.half
+        self.mcg_tensor = mcg
+        self.mul1_tensor = mul1
+        self.mcg = mcg is not None
+        self.mul1 = mul1 is not None
+        self.codebook = ops.codebook_id(self.mcg, self.mul1)
+
+    @staticmethod
+    def unpack_bf(bitfield: torch.Tensor) -> torch.Tensor:
+        """Packed sign bits -> fp16 +-1: bit i of int16 word j is element 16*j+i,
+        set means -1 (recipe-lna/exllamav3/exl3.py.lna:142-158)."""
+        bits = bitfield.reshape(-1).view(torch.uint16).to(torch.int32)
+        shifts = torch.arange(16, device=bits.device, dtype=torch.int32)
+        b = (bits.unsqueeze(-1) >> shifts) & 1
+        return (1.0 - 2.0 * b.to(torch.float16)).reshape(-1).contiguous()
+
+    def forward(self, x: torch.Tensor, params: dict, out_dtype: torch.dtype | None = None) -> torch.Tensor:
+        if "ovr" in params:
+            ovr = params["ovr"]
+            if self.key in ovr and getattr(ovr[self.key], "inner", None) is not self:
+                return ovr[self.key].forward(x, params, out_dtype)
+        assert x.is_contiguous(), f"LinearEXL3 {self.key}: non-contiguous input {tuple(x.shape)}"
+        dtype = out_dtype or self.default_out_dtype
+        rows = x.numel() // x.shape[-1]
+        if not params.get("reconstruct") and (rows <= AUTO_RECONSTRUCT_THRESHOLD
+                                              or self.config.infer_params.no_reconstruct):
+            x2 = x.view(rows, self.in_features)
+            if x2.dtype != torch.float16:
+                x2 = x2.to(torch.float16)
+            y = torch.empty((rows, self.out_features), dtype=dtype if dtype in ops.OUT_KIND else torch.float32,
+                            device=x.device)
+            ops.gemm_into(x2, self.trellis, self.suh, self.svh, y, self.codebook)
+            if y.dtype != dtype:
+                y = y.to(dtype)
+            if self.bias is not None:
+                y += self.bias
+            return y.view(*x.shape[:-1], self.out_features)
+        return self.reconstruct_hgemm(x, out_dtype)
+
+    def reconstruct_hgemm(self, x: torch.Tensor, out_dtype) -> torch.Tensor:
+        """Many rows: reconstruct the original-basis weight (both rotations and
+        sign vectors folded in) on the GPU, then one fp16 GEMM
+        (recipe-lna/exllamav3/exl3.py.lna:161-218, its fused-reconstruct branch)."""
+        rows = x.numel() // x.shape[-1]
+        x2 = x.view(rows, self.in_features)
+        if x2.dtype != torch.float16:
+            x2 = x2.to(torch.float16)
+        w = ops.dequant_trellis(self.trellis, self.suh, self.svh, self.K, self.mcg, self.mul1)
+        y = torch.matmul(x2, w).to(out_dtype or self.default_out_dtype)
+        if self.bias is not None:
+            y += self.bias
+        return y.view(*x.shape[:-1], self.out_features)
+
+    def get_weight_tensor(self) -> torch.Tensor:
+        return ops.dequant_trellis(self.trellis, self.suh, self.svh, self.K, self.mcg, self.mul1)
+
+    def get_inner_weight_tensor(self) -> torch.Tensor:
+        return ops.reconstruct_weight(self.trellis, self.codebook)
+
+    def get_bias_tensor(self) -> torch.Tensor | None:
+        return self.bias
+
+
+def make_linear_exl3(trellis, suh, svh, mcg=None, mul1=None, *, out_dtype=torch.float16) -> LinearEXL3:
+    """A LinearEXL3 over already-sharded packed tensors
+    (recipe-lna/vllm_exl3_exl3.py.lna:889-911)."""
+    return LinearEXL3(None, int(suh.numel()), int(svh.numel()), trellis=trellis.contiguous(),
+                      suh=suh.contiguous(), svh=svh.contiguous(),
+                      mcg=mcg.contiguous() if mcg is not None else None,
+                      mul1=mul1.contiguous() if mul1 is not None else None,
+                      out_dtype=out_dtype, transformers_fix=True)
+
+
+def execute_exl3_linear(x, trellis, suh, svh, mcg=None, mul1=None, *, out_dtype=torch.float32):
+    """recipe-lna/vllm_exl3_exl3.py.lna:914-926."""
+    inner = make_linear_exl3(trellis, suh, svh, mcg, mul1, out_dtype=torch.float16)
+    return inner.forward(x.contiguous().half(), {}, out_dtype=out_dtype)
+
+
+# ---------------------------------------------------------------- backend selection
+
+
+def get_moe_kernel_backend() -> str:
+    """VLLM_EXL3_MOE_KERNEL: "lna2" (the routed-MoE decode kernel), "loop" (the
+    unique-expert LinearEXL3 loop) or "auto" (= lna2).  Unknown values warn and
+    mean auto (recipe-lna/vllm_exl3_exl3.py.lna:1052-1067)."""
+    requested = os.environ.get("VLLM_EXL3_MOE_KERNEL", "auto").strip().lower()
+    if requested not in {"lna2", "loop", "auto"}:
+        logger.warning("Unknown VLLM_EXL3_MOE_KERNEL=%r; using auto selection", requested)
+        requested = "auto"
+    return "lna2" if requested == "auto" else requested
+
+
+def moe_kernel_strict() -> int:
+    """VLLM_EXL3_MOE_STRICT: 1 raises when the kernel is not ready, 2 also on
+    shape declines (recipe-lna/vllm_exl3_exl3.py.lna:1070-1089)."""
+    try:
+        return int(os.environ.get("VLLM_EXL3_MOE_STRICT", "0") or 0)
+    except ValueError:
+        return 0
+
+
+_MOE_CALLS = {"lna2": 0, "loop": 0}
+_LNA2_REJECT_LOGGED: set[str] = set()
+_LNA2_ACTIVE_LOGGED = False
+
+
+def moe_kernel_call_counts() -> dict[str, int]:
+    return dict(_MOE_CALLS)
+
+
+def reset_moe_kernel_call_counts() -> None:
+    for k in _MOE_CALLS:
+        _MOE_CALLS[k] = 0
+
+
+def moe_kernel_declined_reasons() -> list[str]:
+    return sorted(_LNA2_REJECT_LOGGED)
+
+
+def _lna2_log_active() -> None:
+    global _LNA2_ACTIVE_LOGGED
+    if not _LNA2_ACTIVE_LOGGED:
+        _LNA2_ACTIVE_LOGGED = True
+        logger.warning("LNA2 MoE kernel ACTIVE (gfx950 routed-MoE decode)")
+
+
+def _lna2_log_reject(why: str, *, not_ready: bool = False) -> None:
+    """One log line per distinct decline reason; raises under the strict level
+    that covers this class of decline (recipe-lna/vllm_exl3_exl3.py.lna:1143-1156)."""
+    if why not in _LNA2_REJECT_LOGGED and len(_LNA2_REJECT_LOGGED) < 12:
+        _LNA2_REJECT_LOGGED.add(why)
+        logger.warning("LNA2 declined (falling back to the LinearEXL3 loop): %s", why)
+    level = moe_kernel_strict()
+    if level >= (1 if not_ready else 2):
+        raise RuntimeError("VLLM_EXL3_MOE_KERNEL=lna2 with VLLM_EXL3_MOE_STRICT=%d, but the lna2 kernel "
+                           "declined this call: %s" % (level, why))
+
+
+def lna2_moe_kernel_available() -> bool:
+    try:
+        ops._lib.load()
+        return True
+    except Exception:
+        return False
+
+
+def lna2_max_rows() -> int:
+    return ops.moe_max_rows()
+
+
+# ---------------------------------------------------------------- routing glue
+
+
+def pin_exl3_expert_map(layer, device: torch.device) -> torch.Tensor | None:
+    """Move expert_map to `device` (int64) once, before any graph capture
+    (recipe-lna/vllm_exl3_exl3.py.lna:951-960)."""
+    emap = getattr(layer, "expert_map", None)
+    if emap is None:
+        return None
+    if emap.device != device or emap.dtype != torch.long:
+        layer.expert_map = emap.to(device=device, dtype=torch.long)
+    return layer.expert_map
+
+
+def map_topk_to_local(ids: torch.Tensor, n_local: int, expert_map: torch.Tensor | None) -> torch.Tensor:
+    """Flattened global ids -> local ids; negative, out-of-range or unmapped ids
+    become the sentinel n_local (recipe-lna/vllm_exl3_exl3.py.lna:963-985)."""
+    flat = ids.reshape(-1)
+    sentinel = flat.new_full(flat.shape, n_local)
+    if expert_map is None:
+        return torch.where((flat < 0) | (flat >= n_local), sentinel, flat)
+    if expert_map.device != flat.device or expert_map.dtype != torch.long:
+        raise RuntimeError("EXL3 expert_map is not pinned to the hidden-state device; "
+                           "call pin_exl3_expert_map before fused apply (CUDA graphs forbid the copy)")
+    n_global = int(expert_map.numel())
+    if n_global == 0:
+        return sentinel
+    mapped = expert_map[flat.clamp(0, n_global - 1)]
+    bad = (flat < 0) | (flat >= n_global) | (mapped < 0) | (mapped >= n_local)
+    return torch.where(bad, sentinel, mapped)
+
+
+# ---------------------------------------------------------------- routed experts
+
+
+def apply_exl3_python_loop(x2d, ids, weights, inners, expert_map, limit, *, only_experts=None, out=None):
+    """Unique-expert LinearEXL3 loop (recipe-lna/vllm_exl3_exl3.py.lna:988-1027):
+    for each distinct routed expert, gate and up in fp32, clamped SiLU*mul,
+    fp16 activation, down in fp32, scaled and index-added into an fp32 output."""
+    tokens, hidden = x2d.shape
+    if out is None:
+        out = torch.zeros(tokens, hidden, dtype=torch.float32, device=x2d.device)
+    for raw in torch.unique(ids).tolist():
+        e = int(raw)
+        if e < 0:
+            continue
+        if expert_map is not None:
+            e = int(expert_map[e].item()) if expert_map.numel() > e else e
+            if e < 0:
+                continue
+        if e >= len(inners) or (only_experts is not None and e not in only_experts):
+            continue
+        token_idx, k_pos = (ids == int(raw)).nonzero(as_tuple=True)
+        h = x2d.index_select(0, token_idx).contiguous().half()
+        pack = inners[e]
+        gate = pack["gate"].forward(h, {}, out_dtype=torch.float32)
+        up = pack["up"].forward(h, {}, out_dtype=torch.float32)
+        act = F.silu(gate.clamp(max=limit)) * up.clamp(min=-limit, max=limit)
+        down = pack["down"].forward(act.contiguous().half(), {}, out_dtype=torch.float32)
+        out.index_add_(0, token_idx, down * weights[token_idx, k_pos].unsqueeze(-1).to(torch.float32))
+    return out
+
+
+def _validate_lna_pointer_contract(inners, hidden: int, intermediate: int) -> None:
+    """Every expert's packed tensors must be contiguous, on one device, and of
+    the layer's geometry before their addresses go into the pointer tables
+    (recipe-lna/vllm_exl3_exl3.py.lna:1318-1374)."""
+    dev = inners[0]["gate"].trellis.device
+    for e, pack in enumerate(inners):
+        for name, k, n in (("gate", hidden, intermediate), ("up", hidden, intermediate),
+                           ("down", intermediate, hidden)):
+            lin = pack[name]
+            kb = lin.K
+            if kb != pack["gate"].K:
+                raise RuntimeError(f"expert {e}: {name} has {kb} bits, gate has {pack['gate'].K}")
+            want = (k // 16, n // 16, 16 * kb)
+            for what, t, shape, dt in (("trellis", lin.trellis, want, torch.int16),
+                                       ("suh", lin.suh, (k,), torch.float16),
+                                       ("svh", lin.svh, (n,), torch.float16)):
+                if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous() or t.device != dev:
+                    raise RuntimeError(f"expert {e} {name}.{what}: {tuple(t.shape)} {t.dtype} "
+                                       f"contiguous={t.is_contiguous()} {t.device}; want {shape} {dt} on {dev}")
+            if lin.codebook != inners[0]["gate"].codebook:
+                raise RuntimeError(f"expert {e} {name}: codebook differs from the layer's")
+
+
+_LNA2_SCRATCH: dict[int, torch.Tensor] = {}
+
+
+def _lna2_scratch_for(layer, device: torch.device) -> torch.Tensor:
+    """The shared routed-MoE scratch of this device, zeroed once on creation and
+    self-resetting after (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296).  One
+    launch at a time per device: launches on concurrent streams would share it."""
+    hidden = int(layer._exl3_hidden_size)
+    inter = int(layer._exl3_intermediate_local)
+    topk = int(getattr(layer, "_exl3_topk", 8))
+    nbytes = ops.moe_scratch_bytes(hidden, inter, topk)
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _LNA2_SCRATCH.get(int(idx))
+    if buf is None or buf.numel() < nbytes:
+        if torch.cuda.is_current_stream_capturing():
+            raise RuntimeError("LNA2 scratch was not prewarmed for this device")
+        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
+        _LNA2_SCRATCH[int(idx)] = buf
+    return buf
+
+
+def lna2_scratch_bytes_resident() -> int:
+    return sum(int(b.numel()) for b in _LNA2_SCRATCH.values())
+
+
+def _prepare_lna_state(layer, inners) -> None:
+    """Preflight: validate the pointer contract and reserve the scratch; sets
+    layer._exl3_lna_ready / _exl3_lna_error (recipe-lna/vllm_exl3_exl3.py.lna:1395-1449)."""
+    layer._exl3_lna_ready = False
+    try:
+        _validate_lna_pointer_contract(inners, int(layer._exl3_hidden_size), int(layer._exl3_intermediate_local))
+        ops._lib.load()
+        _lna2_scratch_for(layer, inners[0]["gate"].trellis.device)
+        layer._exl3_lna_ready = True
+        layer._exl3_lna_error = None
+    except Exception as exc:
+        layer._exl3_lna_error = repr(exc)
+        logger.warning("LNA2 preflight FAILED for %s: %r -- the MoE will fall back to the LinearEXL3 loop",
+                       getattr(layer, "prefix", "?"), exc)
+        if moe_kernel_strict():
+            raise
+
+
+def build_exl3_fused_state(layer, inners: list[dict[str, Any]]) -> None:
+    """Pointer tables (int64 data_ptr per expert and tensor), the per-expert
+    bit-width table and its mask, once after load; then the preflight
+    (recipe-lna/vllm_exl3_exl3.py.lna:1543-1594).  The weights must stay alive
+    and must not move while the tables are in use."""
+    device = inners[0]["gate"].trellis.device
+    tables = {}
+    for key in MOE_TABLE_KEYS:
+        which, attr = key.split("_", 1)
+        tables[key] = torch.tensor([int(getattr(p[which], attr).data_ptr()) for p in inners],
+                                   dtype=torch.int64, device=device)
+    layer._exl3_ptrs = tables
+    bits = [int(p["gate"].K) for p in inners]
+    layer._exl3_bits_table = torch.tensor(bits, dtype=torch.int8, device=device)
+    layer._exl3_bits_mask = ops.bits_mask_of(bits)
+    layer._exl3_codebook = int(inners[0]["gate"].codebook)
+    layer._exl3_ptr_sources = [(p["gate"].trellis, p["down"].trellis) for p in inners]
+    if len(set(bits)) == 1:
+        layer._exl3_k = bits[0]
+    if get_moe_kernel_backend() == "lna2":
+        _prepare_lna_state(layer, inners)
+
+
+def _ptrs_stale(layer, inners) -> bool:
+    """The tables hold raw addresses: a re-bound weight invalidates them."""
+    src = getattr(layer, "_exl3_ptr_sources", None)
+    return src is None or len(src) != len(inners) or any(
+        a is not p["gate"].trellis or b is not p["down"].trellis for (a, b), p in zip(src, inners))
+
+
+def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
+    """The routed-MoE decode kernel, or None (logged) when it declines
+    (recipe-lna/vllm_exl3_exl3.py.lna:1190-1248)."""
+    if not lna2_moe_kernel_available() or not getattr(layer, "_exl3_lna_ready", False):
+        _lna2_log_reject("module=%s lna_ready=%s lna_error=%s" % (
+            lna2_moe_kernel_available(), getattr(layer, "_exl3_lna_ready", None),
+            getattr(layer, "_exl3_lna_error", None)), not_ready=True)
+        return None
+    hidden = int(getattr(layer, "_exl3_hidden_size", -1))
+    inter = int(getattr(layer, "_exl3_intermediate_local", -1))
+    topk = int(ids.shape[-1])
+    if (not x2d.is_cuda or x2d.dim() != 2 or not 1 <= int(x2d.shape[0]) <= lna2_max_rows()
+            or int(x2d.shape[1]) != hidden or hidden % 256 or inter % 256 or not 1 <= topk <= 8
+            or x2d.dtype not in (torch.float16, torch.bfloat16) or not float(limit) > 0.0):
+        _lna2_log_reject("geometry x=%s dtype=%s max_rows=%d hidden=%s inter=%s topk=%s limit=%s" % (
+            tuple(x2d.shape), x2d.dtype, lna2_max_rows(), hidden, inter, topk, limit))
+        return None
+    ptrs = getattr(layer, "_exl3_ptrs", None)
+    if not isinstance(ptrs, dict) or any(k not in ptrs for k in MOE_TABLE_KEYS):
+        _lna2_log_reject("ptr table incomplete", not_ready=True)
+        return None
+    if _ptrs_stale(layer, inners):
+        _lna2_log_reject("ptr tables are stale (weights re-bound after build_exl3_fused_state)", not_ready=True)
+        return None
+    local = map_topk_to_local(ids, len(inners), expert_map).reshape(ids.shape)
+    safe_ids = local.to(torch.int32).contiguous()
+    route_w = weights.reshape(local.shape).to(torch.float32).contiguous()
+    scratch = _lna2_scratch_for(layer, x2d.device)
+    x_in = x2d if x2d.is_contiguous() else x2d.contiguous()
+    out = torch.empty_like(x_in)
+    ops.moe_decode(x_in, out, ptrs, safe_ids, route_w, intermediate=inter,
+                   expert_bits=layer._exl3_bits_table, bits_mask=layer._exl3_bits_mask,
+                   codebook=layer._exl3_codebook, swiglu_limit=float(limit), scratch=scratch)
+    _MOE_CALLS["lna2"] += 1
+    return out
+
+
+def apply_exl3_experts(x, topk_ids, topk_weights, layer, *, limit: float = SWIGLU_LIMIT_DEFAULT,
+                       fused: bool | None = None) -> torch.Tensor:
+    """Routed-expert apply (recipe-lna/vllm_exl3_exl3.py.lna:1707-1779): the
+    routed kernel when selected and able, else the LinearEXL3 loop.  `fused`
+    False forces the loop; True requires the pointer tables.  Output has x's
+    shape and dtype."""
+    inners = getattr(layer, "_exl3_inners", None)
+    if not inners:
+        raise RuntimeError("EXL3 experts were not built after weight load")
+    tokens, hidden = x.shape[-2], x.shape[-1]
+    x2d = x.reshape(tokens, hidden)
+    ids = topk_ids.reshape(tokens, -1).to(torch.long)
+    weights = topk_weights.reshape(tokens, -1)
+    expert_map = pin_exl3_expert_map(layer, x2d.device)
+    have_ptrs = bool(getattr(layer, "_exl3_ptrs", None))
+    if fused is True and not have_ptrs:
+        raise RuntimeError("EXL3 fused apply requested but pointer tables are missing")
+    if get_moe_kernel_backend() == "lna2" and fused is not False:
+        try:
+            res = _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit)
+        except Exception as exc:
+            if moe_kernel_strict():
+                raise
+            res = None
+            layer._exl3_lna2_error = repr(exc)
+            logger.warning("LNA2 dispatch failed; falling back: %s", exc)
+        if res is not None:
+            layer._exl3_last_apply = "lna2"
+            _lna2_log_active()
+            return res.to(dtype=x.dtype).reshape(x.shape)
+    out = apply_exl3_python_loop(x2d, ids, weights, inners, expert_map, limit)
+    _MOE_CALLS["loop"] += 1
+    layer._exl3_last_apply = "loop"
+    return out.to(dtype=x.dtype).reshape(x.shape)
+
+
+# ---------------------------------------------------------------- TP sharding of packed tensors
+
+
+def _narrow_tp(t: torch.Tensor, dim: int, rank: int, size: int) -> torch.Tensor:
+    if size == 1:
+        return t
+    n = t.shape[dim]
+    if n % size:
+        raise ValueError(f"dimension {dim} of size {n} does not split over {size} ranks")
+    step = n // size
+    return t.narrow(dim, rank * step, step).contiguous()
+
+
+def shard_exl3_col(loaded: torch.Tensor, suffix: str, tp_rank: int, tp_size: int) -> torch.Tensor:
+    """Column split (output features): trellis dim 1, svh (recipe-lna/vllm_exl3_exl3.py.lna:855-861)."""
+    if suffix == "trellis":
+        return _narrow_tp(loaded, 1, tp_rank, tp_size)
+    if suffix == "svh":
+        return _narrow_tp(loaded, 0, tp_rank, tp_size)
+    return loaded
+
+
+def shard_exl3_row(loaded: torch.Tensor, suffix: str, tp_rank: int, tp_size: int) -> torch.Tensor:
+    """Row split (input features): trellis dim 0, suh (recipe-lna/vllm_exl3_exl3.py.lna:864-870)."""
+    if suffix == "trellis":
+        return _narrow_tp(loaded, 0, tp_rank, tp_size)
+    if suffix == "suh":
+        return _narrow_tp(loaded, 0, tp_rank, tp_size)
+    return loaded
+
+
+def _suffix_from_mapped_name(weight_name: str) -> str:
+    tail = weight_name.rsplit(".", 1)[-1]
+    for suffix in EXL3_SUFFIXES:
+        if tail == suffix or tail.endswith("_" + suffix):
+            return suffix
+    raise ValueError(f"not an EXL3 packed name: {weight_name}")
+
+
+# ---------------------------------------------------------------- vLLM quant methods
+
+
+class Exl3MoEMethod:
+    """Packed MCG trellis routed experts: create / load / finalize / apply
+    (recipe-lna/vllm_exl3_exl3.py.lna:2045-2307).  One bit width per layer, as
+    in the checkpoint ABI (w13_* [E, 2, ...], w2_* [E, ...])."""
+
+    def __init__(self, moe=None, quant_config=None, bits: int | None = None, tp_rank: int = 0, tp_size: int = 1):
+        self.moe = moe
+        self.quant_config = quant_config
+        self.bits = int(bits) if bits is not None else int(getattr(quant_config, "bits", 0))
+        self.tp_rank, self.tp_size = tp_rank, tp_size
+
+    def get_fused_moe_quant_config(self, layer):
+        return None
+
+    def create_weights(self, layer, num_experts: int, hidden_size: int, intermediate_size_per_partition: int,
+                       params_dtype=None, **extra_weight_attrs) -> None:
+        del params_dtype, extra_weight_attrs
+        inter = intermediate_size_per_partition
+        if hidden_size % 16 or inter % 16:
+            raise ValueError(f"EXL3 trellis tiles are 16-wide; hidden={hidden_size} intermediate_local={inter}")
+        kw, it, ot = self.bits * 16, hidden_size // 16, inter // 16
+        shapes = {
+            "w13_trellis": ((num_experts, 2, it, ot, kw), torch.int16),
+            "w13_suh": ((num_experts, 2, hidden_size), torch.float16),
+            "w13_svh": ((num_experts, 2, inter), torch.float16),
+            "w13_mcg": ((num_experts, 2, 1), torch.int32),
+            "w2_trellis": ((num_experts, ot, it, kw), torch.int16),
+            "w2_suh": ((num_experts, inter), torch.float16),
+            "w2_svh": ((num_experts, hidden_size), torch.float16),
+            "w2_mcg": ((num_experts, 1), torch.int32),
+        }
+        for name, (shape, dt) in shapes.items():
+            p = Parameter(torch.empty(shape, dtype=dt), requires_grad=False)
+            p.weight_loader = self._load_exl3
+            layer.register_parameter(name, p)
+        layer._exl3_hidden_size = hidden_size
+        layer._exl3_intermediate_local = inter
+        layer._exl3_k_words = kw
+        layer._exl3_bits = self.bits
+
+    def _load_exl3(self, param: Parameter, loaded_weight: torch.Tensor, weight_name: str,
+                   shard_id: str = "w1", expert_id: int = 0, return_success: bool = False):
+        """Copy one checkpoint tensor of one expert (w1 = gate, w3 = up, w2 =
+        down) into its slot, TP-sharded (recipe-lna/vllm_exl3_exl3.py.lna:2147-2195)."""
+        suffix = _suffix_from_mapped_name(weight_name)
+        loaded = loaded_weight.detach().contiguous()
+        if shard_id in ("w1", "w3"):
+            sharded = shard_exl3_col(loaded, suffix, self.tp_rank, self.tp_size)
+            dest = param.data[expert_id, 0 if shard_id == "w1" else 1]
+        elif shard_id == "w2":
+            sharded = shard_exl3_row(loaded, suffix, self.tp_rank, self.tp_size)
+            dest = param.data[expert_id]
+        else:
+            raise ValueError(f"unknown EXL3 shard_id={shard_id}")
+        if tuple(dest.shape) != tuple(sharded.shape):
+            raise RuntimeError(f"EXL3 load shape mismatch {weight_name} shard={shard_id} expert={expert_id}: "
+                               f"dest {tuple(dest.shape)} != loaded {tuple(sharded.shape)}")
+        dest.copy_(sharded)
+        return True if return_success else None
+
+    def process_weights_after_loading(self, layer) -> None:
+        if not hasattr(layer, "w13_trellis"):
+            return
+        for m in (layer.w13_mcg.reshape(-1), layer.w2_mcg.reshape(-1)):
+            if not torch.all(m == MCG_MARKER_SIGNED_INT32):
+                raise RuntimeError("EXL3 mcg marker is not the MCG int32 0xCBAC1FED / "
+                                   f"{MCG_MARKER_SIGNED_INT32}; packed ABI mismatch")
+        inners = []
+        for e in range(int(layer.w13_trellis.shape[0])):
+            inners.append({
+                "gate": make_linear_exl3(layer.w13_trellis[e, 0], layer.w13_suh[e, 0], layer.w13_svh[e, 0],
+                                         layer.w13_mcg[e, 0]),
+                "up": make_linear_exl3(layer.w13_trellis[e, 1], layer.w13_suh[e, 1], layer.w13_svh[e, 1],
+                                       layer.w13_mcg[e, 1]),
+                "down": make_linear_exl3(layer.w2_trellis[e], layer.w2_suh[e], layer.w2_svh[e], layer.w2_mcg[e]),
+            })
+        layer._exl3_inners = inners
+        if layer.w13_trellis.is_cuda:
+            build_exl3_fused_state(layer, inners)
+
+    def apply(self, layer, x, topk_weights, topk_ids, shared_experts=None, shared_experts_input=None):
+        del shared_experts, shared_experts_input
+        limit = getattr(self.moe, "swiglu_limit", None) or SWIGLU_LIMIT_DEFAULT
+        return apply_exl3_experts(x, topk_ids, topk_weights, layer, limit=float(limit))
+
+
+class Exl3LinearMethod:
+    """EXL3 dense linear with one or more same-input output shards
+    (recipe-lna/vllm_exl3_exl3.py.lna:2310-2853, EXL3 shards only)."""
+
+    def __init__(self, quant_config=None, bits: int | None = None):
+        self.quant_config = quant_config
+        self.bits = int(bits) if bits is not None else int(getattr(quant_config, "bits", 0))
+
+    def create_weights(self, layer, input_size_per_partition: int, output_partition_sizes: list[int],
+                       input_size: int = 0, output_size: int = 0, params_dtype=None, **extra_weight_attrs):
+        del input_size, output_size, params_dtype, extra_weight_attrs
+        k = input_size_per_partition
+        for i, n in enumerate(output_partition_sizes):
+            if k % 16 or n % 16:
+                raise ValueError(f"EXL3 trellis tiles are 16-wide; shard {i}: in={k} out={n}")
+        n_shards = len(output_partition_sizes)
+        total_tiles = sum(n // 16 for n in output_partition_sizes)
+        params = {
+            "trellis": torch.empty(k // 16, total_tiles, self.bits * 16, dtype=torch.int16),
+            "suh": torch.empty(n_shards, k, dtype=torch.float16),
+            "svh": torch.empty(sum(output_partition_sizes), dtype=torch.float16),
+            "mcg": torch.zeros(n_shards, 1, dtype=torch.int32),
+            "mul1": torch.zeros(n_shards, 1, dtype=torch.int32),
+        }
+        for name, t in params.items():
+            layer.register_parameter(name, Parameter(t, requires_grad=False))
+        layer._exl3_linear_n_shards = n_shards
+        layer._exl3_linear_output_partition_sizes = list(output_partition_sizes)
+        layer._exl3_linear_input_size_per_partition = k
+        layer._exl3_linear_bf16_shards = []
+
+    def process_weights_after_loading(self, layer) -> None:
+        sizes = layer._exl3_linear_output_partition_sizes
+        linears, t0, o0 = [], 0, 0
+        for i, n in enumerate(sizes):
+            mcg = layer.mcg[i] if int(layer.mcg[i].item()) == MCG_MARKER_SIGNED_INT32 else None
+            mul1 = layer.mul1[i] if int(layer.mul1[i].item()) == MUL1_MARKER_SIGNED_INT32 else None
+            if mcg is None and mul1 is None and (int(layer.mcg[i].item()) or int(layer.mul1[i].item())):
+                raise RuntimeError(f"EXL3 shard {i}: unknown codebook marker")
+            trellis = layer.trellis[:, t0:t0 + n // 16].contiguous()
+            linears.append(make_linear_exl3(trellis, layer.suh[i], layer.svh[o0:o0 + n], mcg, mul1))
+            t0 += n // 16
+            o0 += n
+        layer._exl3_linears = linears
+
+    def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+        linears = getattr(layer, "_exl3_linears", None)
+        if not linears:
+            raise RuntimeError("EXL3 linear layers were not built after weight load")
+        orig = x.shape
+        x2 = x.reshape(-1, orig[-1])
+        xh = x2.to(torch.float16).contiguous()
+        outs = []
+        for i, lin in enumerate(linears):
+            if lin is None:
+                raise RuntimeError(f"EXL3 linear shard {i} is None")
+            outs.append(lin.forward(xh, {}, out_dtype=torch.float32))
+        y = torch.cat(outs, dim=1) if len(outs) > 1 else outs[0]
+        y = y.to(dtype=x.dtype)
+        if bias is not None:
+            y = y + bias
+        return y.reshape(*orig[:-1], y.shape[-1])

@@ -1,0 +1,303 @@
+"""CPU tests of the host side: the C-ABI library loads and exports every symbol
+include/exl3_amd.h declares, its argument checks answer without a device, and
+the plugin surface's dispatch / routing / loader logic (no kernel launches)."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+import torch
+
+from dsv4_carve_amd import _lib, ops
+from dsv4_carve_amd import vllm_exl3 as V
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "exl3_amd.h")
+
+
+def header_symbols() -> set[str]:
+    text = open(HEADER).read()
+    return set(re.findall(r"^[a-z][\w\s\*]*?\b(exl3_\w+)\s*\(", text, flags=re.M))
+
+
+def test_header_matches_binding_table():
+    assert header_symbols() == set(_lib.EXPORTS)
+    assert set(_lib._SIGS) == set(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {l.split()[-1] for l in out.splitlines() if " T " in l}
+    assert header_symbols() <= exported
+
+
+def test_library_targets_gfx950_only():
+    # the code object bundle names its targets; there is exactly one
+    blob = open(_lib.LIB_PATH, "rb").read()
+    targets = set(re.findall(rb"amdgcn-amd-amdhsa--(gfx\w+)", blob))
+    assert targets == {b"gfx950"}, targets
+
+
+def _err():
+    return _lib.load().exl3_last_error().decode()
+
+
+def test_moe_host_arithmetic_without_device():
+    lib = _lib.load()
+    assert lib.exl3_moe_max_rows() == 16
+    a = lib.exl3_moe_scratch_bytes(4096, 2048, 8)
+    b = lib.exl3_moe_scratch_bytes(4096, 256, 6)
+    assert a > b > 0 and a % 256 == 0
+    assert lib.exl3_moe_scratch_bytes(4000, 2048, 8) == -1 and "multiples of 256" in _err()
+    assert lib.exl3_moe_scratch_bytes(4096, 2048, 9) == -1 and "topk" in _err()
+
+
+def _moe_call(**kw):
+    lib = _lib.load()
+    one = ctypes.c_void_p(16)
+    args = dict(x=one, x_kind=0, out=one, out_kind=2, m=1, hidden=512, intermediate=256, n_experts=4, topk=2,
+                tabs=[one] * 9, ids=one, w=one, ebits=None, bits=3, mask=0, cb=1, limit=10.0, scratch=one,
+                scratch_bytes=1 << 30, stream=None)
+    args.update(kw)
+    return lib.exl3_moe_decode(args["x"], args["x_kind"], args["out"], args["out_kind"], args["m"], args["hidden"],
+                               args["intermediate"], args["n_experts"], args["topk"], *args["tabs"], args["ids"],
+                               args["w"], args["ebits"], args["bits"], args["mask"], args["cb"], args["limit"],
+                               args["scratch"], args["scratch_bytes"], args["stream"])
+
+
+@pytest.mark.parametrize("kw,msg", [
+    ({"x": None}, "null pointer"),
+    ({"tabs": [ctypes.c_void_p(16)] * 8 + [None]}, "null pointer table"),
+    ({"x_kind": 2}, "fp16 or bf16"),
+    ({"out_kind": 3}, "fp16, bf16 or fp32"),
+    ({"m": 0}, "row count"),
+    ({"m": 17}, "row count"),
+    ({"hidden": 500}, "multiples of 256"),
+    ({"intermediate": 128}, "multiples of 256"),
+    ({"n_experts": 0}, "expert count"),
+    ({"topk": 9}, "topk"),
+    ({"limit": 0.0}, "SwiGLU limit"),
+    ({"limit": float("inf")}, "SwiGLU limit"),
+    ({"limit": float("nan")}, "SwiGLU limit"),
+    ({"cb": 3}, "codebook"),
+    ({"bits": 0}, "bits must be in 1..8"),
+    ({"bits": 9}, "bits must be in 1..8"),
+    ({"ebits": ctypes.c_void_p(16), "mask": 1}, "bits_mask"),
+    ({"ebits": ctypes.c_void_p(16), "mask": 0}, "bits_mask"),
+    ({"scratch_bytes": 16}, "scratch too small"),
+])
+def test_moe_argument_errors_without_device(kw, msg):
+    assert _moe_call(**kw) == -1
+    assert msg in _err()
+
+
+@pytest.mark.parametrize("k,n,cb,kind,msg", [
+    (100, 256, 1, 2, "k must be a positive multiple of 128"),
+    (256, 100, 1, 2, "n must be a positive multiple of 128"),
+    (256, 256, 5, 2, "codebook"),
+    (256, 256, 1, 7, "c_kind"),
+])
+def test_gemm_argument_errors_without_device(k, n, cb, kind, msg):
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    assert lib.exl3_gemm(p, 1, k, p, n, 3, cb, p, p, p, kind, p, 1 << 30, None) == -1
+    assert msg in _err()
+
+
+def test_dequant_argument_errors_without_device():
+    lib = _lib.load()
+    p = ctypes.c_void_p(16)
+    assert lib.exl3_dequant(p, 24, 32, 3, 1, None, None, p, None) == -1 and "multiples of 16" in _err()
+    assert lib.exl3_dequant(p, 32, 32, 9, 1, None, None, p, None) == -1 and "bits" in _err()
+    assert lib.exl3_dequant(p, 32, 32, 3, 1, p, None, p, None) == -1 and "both" in _err()
+    assert lib.exl3_dequant(p, 32, 32, 3, 1, p, p, p, None) == -1 and "128" in _err()
+
+
+def test_check_raises_library_message():
+    lib = _lib.load()
+    assert lib.exl3_moe_scratch_bytes(1, 1, 1) == -1
+    with pytest.raises(_lib.Exl3Error, match="multiples of 256"):
+        _lib.check(-1)
+
+
+# ---------------------------------------------------------------- no CPU fallback
+
+
+def test_ops_refuse_cpu_tensors():
+    t = torch.zeros((8, 8, 48), dtype=torch.int16)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        ops.reconstruct_weight(t)
+    x = torch.zeros((1, 128), dtype=torch.float16)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        ops.gemm(x, t, torch.ones(128, dtype=torch.float16), torch.ones(128, dtype=torch.float16))
+
+
+# ---------------------------------------------------------------- plugin host logic
+
+
+def test_map_topk_to_local_without_map():
+    ids = torch.tensor([[0, 3, -1], [7, 2, 8]])
+    got = V.map_topk_to_local(ids, 8, None).reshape(ids.shape)
+    assert got.tolist() == [[0, 3, 8], [7, 2, 8]]
+
+
+def test_map_topk_to_local_with_expert_map():
+    emap = torch.tensor([-1, 0, 1, -1, 2, 3], dtype=torch.long)     # 6 global -> 4 local
+    ids = torch.tensor([[1, 4, 0, 5], [6, -2, 2, 3]])
+    got = V.map_topk_to_local(ids, 4, emap).reshape(ids.shape)
+    assert got.tolist() == [[0, 2, 4, 3], [4, 4, 1, 4]]
+    with pytest.raises(RuntimeError, match="not pinned"):
+        V.map_topk_to_local(ids, 4, emap.to(torch.int32))
+    assert V.map_topk_to_local(ids, 4, torch.empty(0, dtype=torch.long)).tolist() == [4] * 8
+
+
+def test_pin_expert_map():
+    class L:
+        expert_map = torch.tensor([1, 0], dtype=torch.int32)
+
+    layer = L()
+    m = V.pin_exl3_expert_map(layer, torch.device("cpu"))
+    assert m.dtype == torch.long and layer.expert_map is m
+    assert V.pin_exl3_expert_map(object(), torch.device("cpu")) is None
+
+
+@pytest.mark.parametrize("env,want", [(None, "lna2"), ("auto", "lna2"), ("LNA2", "lna2"), ("loop", "loop"),
+                                      ("exllamav3", "lna2"), ("bogus", "lna2")])
+def test_backend_selection(monkeypatch, env, want):
+    if env is None:
+        monkeypatch.delenv("VLLM_EXL3_MOE_KERNEL", raising=False)
+    else:
+        monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", env)
+    assert V.get_moe_kernel_backend() == want
+
+
+def test_strict_levels(monkeypatch):
+    V._LNA2_REJECT_LOGGED.clear()
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "0")
+    V._lna2_log_reject("shape a")
+    V._lna2_log_reject("ready b", not_ready=True)
+    assert V.moe_kernel_declined_reasons() == ["ready b", "shape a"]
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "1")
+    V._lna2_log_reject("shape a")
+    with pytest.raises(RuntimeError, match="STRICT=1"):
+        V._lna2_log_reject("ready b", not_ready=True)
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "2")
+    with pytest.raises(RuntimeError, match="STRICT=2"):
+        V._lna2_log_reject("shape a")
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "x")
+    assert V.moe_kernel_strict() == 0
+    V._LNA2_REJECT_LOGGED.clear()
+
+
+def test_unpack_bf():
+    rng = np.random.default_rng(1)
+    words = rng.integers(0, 1 << 16, 8, dtype=np.uint16)
+    got = V.LinearEXL3.unpack_bf(torch.from_numpy(words.view(np.int16))).numpy()
+    want = np.array([-1.0 if (int(w) >> i) & 1 else 1.0 for w in words for i in range(16)], np.float16)
+    assert np.array_equal(got, want)
+
+
+def test_linear_constructor_checks():
+    t = torch.zeros((8, 8, 48), dtype=torch.int16)
+    h = torch.ones(128, dtype=torch.float16)
+    with pytest.raises(AssertionError, match="scale"):
+        V.LinearEXL3(None, 128, 128, scale=torch.ones(1), suh=h, svh=h, trellis=t)
+    with pytest.raises(AssertionError, match="trellis is wrong datatype"):
+        V.LinearEXL3(None, 128, 128, suh=h, svh=h, trellis=t.float())
+    with pytest.raises(AssertionError, match="suh"):
+        V.LinearEXL3(None, 128, 128, suh=h.float(), svh=h, trellis=t)
+    lin = V.LinearEXL3(None, 128, 128, suh=h, svh=h, trellis=t, mcg=torch.tensor([V.MCG_MARKER_SIGNED_INT32]))
+    assert lin.K == 3 and lin.mcg and not lin.mul1 and lin.codebook == ops.CB_MCG
+    with pytest.raises(AssertionError, match="non-contiguous"):
+        lin.forward(torch.zeros((128, 2), dtype=torch.float16).t(), {})
+    with pytest.raises(RuntimeError, match="Specified both"):
+        V.LinearEXL3(None, 128, 128, suh=h, svh=h, trellis=t, mcg=torch.ones(1), mul1=torch.ones(1))
+
+
+def test_tp_sharding_of_packed_tensors():
+    t = torch.arange(4 * 8 * 32, dtype=torch.int16).reshape(4, 8, 32)
+    col = V.shard_exl3_col(t, "trellis", 1, 2)
+    assert torch.equal(col, t[:, 4:])
+    row = V.shard_exl3_row(t, "trellis", 1, 4)
+    assert torch.equal(row, t[1:2])
+    v = torch.arange(8, dtype=torch.float16)
+    assert torch.equal(V.shard_exl3_col(v, "svh", 0, 2), v[:4])
+    assert torch.equal(V.shard_exl3_col(v, "suh", 0, 2), v)
+    assert torch.equal(V.shard_exl3_row(v, "suh", 1, 2), v[4:])
+    with pytest.raises(ValueError):
+        V.shard_exl3_col(v, "svh", 0, 3)
+    assert V._suffix_from_mapped_name("layers.3.ffn.experts.7.w1.trellis") == "trellis"
+    assert V._suffix_from_mapped_name("experts.w13_svh") == "svh"
+    with pytest.raises(ValueError):
+        V._suffix_from_mapped_name("experts.w13_weight")
+
+
+def _moe_layer_cpu(E=2, H=256, I=256, bits=2):
+    layer = torch.nn.Module()
+    meth = V.Exl3MoEMethod(bits=bits)
+    meth.create_weights(layer, E, H, I)
+    return layer, meth
+
+
+def test_moe_method_create_and_load():
+    layer, meth = _moe_layer_cpu()
+    assert tuple(layer.w13_trellis.shape) == (2, 2, 16, 16, 32)
+    assert tuple(layer.w2_trellis.shape) == (2, 16, 16, 32)
+    tr = torch.ones((16, 16, 32), dtype=torch.int16)
+    layer.w13_trellis.weight_loader(layer.w13_trellis, tr * 3, "experts.1.w3.trellis", "w3", 1)
+    assert int(layer.w13_trellis[1, 1].sum()) == 3 * tr.numel() and int(layer.w13_trellis[1, 0].abs().sum()) >= 0
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        meth._load_exl3(layer.w2_trellis, tr[:8], "experts.0.w2.trellis", "w2", 0)
+    with pytest.raises(ValueError, match="shard_id"):
+        meth._load_exl3(layer.w2_trellis, tr, "experts.0.w2.trellis", "w4", 0)
+    with pytest.raises(ValueError):
+        V.Exl3MoEMethod(bits=2).create_weights(torch.nn.Module(), 2, 250, 256)
+
+
+def test_moe_method_rejects_wrong_marker():
+    layer, meth = _moe_layer_cpu()
+    layer.w13_mcg.data.fill_(V.MCG_MARKER_SIGNED_INT32)
+    layer.w2_mcg.data.fill_(V.MUL1_MARKER_SIGNED_INT32)
+    with pytest.raises(RuntimeError, match="marker"):
+        meth.process_weights_after_loading(layer)
+
+
+def test_moe_apply_has_no_cpu_fallback():
+    layer, meth = _moe_layer_cpu()
+    for p in (layer.w13_trellis, layer.w2_trellis):
+        p.data.zero_()
+    for p in (layer.w13_suh, layer.w13_svh, layer.w2_suh, layer.w2_svh):
+        p.data.fill_(1.0)
+    layer.w13_mcg.data.fill_(V.MCG_MARKER_SIGNED_INT32)
+    layer.w2_mcg.data.fill_(V.MCG_MARKER_SIGNED_INT32)
+    meth.process_weights_after_loading(layer)
+    assert len(layer._exl3_inners) == 2 and layer._exl3_inners[0]["down"].in_features == 256
+    x = torch.zeros((1, 256), dtype=torch.float16)
+    with pytest.raises((NotImplementedError, RuntimeError)):
+        meth.apply(layer, x, torch.ones((1, 1)), torch.zeros((1, 1), dtype=torch.long))
+    with pytest.raises(RuntimeError, match="not built"):
+        V.apply_exl3_experts(x, torch.zeros((1, 1), dtype=torch.long), torch.ones((1, 1)), torch.nn.Module())
+
+
+def test_linear_method_shards():
+    layer = torch.nn.Module()
+    meth = V.Exl3LinearMethod(bits=2)
+    meth.create_weights(layer, 128, [256, 128], 128, 384)
+    assert tuple(layer.trellis.shape) == (8, 24, 32) and tuple(layer.suh.shape) == (2, 128)
+    layer.mcg.data.fill_(V.MCG_MARKER_SIGNED_INT32)
+    layer.trellis.data.copy_(torch.arange(layer.trellis.numel(), dtype=torch.int32).reshape(8, 24, 32).to(torch.int16))
+    meth.process_weights_after_loading(layer)
+    a, b = layer._exl3_linears
+    assert (a.out_features, b.out_features) == (256, 128)
+    assert torch.equal(b.trellis, layer.trellis[:, 16:]) and b.trellis.is_contiguous()
+    with pytest.raises(RuntimeError, match="not built"):
+        meth.apply(torch.nn.Module(), torch.zeros(1, 128))
