@@ -63,8 +63,10 @@ class DeviceLayer:
         self.mask = sum(1 << b for b in set(self.bits))
 
 
-def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False):
-    """Returns (us per step, mean algorithmic bytes per step)."""
+def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, eager=False):
+    """Returns (us per step, mean algorithmic bytes per step).  The K steps are
+    replayed from one HIP graph; `eager` launches them one by one instead (for
+    counter collection, which sees every dispatch)."""
     import torch
     from dsv4_carve_amd import ops, synth
 
@@ -83,6 +85,16 @@ def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False):
     for i in range(warmup):
         launch(i)
     torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    nbytes = float(np.mean([step_bytes(pool[i % POOL][0], layer.bits, layer.hidden, layer.inter)
+                            for i in range(steps)]))
+    if eager:
+        start.record()
+        for i in range(steps):
+            launch(i)
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1000.0 / steps, nbytes
     stream = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=stream):
@@ -91,26 +103,28 @@ def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False):
     torch.cuda.synchronize()
     graph.replay()                       # one untimed replay (graph upload)
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # the replay runs on the current stream, where the events are recorded
     start.record()
     graph.replay()
     end.record()
     torch.cuda.synchronize()
-    us = start.elapsed_time(end) * 1000.0 / steps
-    nbytes = float(np.mean([step_bytes(pool[i % POOL][0], layer.bits, layer.hidden, layer.inter)
-                            for i in range(steps)]))
-    return us, nbytes
+    return start.elapsed_time(end) * 1000.0 / steps, nbytes
 
 
 def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> dict:
-    """CPU restatement timed on one 3-bit and one 2-bit expert, scaled to the
-    mean set of distinct experts per step at this row count."""
+    """CPU restatement timed on four 3-bit and four 2-bit experts of the layer,
+    scaled to the mean set of distinct experts per step at this row count."""
     import torch
     from dsv4_carve_amd import synth
     from oracle import cpu_baseline as CB
 
-    t3 = CB.time_expert(synth.expert(0, HIDDEN, INTER, 3, seed), rows)
-    t2 = CB.time_expert(synth.expert(200, HIDDEN, INTER, 2, seed), rows)
+    def timed(e, b):
+        t = CB.time_expert(synth.expert(e, HIDDEN, INTER, b, seed), rows)
+        print(f"[bench] cpu baseline: expert {e} ({b}-bit) {t * 1e3:.0f} ms", file=sys.stderr, flush=True)
+        return t
+
+    t3 = float(np.mean([timed(e, 3) for e in range(4)]))
+    t2 = float(np.mean([timed(e, 2) for e in range(128, 132)]))
     n3 = n2 = 0.0
     for ids in us_ids:
         act = {int(e) for e in ids.reshape(-1)}
@@ -123,9 +137,10 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
         "unit": "us/layer",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"one 3-bit and one 2-bit expert ({rows} rows, gate+up+down, dequant per call + fp32 "
-                   f"matmul, median of 3 after 1 warm-up: {t3 * 1e3:.0f} ms and {t2 * 1e3:.0f} ms), scaled by the "
-                   f"mean distinct experts per step ({n3:.1f} 3-bit + {n2:.1f} 2-bit)"),
+        "sample": (f"experts 0-3 (3-bit) and 128-131 (2-bit) of the layer, {rows} rows each: gate+up+down with "
+                   f"per-call dequant + fp32 matmul (the reference CPU path), median of 3 after 1 warm-up per "
+                   f"expert; mean {t3 * 1e3:.0f} ms (3-bit) and {t2 * 1e3:.0f} ms (2-bit) per expert, scaled by "
+                   f"the mean distinct experts per step ({n3:.1f} 3-bit + {n2:.1f} 2-bit)"),
     }
 
 
@@ -137,6 +152,9 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline measurement")
+    ap.add_argument("--eager", action="store_true", help="launch the timed steps one by one (no graph)")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="end with one device-to-device copy of this many MiB (HBM counter calibration)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
@@ -154,7 +172,7 @@ def main() -> int:
     layer = DeviceLayer(dev, EXPERTS, HIDDEN, INTER, bits, seed=1)
     print(f"[bench] layer built in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
 
-    us, nbytes = time_layer(layer, dev, a.rows, TOPK, a.steps, a.warmup, seed=a.rows)
+    us, nbytes = time_layer(layer, dev, a.rows, TOPK, a.steps, a.warmup, seed=a.rows, eager=a.eager)
     gbs = nbytes / (us * 1e-6) / 1e9
     print(f"[bench] rows={a.rows}: {us:.1f} us/layer, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
@@ -178,16 +196,25 @@ def main() -> int:
             for m in (1, 2, 4, 8, 16):
                 u, b = time_layer(tl, dev, m, 6, 40, 3, seed=100 + m)
                 tp[f"K{kb}"][str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1)}
+                print(f"[bench] tp8 slice K{kb} m={m}: {tp[f'K{kb}'][str(m)]}", file=sys.stderr, flush=True)
             del tl
             torch.cuda.empty_cache()
         extra["tp8_slice_h4096_i256_top6"] = tp
-        print(f"[bench] tp8 slice: {tp}", file=sys.stderr, flush=True)
 
     cpu = None
     if not a.no_cpu:
         pool_ids = [synth.routing(a.rows, EXPERTS, TOPK, seed=a.rows * 1000 + i)[0] for i in range(POOL)]
         cpu = cpu_baseline(a.rows, bits, seed=1, us_ids=pool_ids)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+
+    if a.calib_copy_mib:
+        src = torch.ones(a.calib_copy_mib << 18, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] calibration copy: {a.calib_copy_mib} MiB read + {a.calib_copy_mib} MiB written",
+              file=sys.stderr, flush=True)
 
     traffic = None
     prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_c2_m16_traffic.json")

@@ -11,9 +11,12 @@
 //     block) sums them in fixed order, applies the output Hadamard + svh, the
 //     clamped SwiGLU, the down projection's suh + input Hadamard, stores the
 //     fp16 down input and publishes an epoch flag.
-//   * A down item spins on the flags of the column blocks it reads.  Those were
-//     ticketed earlier and never wait, so every wait ends whatever the number
-//     of resident waves.
+//   * A down item spins on the flags of the column blocks it reads; a gather
+//     item on the flag of its H-block.  What it waits for has a smaller ticket,
+//     and every ticket comes from the one counter, drawn by a running wave: a
+//     smaller ticket is held by a running wave or already done, and those never
+//     wait on larger ones.  So every wait ends whatever the number of resident
+//     waves (other kernels may hold CUs; no co-residency is assumed).
 //   * down items write partials; the last arriver of a (group, H-block) applies
 //     the output Hadamard + svh; the last group to finish an H-block gathers the
 //     block of `out` in top-k slot order (fp32) and casts once.
@@ -33,6 +36,7 @@ constexpr int MAX_M = 16;
 constexpr int MAX_TOPK = 8;
 constexpr int MAX_SLOTS = MAX_M * MAX_TOPK;   // also the bound on groups and pairs
 constexpr int MAX_EXPERTS = 2048;             // route-plan bitmask capacity
+constexpr int MAX_BLOCKS = 64;                // hidden/256 and intermediate/256 (both <= 16384)
 constexpr int NSTEP_CAP = 8;
 
 // Steps (64 k-rows each) per item: a power of two in 2..8 dividing k/64.  The
@@ -64,13 +68,18 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     L.SA = H / STEP_K / L.stepsA;
     L.SB = I / STEP_K / L.stepsB;
     const int64_t P = (int64_t)MAX_M * topk;      // max pairs = max groups
+    // The control words sit at fixed offsets with fixed strides whatever the
+    // geometry, so one scratch buffer can serve layers of different shapes:
+    // every counter is back at zero after a launch and every flag holds an
+    // older epoch, whichever shape used the slot last.
     int64_t o = 0;
     L.ctrl = o;  o += 256;
-    L.cntA = o;  o = al(o + P * L.nI * 4);
-    L.doneA = o; o = al(o + P * L.nI * 4);
-    L.cntB = o;  o = al(o + P * L.nH * 4);
-    L.cntG = o;  o = al(o + (int64_t)L.nH * 4);
-    L.doneB = o; o = al(o + (int64_t)L.nH * 4);
+    L.cntA = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
+    L.doneA = o; o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
+    L.cntB = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
+    L.cntG = o;  o += (int64_t)MAX_BLOCKS * 4;
+    L.doneB = o; o += (int64_t)MAX_BLOCKS * 4;
+    o = al(o);
     L.PA = o;    o = al(o + P * 2 * L.SA * I * 4);
     L.DI = o;    o = al(o + P * I * 2);
     L.PB = o;    o = al(o + P * L.SB * H * 4);
@@ -290,7 +299,7 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     store_partials(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, ld, R, COLS,
                    reinterpret_cast<float*>(xa));
     publish_fence();
-    int* cnt = at<int>(P.scratch, L.cntA) + g * L.nI + cb;
+    int* cnt = at<int>(P.scratch, L.cntA) + g * MAX_BLOCKS + cb;
     const bool last = wave_atomic_add(cnt, 1) == 2 * L.SA - 1;
     tr(EV_A_END, last);
     if (!last) return;
@@ -330,7 +339,7 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     reset_counter(cnt);
     publish_fence();
     if (lane == 0)
-        __hip_atomic_store(at<int>(P.scratch, L.doneA) + g * L.nI + cb, epoch + 1, __ATOMIC_RELAXED,
+        __hip_atomic_store(at<int>(P.scratch, L.doneA) + g * MAX_BLOCKS + cb, epoch + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     tr(EV_EPI_A_END);
 }
@@ -351,7 +360,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     load_tile<B>(first, tp);
 
     // wait for the gate/up column blocks this chunk reads
-    int* doneA = at<int>(P.scratch, L.doneA) + g * L.nI;
+    int* doneA = at<int>(P.scratch, L.doneA) + g * MAX_BLOCKS;
     for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c) wait_flag(doneA + c, epoch + 1);
     tr(EV_B_WAITED);
 
@@ -367,7 +376,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS,
                    reinterpret_cast<float*>(xa));
     publish_fence();
-    int* cnt = at<int>(P.scratch, L.cntB) + g * L.nH + cb;
+    int* cnt = at<int>(P.scratch, L.cntB) + g * MAX_BLOCKS + cb;
     const bool last = wave_atomic_add(cnt, 1) == L.SB - 1;
     tr(EV_B_END, last);
     if (!last) return;
@@ -501,7 +510,7 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
     // Ticket order: gate/up items, down items, gather items.  A wave's first
     // ticket is its own index (no burst on the counter at launch); later ones
     // come from the counter, offset by the grid size.
-    for (int t = blockIdx.x; t < total; t = (int)gridDim.x + wave_atomic_add(&ctrl->ticket, 1)) {
+    for (int t = wave_atomic_add(&ctrl->ticket, 1); t < total; t = wave_atomic_add(&ctrl->ticket, 1)) {
         if (t < nA) {
             tr(EV_A_BEGIN, t);
             item_a<MASK, CB>(P, pl, xa, t, epoch, tr);

@@ -56,6 +56,8 @@ int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t top
     clear_error();
     if (hidden <= 0 || hidden % COLS || intermediate <= 0 || intermediate % COLS)
         return fail("hidden and intermediate must be positive multiples of 256");
+    if (hidden > COLS * MAX_BLOCKS || intermediate > COLS * MAX_BLOCKS)
+        return fail("hidden and intermediate must be at most 16384");
     if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..8");
     return layout((int)hidden, (int)intermediate, (int)topk).total + trace_bytes();
 }
@@ -91,6 +93,8 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
     if (m < 1 || m > MAX_M) return fail("row count out of range (1 <= m <= exl3_moe_max_rows())");
     if (hidden <= 0 || hidden % COLS || intermediate <= 0 || intermediate % COLS)
         return fail("hidden and intermediate must be positive multiples of 256");
+    if (hidden > COLS * MAX_BLOCKS || intermediate > COLS * MAX_BLOCKS)
+        return fail("hidden and intermediate must be at most 16384");
     if (n_experts < 1 || n_experts > MAX_EXPERTS) return fail("expert count out of range (1..2048)");
     if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..8");
     if (!(swiglu_limit > 0.0f) || !isfinite(swiglu_limit)) return fail("requires a finite positive SwiGLU limit");

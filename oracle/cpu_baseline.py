@@ -70,9 +70,16 @@ def expert_rows(x16: np.ndarray, ex: dict, limit: float, lut: torch.Tensor) -> t
     return linear(act.half().float(), ex["down"], ex["bits"], lut)
 
 
+def threads() -> int:
+    """Host threads for the baseline: every core, capped by OMP_NUM_THREADS when set."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    return min(n, int(env)) if env and env.isdigit() and int(env) > 0 else n
+
+
 def time_expert(ex: dict, rows: int, reps: int = 3, limit: float = 10.0) -> float:
     """Median seconds for one expert's gate+up+down on `rows` rows (dequant each call)."""
-    torch.set_num_threads(os.cpu_count() or 1)
+    torch.set_num_threads(threads())
     lut = torch.from_numpy(O.codebook_lut(O.CB_MCG).view(np.float16).copy())
     x = np.random.default_rng(0).standard_normal((rows, ex["gate"]["suh"].size)).astype(np.float16)
     expert_rows(x, ex, limit, lut)                 # warm-up

@@ -48,15 +48,17 @@ class Layer:
         self.mask = sum(1 << b for b in set(self.bits))
         self.cache = {}
 
-    def run(self, x, ids, w, out_dtype=None, limit=LIMIT):
+    def run(self, x, ids, w, out_dtype=None, limit=LIMIT, scratch=None, uniform=False):
+        """uniform: pass the one bit width as `bits` instead of the per-expert table."""
         import torch
         from dsv4_carve_amd import ops
 
         dev = self.ebits.device
         xd = x if isinstance(x, torch.Tensor) else to_dev(x, dev)
         out = torch.empty(xd.shape, dtype=out_dtype or torch.float32, device=dev)
+        widths = dict(bits=self.bits[0]) if uniform else dict(expert_bits=self.ebits, bits_mask=self.mask)
         ops.moe_decode(xd, out, self.tables, to_dev(ids.astype(np.int32), dev), to_dev(w.astype(np.float32), dev),
-                       intermediate=self.I, expert_bits=self.ebits, bits_mask=self.mask, swiglu_limit=limit)
+                       intermediate=self.I, swiglu_limit=limit, scratch=scratch, **widths)
         return out
 
     def ref(self, x16, ids, w, limit=LIMIT):
@@ -268,3 +270,48 @@ def test_c2_size_independent_properties(c2, dev):
     for r in (0, 9, 15):
         single = c2.run(x[r:r + 1], ids[r:r + 1], w[r:r + 1])[0].cpu().numpy()
         assert rel_l2(single, a[r].cpu().numpy()) < 1e-4, f"row {r} differs when computed alone"
+
+
+# ---------------------------------------------------------------- one scratch, several shapes
+
+
+def test_scratch_shared_across_geometries(dev):
+    """One zeroed scratch serves layers of different (hidden, intermediate,
+    top-k) in any order: the control words sit at fixed offsets, so a smaller
+    layer after a larger one finds its counters at zero rather than on the
+    larger layer's partial sums."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    big = Layer(dev, 24, 1024, 768, [3, 2] * 12, seed=31)
+    small = Layer(dev, 12, 512, 256, [2, 3, 4] * 4, seed=32)
+    scratch = torch.zeros(ops.moe_scratch_bytes(1024, 768, 8), dtype=torch.uint8, device=dev)
+    assert scratch.numel() >= ops.moe_scratch_bytes(512, 256, 6)
+    for it in range(2):
+        for layer, topk, m in ((big, 8, 16), (small, 6, 16), (small, 6, 3), (big, 8, 5)):
+            print(f"shared scratch it={it} H={layer.H} I={layer.I} top{topk} m={m}", flush=True)
+            ids, w = synth.routing(m, layer.E, topk, seed=300 + 10 * it + m)
+            x = synth.activations(m, layer.H, seed=301 + it)
+            got = layer.run(x, ids, w, scratch=scratch).cpu().numpy()
+            assert_close(got, layer.ref(x, ids, w), what=f"shared scratch H={layer.H} m={m}")
+
+
+# ---------------------------------------------------------------- the reference kernel's own geometry
+
+
+@pytest.fixture(scope="module")
+def tp_slice(dev):
+    """One GPU's share of the layer under 8-way tensor parallelism, the lna2
+    kernel's fixed geometry: 256 experts, hidden 4096, intermediate 256, top-6,
+    one width for all experts."""
+    return {kb: Layer(dev, 256, 4096, 256, [kb] * 256, seed=40 + kb) for kb in (2, 3)}
+
+
+@pytest.mark.parametrize("kb,m,uniform", [(2, 16, False), (2, 1, True), (3, 4, True), (3, 9, False)])
+def test_tp_slice_against_oracle(tp_slice, kb, m, uniform):
+    print(f"tp slice K{kb} m={m} uniform={uniform}", flush=True)
+    layer = tp_slice[kb]
+    ids, w = synth.routing(m, 256, 6, seed=500 + 7 * kb + m)
+    x = synth.activations(m, 4096, seed=501 + m)
+    got = layer.run(x, ids, w, uniform=uniform).cpu().numpy()
+    assert_close(got, layer.ref(x, ids, w), what=f"tp slice K{kb} m={m}")
