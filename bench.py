@@ -111,6 +111,168 @@ def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, 
     return start.elapsed_time(end) * 1000.0 / steps, nbytes
 
 
+DENSE_SHAPES = ((4096, 4096), (4096, 1536), (1536, 4096), (4096, 12288))
+DENSE_BITS = (2, 3, 4, 6)
+DENSE_ROWS = (1, 2, 4, 8, 16)
+
+
+def dense_bytes(k: int, n: int, bits: int, rows: int) -> int:
+    """Algorithmic bytes of one dense call: trellis + suh + svh, x in, fp16 y out."""
+    return k * n * bits // 8 + 2 * (k + n) + rows * k * 2 + rows * n * 2
+
+
+def time_dense(dev, k, n, bits, rows_list, steps=40):
+    """us per call of the trellis-decode GEMV for each row count, cold (cycling
+    through > 512 MB of distinct weight copies, so no copy is still in the
+    256 MB MALL when reused) and warm (one copy).  Weights are seeded on the
+    device: this measures speed only (parity is the tests' job)."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(k * 131 + n * 7 + bits)
+    wbytes = k * n * bits // 8
+    copies = max(2, -(-(600 << 20) // wbytes))
+    pool = [torch.randint(-32768, 32767, (k // 16, n // 16, 16 * bits), dtype=torch.int16, device=dev,
+                          generator=g) for _ in range(copies)]
+    suh = (torch.randint(0, 2, (k,), device=dev, generator=g) * 2 - 1).to(torch.float16)
+    svh = ((torch.randint(0, 2, (n,), device=dev, generator=g) * 2 - 1) *
+           (torch.rand(n, device=dev, generator=g) * 1.5 + 0.5) / k ** 0.5).to(torch.float16)
+    res = {}
+    for rows in rows_list:
+        x = torch.randn((rows, k), device=dev, generator=g).to(torch.float16)
+        y = torch.empty((rows, n), dtype=torch.float16, device=dev)
+        ops.prepare_gemm(dev, rows, k, n)
+        out = {}
+        for mode, order in (("cold", [i % copies for i in range(steps)]), ("warm", [0] * steps)):
+            for i in order[:3]:
+                ops.gemm_into(x, pool[i], suh, svh, y)
+            torch.cuda.synchronize()
+            stream = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in order:
+                    ops.gemm_into(x, pool[i], suh, svh, y)
+            graph.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            out[mode] = a.elapsed_time(b) * 1000.0 / steps
+        nb = dense_bytes(k, n, bits, rows)
+        res[str(rows)] = {"us": round(out["cold"], 2), "GBps": round(nb / (out["cold"] * 1e-6) / 1e9, 1),
+                          "warm_us": round(out["warm"], 2)}
+    del pool
+    torch.cuda.empty_cache()
+    return res
+
+
+C3_LAYERS = 43
+
+
+class StackLayer:
+    """One decode MoE block of the 43-layer stack: the 256 routed experts (3-bit
+    then 2-bit halves) plus a 6-bit shared expert (4096 -> 2x2048 -> 4096) as
+    expert 256, whose slot every row gets with weight 1.  Weights are seeded on
+    the device (speed only; parity is the tests' job)."""
+
+    def __init__(self, dev, seed):
+        import torch
+        from dsv4_carve_amd.ops import MOE_TABLE_KEYS
+
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+        H, I = HIDDEN, INTER
+        self.bits = synth_bits = [3] * (EXPERTS // 2) + [2] * (EXPERTS // 2) + [6]
+        words = {b: H * I * b // 16 for b in set(synth_bits)}
+        self.keep = []
+        tr = {}
+        for b in sorted(set(synth_bits)):
+            n_e = synth_bits.count(b)
+            t = torch.randint(-32768, 32767, (n_e, 3, words[b]), dtype=torch.int16, device=dev, generator=g)
+            self.keep.append(t)
+            tr[b] = t
+        n = len(synth_bits)
+        vh = ((torch.randint(0, 2, (n, 3, H), device=dev, generator=g) * 2 - 1).to(torch.float16) / 64)
+        vi = ((torch.randint(0, 2, (n, 3, I), device=dev, generator=g) * 2 - 1).to(torch.float16) / 45)
+        self.keep += [vh, vi]
+        idx = {b: 0 for b in tr}
+        cols = {k: [] for k in MOE_TABLE_KEYS}
+        for e, b in enumerate(synth_bits):
+            j = idx[b]
+            idx[b] += 1
+            base = tr[b][j]
+            for p, proj in enumerate(("gate", "up", "down")):
+                cols[f"{proj}_trellis"].append(int(base[p].data_ptr()))
+            cols["gate_suh"].append(int(vh[e, 0].data_ptr()))
+            cols["up_suh"].append(int(vh[e, 1].data_ptr()))
+            cols["down_svh"].append(int(vh[e, 2].data_ptr()))
+            cols["gate_svh"].append(int(vi[e, 0].data_ptr()))
+            cols["up_svh"].append(int(vi[e, 1].data_ptr()))
+            cols["down_suh"].append(int(vi[e, 2].data_ptr()))
+        self.tables = {k: torch.tensor(v, dtype=torch.int64, device=dev) for k, v in cols.items()}
+        self.ebits = torch.tensor(synth_bits, dtype=torch.int8, device=dev)
+        self.mask = sum(1 << b for b in set(synth_bits))
+
+
+def time_stack(dev, rows, steps, warmup):
+    """us per decode step of C3_LAYERS routed+shared MoE blocks (one launch per
+    block, each block's output is the next block's input), with independent
+    routing per layer and step; returns (us per step, algorithmic bytes per step)."""
+    import torch
+    from dsv4_carve_amd import ops, synth
+
+    layers = []
+    for l in range(C3_LAYERS):
+        layers.append(StackLayer(dev, 9000 + l))
+        if l % 10 == 9:
+            torch.cuda.synchronize()
+            print(f"[bench] stack: {l + 1} layers built", file=sys.stderr, flush=True)
+    torch.cuda.synchronize()
+    shared = EXPERTS
+    pools, nbytes = [], 0.0
+    for l in range(C3_LAYERS):
+        pl = []
+        for i in range(4):
+            ids, w = synth.routing(rows, EXPERTS, TOPK, seed=70000 + 97 * l + i)
+            ids = np.concatenate([ids, np.full((rows, 1), shared, np.int32)], axis=1)
+            w = np.concatenate([w, np.ones((rows, 1), np.float32)], axis=1)
+            pl.append((torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev)))
+            nbytes += step_bytes(ids, layers[l].bits, HIDDEN, INTER) / 4
+        pools.append(pl)
+    acts = [torch.from_numpy(synth.activations(rows, HIDDEN, seed=5)).to(dev)]
+    acts += [torch.empty((rows, HIDDEN), dtype=torch.float16, device=dev) for _ in range(C3_LAYERS)]
+    scratch = ops.moe_scratch(dev, HIDDEN, INTER, TOPK + 1)
+
+    def step(i):
+        for l in range(C3_LAYERS):
+            ids, w = pools[l][i % 4]
+            ops.moe_decode(acts[l], acts[l + 1], layers[l].tables, ids, w, intermediate=INTER,
+                           expert_bits=layers[l].ebits, bits_mask=layers[l].mask, scratch=scratch)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            step(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / steps
+    del layers, graph
+    torch.cuda.empty_cache()
+    return us, nbytes
+
+
 def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> dict:
     """CPU restatement timed on four 3-bit and four 2-bit experts of the layer,
     scaled to the mean set of distinct experts per step at this row count."""
@@ -200,6 +362,29 @@ def main() -> int:
             del tl
             torch.cuda.empty_cache()
         extra["tp8_slice_h4096_i256_top6"] = tp
+
+    if not a.no_extra:
+        us3, b3 = time_stack(dev, 16, 4, 1)
+        extra["stack_43_layers_routed_plus_shared_rows16"] = {
+            "us_per_step": round(us3, 1), "GBps": round(b3 / (us3 * 1e-6) / 1e9, 1),
+            "frac": round(b3 / (us3 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_step": int(b3)}
+        print(f"[bench] 43-layer stack: {extra['stack_43_layers_routed_plus_shared_rows16']}", file=sys.stderr,
+              flush=True)
+        dense = {}
+        for (k, n) in DENSE_SHAPES:
+            for b in DENSE_BITS:
+                key = f"{k}x{n}_K{b}"
+                dense[key] = time_dense(dev, k, n, b, DENSE_ROWS)
+                print(f"[bench] dense {key}: {dense[key]}", file=sys.stderr, flush=True)
+        extra["dense_gemv_cold"] = dense
+        if not a.no_cpu:
+            # the single-linear CPU reference path (4096 x 4096, 6-bit, one row)
+            from oracle import cpu_baseline as CB
+            lin = synth.dense(4096, 4096, 6, seed=3)
+            t = CB.time_linear(lin, 1)
+            extra["dense_4096x4096_K6_cpu"] = {"us": round(t * 1e6, 1), "cores": CB.threads(),
+                                               "sample": "dequant + fp32 matmul per call, median of 5 after 1 warm-up"}
+            print(f"[bench] dense cpu: {extra['dense_4096x4096_K6_cpu']}", file=sys.stderr, flush=True)
 
     cpu = None
     if not a.no_cpu:

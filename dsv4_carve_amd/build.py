@@ -30,7 +30,7 @@ UNITS += [("exl3_dense_inst.hip", [f"-DEXL3_BITS={b}"], f"exl3_dense_b{b}.o") fo
 UNITS += [("exl3_moe_capi.hip", [], "exl3_moe_capi.o")]
 # (bit-width mask, codebook) instances of the MoE kernel; keep in sync with
 # EXL3_MOE_INSTANCES in csrc/exl3_moe_capi.hip.
-MOE_UNITS = [(0x004, 1), (0x008, 1), (0x010, 1), (0x040, 1), (0x00C, 1), (0x01C, 1),
+MOE_UNITS = [(0x004, 1), (0x008, 1), (0x010, 1), (0x040, 1), (0x00C, 1), (0x01C, 1), (0x04C, 1),
              (0x1FE, 1), (0x1FE, 0), (0x1FE, 2)]
 UNITS += [("exl3_moe_inst.hip", [f"-DEXL3_MOE_MASK=0x{m:03X}u", f"-DEXL3_MOE_CB={c}"],
            f"exl3_moe_m{m:03x}_c{c}.o") for m, c in MOE_UNITS]

@@ -197,19 +197,54 @@ __device__ __forceinline__ void st_dev4(float* p, float4_t v) {
 __device__ __forceinline__ void st_dev2(uint32_t* p, uint2 v) {
     asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
-// Up to 8 16-byte device-scope loads issued back to back, then one wait.  The
-// wait lists every destination as read-write so no use can be scheduled
-// before it.
-template <int N>
-__device__ __forceinline__ void ld_dev4_batch(float4_t (&v)[8], const float* const (&p)[8]) {
-    static_assert(N >= 1 && N <= 8, "batch of 1..8");
-#pragma unroll
-    for (int j = 0; j < N; ++j)
-        asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(v[j]) : "v"(p[j]) : "memory");
-    asm volatile("s_waitcnt vmcnt(0)"
-                 : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7])
-                 :
-                 : "memory");
+// Eight 16-byte device-scope loads issued back to back and the wait for them,
+// in one asm statement: the destinations are defined only when the data is
+// there, so the compiler cannot place a use (or a copy) of one before it.
+// Early-clobber outputs keep every destination apart from the addresses.
+__device__ __forceinline__ void ld_dev4_x8(float4_t (&v)[8], const float* const (&p)[8]) {
+    asm volatile(
+        "global_load_dwordx4 %0, %8, off sc1\n\t"
+        "global_load_dwordx4 %1, %9, off sc1\n\t"
+        "global_load_dwordx4 %2, %10, off sc1\n\t"
+        "global_load_dwordx4 %3, %11, off sc1\n\t"
+        "global_load_dwordx4 %4, %12, off sc1\n\t"
+        "global_load_dwordx4 %5, %13, off sc1\n\t"
+        "global_load_dwordx4 %6, %14, off sc1\n\t"
+        "global_load_dwordx4 %7, %15, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
+          "=&v"(v[7])
+        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7])
+        : "memory");
+}
+
+// Sixteen such loads (two sets of eight) and one wait, as above.
+__device__ __forceinline__ void ld_dev4_x16(float4_t (&a)[8], float4_t (&b)[8], const float* const (&pa)[8],
+                                            const float* const (&pb)[8]) {
+    asm volatile(
+        "global_load_dwordx4 %0, %16, off sc1\n\t"
+        "global_load_dwordx4 %1, %17, off sc1\n\t"
+        "global_load_dwordx4 %2, %18, off sc1\n\t"
+        "global_load_dwordx4 %3, %19, off sc1\n\t"
+        "global_load_dwordx4 %4, %20, off sc1\n\t"
+        "global_load_dwordx4 %5, %21, off sc1\n\t"
+        "global_load_dwordx4 %6, %22, off sc1\n\t"
+        "global_load_dwordx4 %7, %23, off sc1\n\t"
+        "global_load_dwordx4 %8, %24, off sc1\n\t"
+        "global_load_dwordx4 %9, %25, off sc1\n\t"
+        "global_load_dwordx4 %10, %26, off sc1\n\t"
+        "global_load_dwordx4 %11, %27, off sc1\n\t"
+        "global_load_dwordx4 %12, %28, off sc1\n\t"
+        "global_load_dwordx4 %13, %29, off sc1\n\t"
+        "global_load_dwordx4 %14, %30, off sc1\n\t"
+        "global_load_dwordx4 %15, %31, off sc1\n\t"
+        "s_waitcnt vmcnt(0)"
+        : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(a[4]), "=&v"(a[5]), "=&v"(a[6]),
+          "=&v"(a[7]), "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]),
+          "=&v"(b[6]), "=&v"(b[7])
+        : "v"(pa[0]), "v"(pa[1]), "v"(pa[2]), "v"(pa[3]), "v"(pa[4]), "v"(pa[5]), "v"(pa[6]), "v"(pa[7]),
+          "v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]), "v"(pb[4]), "v"(pb[5]), "v"(pb[6]), "v"(pb[7])
+        : "memory");
 }
 
 // Completes this wave's outstanding memory operations (its device-scope data
@@ -234,12 +269,7 @@ __device__ __forceinline__ void sum_partials2(const float* a, const float* b, si
             qa[j] = a + (size_t)min(i0 + j, count - 1) * stride;
             qb[j] = b + (size_t)min(i0 + j, count - 1) * stride;
         }
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-            asm volatile("global_load_dwordx4 %0, %1, off sc1" : "=v"(va[j]) : "v"(qa[j]) : "memory");
-        ld_dev4_batch<8>(vb, qb);      // its wait covers the eight loads above too
-        asm volatile("" : "+v"(va[0]), "+v"(va[1]), "+v"(va[2]), "+v"(va[3]), "+v"(va[4]), "+v"(va[5]),
-                          "+v"(va[6]), "+v"(va[7]));
+        ld_dev4_x16(va, vb, qa, qb);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             if (i0 + j < count) {
@@ -258,7 +288,7 @@ __device__ __forceinline__ float4_t sum_partials(const float* p, size_t stride, 
         const float* q[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) q[j] = p + (size_t)min(i0 + j, count - 1) * stride;
-        ld_dev4_batch<8>(v, q);
+        ld_dev4_x8(v, q);
 #pragma unroll
         for (int j = 0; j < 8; ++j)
             if (i0 + j < count) acc += v[j];

@@ -33,7 +33,7 @@ namespace exl3 {
 namespace moe {
 
 constexpr int MAX_M = 16;
-constexpr int MAX_TOPK = 8;
+constexpr int MAX_TOPK = 9;                   // e.g. 8 routed slots + a shared expert
 constexpr int MAX_SLOTS = MAX_M * MAX_TOPK;   // also the bound on groups and pairs
 constexpr int MAX_EXPERTS = 2048;             // route-plan bitmask capacity
 constexpr int MAX_BLOCKS = 64;                // hidden/256 and intermediate/256 (both <= 16384)
@@ -419,22 +419,24 @@ __device__ void item_g(const Params& P, const Plan& pl, int t, int epoch, Tracer
     const int lane = threadIdx.x;
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
     const float* DC = at<float>(P.scratch, L.DC);
-    float4_t d[MAX_TOPK];
-    float wt[MAX_TOPK];
-    const float* q[MAX_TOPK];
+    static_assert(MAX_TOPK <= 16, "one batch of slot loads");
+    float4_t d[2][8];
+    float wt[16];
+    const float* q[2][8];
 #pragma unroll
-    for (int j = 0; j < MAX_TOPK; ++j) {       // issue every slot's load first
+    for (int j = 0; j < 16; ++j) {             // every slot's load issued first
         const int pair = j < P.topk ? pl.slotpair[row * P.topk + j] : -1;
         wt[j] = pair >= 0 ? P.w[row * P.topk + j] : 0.f;
-        q[j] = DC + (size_t)(pair >= 0 ? pair : 0) * P.H + col;
+        q[j >> 3][j & 7] = DC + (size_t)(pair >= 0 ? pair : 0) * P.H + col;
     }
-    ld_dev4_batch<MAX_TOPK>(d, q);
+    if (P.topk <= 8) ld_dev4_x8(d[0], q[0]);
+    else ld_dev4_x16(d[0], d[1], q[0], q[1]);
     float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < MAX_TOPK; ++j) {       // fp32 sum in top-k slot order
         if (j >= P.topk || pl.slotpair[row * P.topk + j] < 0) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[j][i];
+        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[j >> 3][j & 7][i];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
@@ -507,9 +509,8 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
         for (int i = threadIdx.x; i < P.m * P.H; i += WAVE) store_out(P.out, i, P.out_kind, 0.f);
     }
 
-    // Ticket order: gate/up items, down items, gather items.  A wave's first
-    // ticket is its own index (no burst on the counter at launch); later ones
-    // come from the counter, offset by the grid size.
+    // Ticket order: gate/up items, down items, gather items; every ticket is
+    // drawn from the counter by the wave that will run it.
     for (int t = wave_atomic_add(&ctrl->ticket, 1); t < total; t = wave_atomic_add(&ctrl->ticket, 1)) {
         if (t < nA) {
             tr(EV_A_BEGIN, t);

@@ -15,6 +15,7 @@ namespace moe {
 #define EXL3_MOE_INSTANCES(X)                 \
     X(0x004u, 1) X(0x008u, 1) X(0x010u, 1)    \
     X(0x040u, 1) X(0x00Cu, 1) X(0x01Cu, 1)    \
+    X(0x04Cu, 1)                              \
     X(0x1FEu, 1) X(0x1FEu, 0) X(0x1FEu, 2)
 
 #define EXL3_DECL(M, C)                                                          \
@@ -58,7 +59,7 @@ int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t top
         return fail("hidden and intermediate must be positive multiples of 256");
     if (hidden > COLS * MAX_BLOCKS || intermediate > COLS * MAX_BLOCKS)
         return fail("hidden and intermediate must be at most 16384");
-    if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..8");
+    if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..9");
     return layout((int)hidden, (int)intermediate, (int)topk).total + trace_bytes();
 }
 
@@ -96,7 +97,7 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
     if (hidden > COLS * MAX_BLOCKS || intermediate > COLS * MAX_BLOCKS)
         return fail("hidden and intermediate must be at most 16384");
     if (n_experts < 1 || n_experts > MAX_EXPERTS) return fail("expert count out of range (1..2048)");
-    if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..8");
+    if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..9");
     if (!(swiglu_limit > 0.0f) || !isfinite(swiglu_limit)) return fail("requires a finite positive SwiGLU limit");
     if (codebook < CB_3INST || codebook > CB_MUL1) return fail("codebook must be 0, 1 or 2");
     uint32_t mask;

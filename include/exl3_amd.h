@@ -63,8 +63,9 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
  *   out[r] = sum_j routing_weights[r][j] * d   (fp32, slot order), one cast.
  * Replaces vllm_exl3_c.lna2_moe_decode (recipe-lna/lna2/lna_moe_ticket.cu:507-581)
  * and generalises its fixed geometry (H=4096, I=256, top-6, one K per launch,
- * :34-36, 532) to any hidden % 256 == 0, intermediate % 256 == 0, topk <= 8 and
- * a per-expert bit width.
+ * :34-36, 532) to any hidden and intermediate that are multiples of 256 up to
+ * 16384, topk <= 9 (room for a shared expert as one more slot of weight 1)
+ * and a per-expert bit width.
  *   x: [m][hidden] (x_kind), out: [m][hidden] (out_kind), 1 <= m <= exl3_moe_max_rows().
  *   Pointer tables: device int64 [n_experts] of data pointers (as built by
  *     build_exl3_fused_state, recipe-lna/vllm_exl3_exl3.py.lna:1543-1569).
@@ -74,8 +75,9 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
  *     when expert_bits is NULL).
  *   swiglu_limit: finite and > 0 (lna_moe_ticket.cu:552-553).
  *   scratch: >= exl3_moe_scratch_bytes(hidden, intermediate, topk) bytes, zeroed
- *     once before first use; self-resetting afterwards.  One launch at a time
- *     per scratch buffer.
+ *     once before first use; self-resetting afterwards, and one buffer may
+ *     serve layers of different shapes (its control words have fixed
+ *     offsets).  One launch at a time per scratch buffer.
  */
 int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk);
 int exl3_moe_max_rows(void);

@@ -89,3 +89,17 @@ def time_expert(ex: dict, rows: int, reps: int = 3, limit: float = 10.0) -> floa
         expert_rows(x, ex, limit, lut)
         ts.append(time.perf_counter() - t0)
     return float(np.median(ts))
+
+
+def time_linear(p: dict, rows: int, reps: int = 5) -> float:
+    """Median seconds for one dense linear (dequant each call + fp32 matmul)."""
+    torch.set_num_threads(threads())
+    lut = torch.from_numpy(O.codebook_lut(O.CB_MCG).view(np.float16).copy())
+    x = torch.from_numpy(np.random.default_rng(1).standard_normal((rows, p["suh"].size)).astype(np.float32))
+    linear(x, p, p["bits"], lut)
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        linear(x, p, p["bits"], lut)
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))

@@ -315,3 +315,22 @@ def test_tp_slice_against_oracle(tp_slice, kb, m, uniform):
     x = synth.activations(m, 4096, seed=501 + m)
     got = layer.run(x, ids, w, uniform=uniform).cpu().numpy()
     assert_close(got, layer.ref(x, ids, w), what=f"tp slice K{kb} m={m}")
+
+
+# ---------------------------------------------------------------- shared expert fused as one more slot
+
+
+@pytest.mark.parametrize("m", [1, 7, 16])
+def test_shared_expert_as_extra_slot(dev, m):
+    """Routed top-8 plus a 6-bit shared expert appended to every row with
+    weight 1: out = sum of the routed experts + the shared expert, in one launch."""
+    print(f"shared expert slot m={m}", flush=True)
+    if not hasattr(test_shared_expert_as_extra_slot, "layer"):
+        test_shared_expert_as_extra_slot.layer = Layer(dev, 13, 512, 256, [3, 2] * 6 + [6], seed=33)
+    layer = test_shared_expert_as_extra_slot.layer
+    ids, w = synth.routing(m, 12, 8, seed=600 + m)
+    ids9 = np.concatenate([ids, np.full((m, 1), 12, np.int32)], axis=1)
+    w9 = np.concatenate([w, np.ones((m, 1), np.float32)], axis=1)
+    x = synth.activations(m, 512, seed=601 + m)
+    got = layer.run(x, ids9, w9).cpu().numpy()
+    assert_close(got, layer.ref(x, ids9, w9), what=f"routed + shared m={m}")

@@ -58,7 +58,9 @@ def test_moe_host_arithmetic_without_device():
     b = lib.exl3_moe_scratch_bytes(4096, 256, 6)
     assert a > b > 0 and a % 256 == 0
     assert lib.exl3_moe_scratch_bytes(4000, 2048, 8) == -1 and "multiples of 256" in _err()
-    assert lib.exl3_moe_scratch_bytes(4096, 2048, 9) == -1 and "topk" in _err()
+    assert lib.exl3_moe_scratch_bytes(4096, 2048, 10) == -1 and "topk" in _err()
+    assert lib.exl3_moe_scratch_bytes(4096, 2048, 9) > 0
+    assert lib.exl3_moe_scratch_bytes(16640, 256, 8) == -1 and "16384" in _err()
 
 
 def _moe_call(**kw):
@@ -84,7 +86,8 @@ def _moe_call(**kw):
     ({"hidden": 500}, "multiples of 256"),
     ({"intermediate": 128}, "multiples of 256"),
     ({"n_experts": 0}, "expert count"),
-    ({"topk": 9}, "topk"),
+    ({"topk": 10}, "topk"),
+    ({"hidden": 16640}, "16384"),
     ({"limit": 0.0}, "SwiGLU limit"),
     ({"limit": float("inf")}, "SwiGLU limit"),
     ({"limit": float("nan")}, "SwiGLU limit"),
