@@ -69,9 +69,10 @@ int exl3_moe_info(int64_t* out, int n) {
     clear_error();
     if (!out || n < 0) return fail("bad output buffer");
     const int cus = device_cus();
+    const int64_t lds = (int64_t)MAX_M * NSTEP_CAP * STEP_K * 2 + (int64_t)sizeof(Plan);
     const int64_t v[] = {cus, (int64_t)cus * cached_waves(4), WAVE, MAX_M, MAX_SLOTS, STEP_K, COLS,
-                         (int64_t)sizeof(Ctrl)};
-    const int k = n < 8 ? n : 8;
+                         layout(COLS, COLS, 1).PA, lds};
+    const int k = n < 9 ? n : 9;
     for (int i = 0; i < k; ++i) out[i] = v[i];
     return k;
 }

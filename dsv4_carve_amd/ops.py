@@ -265,10 +265,12 @@ def moe_scratch(device: torch.device, hidden: int, intermediate: int, topk: int)
 
 
 def moe_info() -> list[int]:
+    """[cus, waves per launch, threads per wave, max rows, max pairs, step k,
+    cols, control-region bytes, LDS bytes per workgroup]."""
     import ctypes
 
-    buf = (ctypes.c_int64 * 8)()
-    n = _lib.check(_lib.load().exl3_moe_info(buf, 8))
+    buf = (ctypes.c_int64 * 9)()
+    n = _lib.check(_lib.load().exl3_moe_info(buf, 9))
     return [int(buf[i]) for i in range(n)]
 
 
@@ -360,6 +362,12 @@ def lna2_moe_prepare(bits: int) -> None:
 
 
 def lna2_moe_info(bits: int) -> list[int]:
-    """[cus, waves per launch, threads per wave, max rows, max pairs, step k, cols, ctrl bytes]."""
+    """The reference's 14 positions (lna_moe_ticket.cu:494-505): [sms, resident,
+    width, teams, threads, cfg, pfd, rows_cap, smem, ctrl_bytes, scratch_bytes,
+    max_m, max_pairs, streams].  Here a "team" is one wave, cfg is 0, pfd is the
+    one step of tile prefetch, scratch_bytes is for the reference geometry and
+    streams is 1 (one launch at a time per scratch buffer)."""
     lna2_moe_prepare(bits)
-    return moe_info()
+    cus, waves, width, max_m, max_pairs, _, _, ctrl, lds = moe_info()
+    return [cus, waves, width, waves, width, 0, 1, max_m, lds, ctrl, lna2_moe_scratch_bytes(), max_m,
+            max_pairs, 1]

@@ -94,7 +94,8 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
  * Launch geometry for diagnostics (replaces lna2_moe_info,
  * recipe-lna/lna2/lna_moe_ticket.cu:494-505): writes up to n values
  * {cus, waves_per_launch, threads_per_wave, max_rows, max_pairs, step_k, cols,
- *  ctrl_bytes} and returns how many were written.
+ *  ctrl_bytes (the fixed control region at the head of the scratch),
+ *  lds_bytes (per single-wave workgroup)} and returns how many were written.
  */
 int exl3_moe_info(int64_t* out, int n);
 

@@ -334,3 +334,27 @@ def test_shared_expert_as_extra_slot(dev, m):
     x = synth.activations(m, 512, seed=601 + m)
     got = layer.run(x, ids9, w9).cpu().numpy()
     assert_close(got, layer.ref(x, ids9, w9), what=f"routed + shared m={m}")
+
+
+def test_lna2_signature_and_info(tp_slice, dev):
+    """The reference plugin's calls, verbatim in shape: scratch sized by
+    lna2_moe_scratch_bytes() with no arguments, lna2_moe_decode with the nine
+    tables positionally and an int width, lna2_moe_info(bits)[13] = streams."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    info = ops.lna2_moe_info(2)
+    assert len(info) == 14 and info[13] == 1 and info[11] == ops.lna2_moe_max_rows() == 16
+    assert info[0] > 0 and info[1] >= info[0] and info[10] == ops.lna2_moe_scratch_bytes()
+    layer = tp_slice[2]
+    scratch = torch.zeros(ops.lna2_moe_scratch_bytes(), dtype=torch.uint8, device=dev)
+    m = 5
+    ids, w = synth.routing(m, 256, 6, seed=777)
+    x = synth.activations(m, 4096, seed=778)
+    xd = to_dev(x, dev)
+    out = torch.empty_like(xd)
+    t = layer.tables
+    ops.lna2_moe_decode(xd, out, t["gate_trellis"], t["gate_suh"], t["gate_svh"], t["up_trellis"], t["up_suh"],
+                        t["up_svh"], t["down_trellis"], t["down_suh"], t["down_svh"],
+                        to_dev(ids.astype(np.int32), dev), to_dev(w, dev), 2, 10.0, scratch)
+    assert_close(out.float().cpu().numpy(), layer.ref(x, ids, w), max_abs=2e-2 + 8e-3, what="lna2 signature")
