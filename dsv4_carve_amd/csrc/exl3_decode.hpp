@@ -88,30 +88,17 @@ __device__ __forceinline__ uint32_t win_lo(const uint32_t* W) {
 // selection, no masking of `src` needed) plus the masked xor (v_bitop3_b32).
 template <bool HI, uint32_t MULT, uint32_t ADD>
 __device__ __forceinline__ uint32_t mcg_bits(uint32_t src) {
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     constexpr uint32_t MLO = MULT & 0xffffu;
-    constexpr uint32_t KHI = MULT & 0xffff0000u;   // lo lane 0, hi lane MULT>>16
-    uint32_t p, x;
-    // p = w * MLO + ADD  (32-bit); p.lo16 is x.lo16, p.hi16 is the carry into x.hi16
-    // (gfx9 VOP3 reads at most one SGPR, so a nonzero ADD goes through a VGPR)
-    if constexpr (ADD == 0u) {
-        if constexpr (HI)
-            asm("v_mad_u32_u16 %0, %1, %2, 0 op_sel:[1,0,0,0]" : "=v"(p) : "v"(src), "s"(MLO));
-        else
-            asm("v_mad_u32_u16 %0, %1, %2, 0" : "=v"(p) : "v"(src), "s"(MLO));
-    } else {
-        if constexpr (HI)
-            asm("v_mad_u32_u16 %0, %1, %2, %3 op_sel:[1,0,0,0]" : "=v"(p) : "v"(src), "s"(MLO), "v"(ADD));
-        else
-            asm("v_mad_u32_u16 %0, %1, %2, %3" : "=v"(p) : "v"(src), "s"(MLO), "v"(ADD));
-    }
-    // x.lo16 = 0 * . + p.lo16 ; x.hi16 = w * (MULT>>16) + p.hi16  (mod 2^16)
-    if constexpr (HI)
-        asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,1,1]"
-            : "=v"(x) : "v"(src), "s"(KHI), "v"(p));
-    else
-        asm("v_pk_mad_u16 %0, %1, %2, %3 op_sel:[0,0,0] op_sel_hi:[0,1,1]"
-            : "=v"(x) : "v"(src), "s"(KHI), "v"(p));
-    return (x & 0x8fff8fffu) ^ 0x3b603b60u;
+    constexpr unsigned short MHI = (unsigned short)(MULT >> 16);
+    const uint32_t w = HI ? (src >> 16) : (src & 0xffffu);
+    // p = w * MLO + ADD (16x16 -> 32 bit): p.lo16 is x.lo16, p.hi16 the carry into x.hi16
+    const uint32_t p = w * MLO + ADD;
+    // x.lo16 = p.lo16 ; x.hi16 = w * (MULT >> 16) + p.hi16  (mod 2^16)
+    const u16x2 sv = __builtin_bit_cast(u16x2, src);
+    const u16x2 wv = HI ? sv.yy : sv.xx;
+    const u16x2 x = wv * (u16x2){0, MHI} + __builtin_bit_cast(u16x2, p);
+    return (__builtin_bit_cast(uint32_t, x) & 0x8fff8fffu) ^ 0x3b603b60u;
 }
 
 template <int CB>

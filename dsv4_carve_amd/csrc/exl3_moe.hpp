@@ -164,11 +164,11 @@ struct Plan {
 
 // Expert-major row bitmask, then a wave-wide exclusive scan over experts
 // (lna_moe_ticket.cu:167-214 computes the same plan with block scans).
-// `tmp` (>= E*6 bytes of LDS) is only used during planning.
+// `tmp` (>= 6 * E bytes of LDS) is only used during planning.
 __device__ inline void build_plan(const Params& P, Plan& pl, char* tmp) {
     const int lane = threadIdx.x;
     uint32_t* rowmask = reinterpret_cast<uint32_t*>(tmp);
-    int16_t* epair = reinterpret_cast<int16_t*>(tmp + 4 * MAX_EXPERTS);
+    int16_t* epair = reinterpret_cast<int16_t*>(tmp + 4 * P.E);
     for (int e = lane; e < P.E; e += WAVE) rowmask[e] = 0u;
     __syncthreads();
     const int slots = P.m * P.topk;
@@ -486,11 +486,19 @@ __device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int
     });
 }
 
+// Dynamic LDS of one workgroup: the activation tile of an item (rows x
+// NSTEP_CAP steps x 64 halves, which is also the fp32 transpose buffer of its
+// partials, 1 KB per row) or the route-plan workspace, whichever is larger.
+// Sized by the batch, so small batches leave room for more resident waves.
+inline int moe_lds_kb(int64_t m, int64_t n_experts) {
+    const int64_t a = m * NSTEP_CAP * STEP_K * 2, b = 6 * n_experts;
+    return (int)(((a > b ? a : b) + 1023) / 1024);
+}
+
 template <uint32_t MASK, int CB>
 __global__ __launch_bounds__(64) void moe_kernel(Params P) {
-    __shared__ uint16_t xa[MAX_M * NSTEP_CAP * STEP_K];     // also route-plan workspace
+    extern __shared__ __align__(16) uint16_t xa[];   // moe_lds_kb(m, E) KB
     __shared__ Plan pl;
-    static_assert(sizeof(xa) >= 6 * MAX_EXPERTS, "plan workspace");
     const Layout& L = P.L;
     Tracer tr;
     tr.init(P.scratch + P.trace_off);
@@ -539,10 +547,10 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
 
 // Launcher for one (bit-width mask, codebook) instantiation; defined in exl3_moe_inst.hip.
 template <uint32_t MASK, int CB>
-int launch_moe(const Params& P, int waves, hipStream_t stream);
+int launch_moe(const Params& P, int waves, int lds_kb, hipStream_t stream);
 
 template <uint32_t MASK, int CB>
-int moe_waves_per_cu();
+int moe_waves_per_cu(int lds_kb);
 
 }  // namespace moe
 }  // namespace exl3

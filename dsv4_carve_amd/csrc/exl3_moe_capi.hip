@@ -19,30 +19,33 @@ namespace moe {
     X(0x1FEu, 1) X(0x1FEu, 0) X(0x1FEu, 2)
 
 #define EXL3_DECL(M, C)                                                          \
-    template <> int launch_moe<M, C>(const Params&, int, hipStream_t);          \
-    template <> int moe_waves_per_cu<M, C>();
+    template <> int launch_moe<M, C>(const Params&, int, int, hipStream_t);     \
+    template <> int moe_waves_per_cu<M, C>(int);
 EXL3_MOE_INSTANCES(EXL3_DECL)
 #undef EXL3_DECL
 
 struct Instance {
     uint32_t mask;
     int cb;
-    int (*launch)(const Params&, int, hipStream_t);
-    int (*waves)();
+    int (*launch)(const Params&, int, int, hipStream_t);
+    int (*waves)(int);
 };
 
 #define EXL3_ENTRY(M, C) {M, C, &launch_moe<M, C>, &moe_waves_per_cu<M, C>},
 static const Instance kInstances[] = {EXL3_MOE_INSTANCES(EXL3_ENTRY)};
 #undef EXL3_ENTRY
 
-static int cached_waves(int idx) {
-    static int cache[MAX_DEVICES][sizeof(kInstances) / sizeof(kInstances[0])] = {};
+// Resident single-wave workgroups per CU for an instance at a dynamic LDS size
+// (1..MAX_LDS_KB KB), asked of the occupancy API once per device.
+constexpr int MAX_LDS_KB = 16;
+static int cached_waves(int idx, int lds_kb) {
+    static int cache[MAX_DEVICES][sizeof(kInstances) / sizeof(kInstances[0])][MAX_LDS_KB + 1] = {};
     static std::mutex mu;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) dev = 0;
     std::lock_guard<std::mutex> lock(mu);
-    if (!cache[dev][idx]) cache[dev][idx] = kInstances[idx].waves();
-    return cache[dev][idx];
+    if (!cache[dev][idx][lds_kb]) cache[dev][idx][lds_kb] = kInstances[idx].waves(lds_kb);
+    return cache[dev][idx][lds_kb];
 }
 
 }  // namespace moe
@@ -69,8 +72,9 @@ int exl3_moe_info(int64_t* out, int n) {
     clear_error();
     if (!out || n < 0) return fail("bad output buffer");
     const int cus = device_cus();
-    const int64_t lds = (int64_t)MAX_M * NSTEP_CAP * STEP_K * 2 + (int64_t)sizeof(Plan);
-    const int64_t v[] = {cus, (int64_t)cus * cached_waves(4), WAVE, MAX_M, MAX_SLOTS, STEP_K, COLS,
+    const int kb = moe_lds_kb(MAX_M, 256);
+    const int64_t lds = (int64_t)kb * 1024 + (int64_t)sizeof(Plan);
+    const int64_t v[] = {cus, (int64_t)cus * cached_waves(4, kb), WAVE, MAX_M, MAX_SLOTS, STEP_K, COLS,
                          layout(COLS, COLS, 1).PA, lds};
     const int k = n < 9 ? n : 9;
     for (int i = 0; i < k; ++i) out[i] = v[i];
@@ -120,7 +124,10 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
 
     // Distinct experts are at most min(E, m * topk); size the items for that.
     const int64_t groups = n_experts < m * topk ? n_experts : m * topk;
-    const int64_t resident = (int64_t)device_cus() * cached_waves(idx);
+    const int lds_kb = moe_lds_kb(m, n_experts);
+    static_assert(MAX_M * NSTEP_CAP * STEP_K * 2 <= MAX_LDS_KB * 1024 && 6 * MAX_EXPERTS <= MAX_LDS_KB * 1024,
+                  "dynamic LDS bound");
+    const int64_t resident = (int64_t)device_cus() * cached_waves(idx, lds_kb);
     const int stepsA = item_steps((int)hidden, groups * 2 * (intermediate / COLS), resident);
     const int stepsB = item_steps((int)intermediate, groups * (hidden / COLS), resident);
     const Layout L = layout((int)hidden, (int)intermediate, (int)topk, stepsA, stepsB);
@@ -140,7 +147,7 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
 
     const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB) + (int64_t)L.nH * m;
     const int waves = (int)(items < resident ? items : resident);
-    return kInstances[idx].launch(P, waves, reinterpret_cast<hipStream_t>(stream));
+    return kInstances[idx].launch(P, waves, lds_kb, reinterpret_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

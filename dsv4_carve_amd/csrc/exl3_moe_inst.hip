@@ -14,16 +14,18 @@ namespace exl3 {
 namespace moe {
 
 template <>
-int launch_moe<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int waves, hipStream_t stream) {
-    hipLaunchKernelGGL((moe_kernel<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(waves), dim3(WAVE), 0, stream, P);
+int launch_moe<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int waves, int lds_kb, hipStream_t stream) {
+    hipLaunchKernelGGL((moe_kernel<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(waves), dim3(WAVE), (size_t)lds_kb * 1024,
+                       stream, P);
     return check_launch();
 }
 
 template <>
-int moe_waves_per_cu<EXL3_MOE_MASK, EXL3_MOE_CB>() {
+int moe_waves_per_cu<EXL3_MOE_MASK, EXL3_MOE_CB>(int lds_kb) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, reinterpret_cast<const void*>(moe_kernel<EXL3_MOE_MASK, EXL3_MOE_CB>), WAVE, 0) != hipSuccess ||
+            &n, reinterpret_cast<const void*>(moe_kernel<EXL3_MOE_MASK, EXL3_MOE_CB>), WAVE,
+            (size_t)lds_kb * 1024) != hipSuccess ||
         n < 1)
         n = 1;
     return n;
