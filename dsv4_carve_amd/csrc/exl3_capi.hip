@@ -77,6 +77,11 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
         int rc = 0;
         EXL3_BITS_SWITCH(bits, rc = launch_gemv<B_>(args));
         if (rc) return rc;
+        if (p.split_reduce) {
+            hipLaunchKernelGGL((gemv_reduce_kernel<16>), dim3(p.n_cb * R), dim3(64), 0, s, partials, svh, cr,
+                               c_kind, R, (int)n, p.n_kc);
+            if ((rc = check_launch())) return rc;
+        }
     }
     return 0;
 }

@@ -112,23 +112,28 @@ __global__ __launch_bounds__(64) void dequant_had_kernel(const int16_t* __restri
 constexpr int GEMV_NSTEP_CAP = 8;   // k rows per item <= 512
 
 struct GemvPlan {
-    int nsteps;   // steps (64 k-rows) per item, even
-    int n_kc;     // k-chunks
-    int n_cb;     // 256-column blocks
+    int nsteps;         // steps (64 k-rows) per item, even
+    int n_kc;           // k-chunks
+    int n_cb;           // 256-column blocks
+    bool split_reduce;  // partial sums finished by gemv_reduce_kernel
 };
 
 inline GemvPlan gemv_plan(int64_t rows, int64_t k, int64_t n, int cus) {
     GemvPlan p;
     p.n_cb = (int)((n + COLS - 1) / COLS);
     const int ksteps = (int)(k / STEP_K);
-    // Aim for >= ~4 waves per CU while keeping the split-K partial traffic
-    // (rows * n * 4 bytes per chunk) small next to the weight bytes.
+    // Aim for >= ~4 waves per CU: small matrices need short k-chunks to spread
+    // over 256 CUs (the partials are small next to the weights either way).
     int nsteps = GEMV_NSTEP_CAP;
-    while (nsteps > 2 && (int64_t)p.n_cb * (ksteps / nsteps) < 4LL * cus && rows <= 4) nsteps /= 2;
+    while (nsteps > 2 && (int64_t)p.n_cb * (ksteps / nsteps) < 4LL * cus) nsteps /= 2;
     while (ksteps % nsteps) nsteps /= 2;
     if (nsteps < 2) nsteps = 2;
     p.nsteps = nsteps;
     p.n_kc = ksteps / nsteps;
+    // The last arriver of a 256-column block would sum rows * n_kc partial
+    // vectors behind a device-scope counter; beyond a handful, a separate
+    // reduction launch (one wave per column block and row) is shorter.
+    p.split_reduce = (int64_t)(rows < MAX_ROWS ? rows : MAX_ROWS) * p.n_kc > 4;
     return p;
 }
 
@@ -138,7 +143,9 @@ inline int64_t gemv_scratch_bytes(int64_t rows, int64_t k, int64_t n, int cus) {
     return ctr + (int64_t)p.n_kc * (rows < 16 ? rows : 16) * n * 4;
 }
 
-template <int BITS, int CB>
+// SPLIT: store the partials and stop (gemv_reduce_kernel finishes them);
+// otherwise the last arriver of each column block finishes it.
+template <int BITS, int CB, bool SPLIT>
 __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x,
                                                   const int16_t* __restrict__ trellis,
                                                   const uint16_t* __restrict__ suh,
@@ -163,6 +170,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
 
     const int cols = min(COLS, N - cb * COLS);
     store_partials(acc, partials + (size_t)kc * R * N + cb * COLS, N, R, cols, reinterpret_cast<float*>(xa));
+    if constexpr (SPLIT) return;
     publish_fence();
     int old = 0;
     if (lane == 0) old = atomicAdd(&counters[cb], 1);
@@ -186,6 +194,40 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
             for (int e = 0; e < 4; ++e) store_out(out, (size_t)m * N + col + e, out_kind, v[e] * HAD_NORM * sv[e]);
     }
     if (lane == 0) __hip_atomic_store(&counters[cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Split-K finish, one wave per (256-column block, row): the partials of chunks
+// 0..n_kc-1 summed in chunk order (as the last-arriver path does), output
+// Hadamard, svh, store.  Runs after gemv_kernel<.., true> on the same stream,
+// so plain loads see its partials.
+template <int BATCH>
+__global__ __launch_bounds__(64) void gemv_reduce_kernel(const float* __restrict__ partials,
+                                                         const uint16_t* __restrict__ svh, void* __restrict__ out,
+                                                         int out_kind, int R, int N, int n_kc) {
+    const int lane = threadIdx.x;
+    const int cb = blockIdx.x / R, m = blockIdx.x - (blockIdx.x / R) * R;
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    const bool ok = col < N;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (ok) {
+        const float* p = partials + (size_t)m * N + col;
+        const size_t stride = (size_t)R * N;
+        for (int k0 = 0; k0 < n_kc; k0 += BATCH) {
+            float4_t t[BATCH];
+#pragma unroll
+            for (int j = 0; j < BATCH; ++j)
+                t[j] = k0 + j < n_kc ? *reinterpret_cast<const float4_t*>(p + (size_t)(k0 + j) * stride)
+                                     : float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < BATCH; ++j)
+                if (k0 + j < n_kc)
+                    for (int e = 0; e < 4; ++e) v[e] = v[e] + t[j][e];
+        }
+    }
+    fwht128_x4(v);
+    if (ok)
+        for (int e = 0; e < 4; ++e)
+            store_out(out, (size_t)m * N + col + e, out_kind, v[e] * HAD_NORM * f16_bits_to_f32(svh[col + e]));
 }
 
 // ---------------------------------------------------------------- per-bit-width launchers

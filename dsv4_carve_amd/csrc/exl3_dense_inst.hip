@@ -35,9 +35,14 @@ int launch_gemv<EXL3_BITS>(const GemvArgs& a) {
     constexpr int B = EXL3_BITS;
     auto go = [&](auto cbc) {
         constexpr int C = decltype(cbc)::value;
-        hipLaunchKernelGGL((gemv_kernel<B, C>), dim3(a.plan.n_cb * a.plan.n_kc), dim3(64), 0, a.stream, a.x,
-                           a.trellis, a.suh, a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps,
-                           a.plan.n_kc, a.counters, a.partials);
+        if (a.plan.split_reduce)
+            hipLaunchKernelGGL((gemv_kernel<B, C, true>), dim3(a.plan.n_cb * a.plan.n_kc), dim3(64), 0, a.stream,
+                               a.x, a.trellis, a.suh, a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps,
+                               a.plan.n_kc, a.counters, a.partials);
+        else
+            hipLaunchKernelGGL((gemv_kernel<B, C, false>), dim3(a.plan.n_cb * a.plan.n_kc), dim3(64), 0, a.stream,
+                               a.x, a.trellis, a.suh, a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps,
+                               a.plan.n_kc, a.counters, a.partials);
     };
     switch (a.codebook) {
         case CB_MCG: go(std::integral_constant<int, CB_MCG>{}); break;
