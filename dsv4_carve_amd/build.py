@@ -34,6 +34,8 @@ MOE_UNITS = [(0x004, 1), (0x008, 1), (0x010, 1), (0x040, 1), (0x00C, 1), (0x01C,
              (0x1FE, 1), (0x1FE, 0), (0x1FE, 2)]
 UNITS += [("exl3_moe_inst.hip", [f"-DEXL3_MOE_MASK=0x{m:03X}u", f"-DEXL3_MOE_CB={c}"],
            f"exl3_moe_m{m:03x}_c{c}.o") for m, c in MOE_UNITS]
+UNITS += [("exl3_prefill_capi.hip", [], "exl3_prefill_capi.o")]
+UNITS += [("exl3_prefill_inst.hip", [f"-DEXL3_BITS={b}"], f"exl3_pf_b{b}.o") for b in range(1, 9)]
 
 
 def _compile(unit):

@@ -1,0 +1,222 @@
+// Routed-MoE layer for many tokens (prefill): the same mathematics as the
+// decode kernel (gate/up, clamped SiLU*mul, down, slot-order fp32 sum), done as
+// grouped GEMMs so every decoded weight is applied to up to 32 rows.
+//
+// Launch sequence (one stream, no host synchronisation, no persistent state):
+//   1. plan:     route (token, slot) pairs by expert (counting sort in LDS),
+//                cut each expert's rows into tiles of PF_RB rows.
+//   2. rotate:   Xh[proj][pair] = half(H (half(x[token] * suh[e])) / sqrt(128))
+//                for the gate and up projections.
+//   3. gemm:     gate/up tiles: decode each 64x256 weight step once per tile
+//                and feed it to the MFMAs of both 16-row blocks; epilogue
+//                output Hadamard + svh -> fp32 [pair][I].
+//   4. act:      half(silu(min(g, L)) * clamp(u, -L, L)), x down_suh, input
+//                Hadamard -> fp16 down input [pair][I].
+//   5. gemm:     down tiles, same kernel -> fp32 [pair][H].
+//   6. gather:   out[t] = sum over slots j of w[t][j] * D[pair(t, j)] in slot
+//                order, one cast.
+// Rounding points follow the decode kernel (lna_moe_ticket.cu:5-12), so a
+// token's result equals the decode kernel's up to fp32 summation order.
+// Reference counterpart: exl3_moe's M16 inner path / reconstruct_hgemm for
+// many rows (recipe-lna/exllamav3/exl3.py.lna:161-218), which dequantizes the
+// whole weight to HBM first.
+#pragma once
+
+#include "exl3_gemv.hpp"
+#include "exl3_capi_util.hpp"
+
+namespace exl3 {
+namespace prefill {
+
+constexpr int PF_RB = 32;                 // rows per tile (two MFMA row blocks)
+constexpr int PF_MAX_EXPERTS = 2048;
+constexpr int PF_MAX_TOPK = 9;
+constexpr int PF_MAX_PAIRS = 65536;
+
+struct PfLayout {
+    int64_t meta, eoff, toff, tile_e, tile_r0, tile_n, pair_slot, pos, Xh, GU, AD, D, total;
+    int64_t max_tiles;
+};
+
+__host__ __device__ inline int64_t pf_al(int64_t v) { return (v + 255) / 256 * 256; }
+
+inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
+    PfLayout L;
+    L.max_tiles = E + (pairs + PF_RB - 1) / PF_RB;
+    int64_t o = 0;
+    L.meta = o;      o = pf_al(o + 64);
+    L.eoff = o;      o = pf_al(o + (E + 1) * 4);
+    L.toff = o;      o = pf_al(o + (E + 1) * 4);
+    L.tile_e = o;    o = pf_al(o + L.max_tiles * 4);
+    L.tile_r0 = o;   o = pf_al(o + L.max_tiles * 4);
+    L.tile_n = o;    o = pf_al(o + L.max_tiles * 4);
+    L.pair_slot = o; o = pf_al(o + pairs * 4);
+    L.pos = o;       o = pf_al(o + pairs * 4);
+    L.Xh = o;        o = pf_al(o + 2 * pairs * H * 2);
+    L.GU = o;        o = pf_al(o + 2 * pairs * I * 4);
+    L.AD = o;        o = pf_al(o + pairs * I * 2);
+    L.D = o;         o = pf_al(o + pairs * H * 4);
+    L.total = o;
+    return L;
+}
+
+struct PfParams {
+    const void* x; int x_kind;
+    void* out; int out_kind;
+    int T, H, I, E, topk, P;             // tokens, hidden, intermediate, experts, top-k, pair slots
+    const int64_t* gt; const int64_t* gsu; const int64_t* gsv;
+    const int64_t* ut; const int64_t* usu; const int64_t* usv;
+    const int64_t* dt; const int64_t* dsu; const int64_t* dsv;
+    const int32_t* ids; const float* w;
+    const int8_t* ebits; int bits;
+    float limit;
+    char* scratch;
+    PfLayout L;
+};
+
+template <typename T>
+__device__ __forceinline__ T* pat(char* base, int64_t off) { return reinterpret_cast<T*>(base + off); }
+
+// ---------------------------------------------------------------- 3/5. grouped GEMM tile
+
+// Duplicated A operand for k-group r from the 16 halves of this lane's row and
+// k-slice (w[j] = halves 2j, 2j+1): the four k of group r are 2r, 2r+1, 2r+8,
+// 2r+9 (the order mma_tile's windows use), each twice (lo/hi addends).
+__device__ __forceinline__ half8_t a_from_words(const u32x4_t& lo, const u32x4_t& hi, int r) {
+    const uint32_t a = lo[r & 3], b = hi[r & 3];
+    u32x4_t d;
+    d[0] = (a & 0xffffu) | (a << 16);
+    d[1] = (a >> 16) | (a & 0xffff0000u);
+    d[2] = (b & 0xffffu) | (b << 16);
+    d[3] = (b >> 16) | (b & 0xffff0000u);
+    return __builtin_bit_cast(half8_t, d);
+}
+
+// The 64 MFMAs of one decoded tile, each B operand applied to both row blocks.
+template <int BITS, int CB>
+__device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[2][2], float4_t (&acc)[2][16]) {
+    half8_t A0[4], A1[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        A0[r] = a_from_words(a[0][0], a[0][1], r);
+        A1[r] = a_from_words(a[1][0], a[1][1], r);
+    }
+    static_for<16>([&](auto NI) {
+        constexpr int n = decltype(NI)::value;
+        static_for<4>([&](auto RI) {
+            constexpr int r = decltype(RI)::value;
+            constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+            u32x4_t b;
+            b[0] = decode_pair<BITS, CB, T0 + 0>(W);
+            b[1] = decode_pair<BITS, CB, T0 + 1>(W);
+            b[2] = decode_pair<BITS, CB, T0 + 2>(W);
+            b[3] = decode_pair<BITS, CB, T0 + 3>(W);
+            const half8_t B = __builtin_bit_cast(half8_t, b);
+            acc[0][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[r], B, acc[0][n], 0, 0, 0);
+            acc[1][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[r], B, acc[1][n], 0, 0, 0);
+        });
+    });
+}
+
+// One (tile, 256-column block) of C[rows, N] = A[rows, K] . Wq[K, N], rows of A
+// at A + (row0 + i) * K (fp16, already rotated), i < nrows <= 32; epilogue
+// y = (H c / sqrt(128)) * svh written as fp32 to out + (row0 + i) * N.
+template <int BITS, int CB>
+__device__ __forceinline__ void pf_tile(const uint16_t* A, int row0, int nrows, const int16_t* trellis, const uint16_t* svh,
+                        int K, int N, int cb, float* out, float* tbuf) {
+    const int lane = threadIdx.x;
+    const int g = lane >> 4, c = lane & 15;
+    const int n16 = N / 16;
+    const u32x4_t* tp = tile_ptr<BITS>(trellis, n16, 0, cb * 16);
+    const size_t tstep = (size_t)4 * n16 * tile_vecs<BITS>();
+    // A rows of this lane: c and c + 16 (zero beyond nrows); k-slice g of each
+    // step.  Every load reads a valid row and a dead row is zeroed after, so
+    // the loop has no branches (the accumulators stay put in registers).
+    const bool live0 = c < nrows, live1 = c + 16 < nrows;
+    const u32x4_t* a0 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live0 ? c : 0)) * K + 16 * g);
+    const u32x4_t* a1 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live1 ? c + 16 : 0)) * K + 16 * g);
+    const uint32_t m0 = live0 ? 0xffffffffu : 0u, m1 = live1 ? 0xffffffffu : 0u;
+    const int astep = STEP_K / 8;        // 16-byte vectors per 64 k
+
+    float4_t acc[2][16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[0][i] = acc[1][i] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    const int nsteps = K / STEP_K;       // even (K % 128 == 0)
+    TileRegs<BITS> t0, t1;
+    u32x4_t ac[2][2];
+    auto load_a = [&](int s) {
+        ac[0][0] = a0[s * astep] & m0; ac[0][1] = a0[s * astep + 1] & m0;
+        ac[1][0] = a1[s * astep] & m1; ac[1][1] = a1[s * astep + 1] & m1;
+    };
+    load_tile<BITS>(t0, tp);
+    for (int s = 0; s < nsteps; s += 2) {
+        load_tile<BITS>(t1, tp + (s + 1) * tstep);
+        load_a(s);
+        mma_tile2<BITS, CB>(t0.words(), ac, acc);
+        // the last iteration reloads its own step (a valid address, unused)
+        load_tile<BITS>(t0, tp + min(s + 2, nsteps - 1) * tstep);
+        load_a(s + 1);
+        mma_tile2<BITS, CB>(t1.words(), ac, acc);
+    }
+
+    // epilogue: both row blocks transposed through LDS at once (the
+    // accumulators die here), then one output row per pass
+    const int col = 128 * (lane >> 5) + 4 * (lane & 31);
+    __syncthreads();
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4_t* t = reinterpret_cast<float4_t*>(tbuf + (16 * rb + 4 * g + i) * COLS + 16 * c);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                t[q] = float4_t{acc[rb][4 * q][i], acc[rb][4 * q + 1][i], acc[rb][4 * q + 2][i], acc[rb][4 * q + 3][i]};
+        }
+    __syncthreads();
+    float sv[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sv[e] = f16_bits_to_f32(svh[cb * COLS + col + e]);
+    for (int row = 0; row < nrows; ++row) {
+        const float4_t v4 = reinterpret_cast<const float4_t*>(tbuf + row * COLS)[col / 4];
+        float v[4] = {v4[0], v4[1], v4[2], v4[3]};
+        fwht128_x4(v);
+        float4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = v[e] * HAD_NORM * sv[e];
+        *reinterpret_cast<float4_t*>(out + (size_t)(row0 + row) * N + cb * COLS + col) = o;
+    }
+}
+
+// gate/up (DOWN = false): blockIdx = (tile, projection, column block of I);
+// down (DOWN = true): blockIdx = (tile, column block of H).  One launch per bit
+// width present (one width per kernel keeps the registers at two waves per
+// SIMD); blocks past the planned tile count or of another width return at once.
+template <int BITS, int CB, bool DOWN>
+__global__ __launch_bounds__(64) void pf_gemm_kernel(PfParams P) {
+    __shared__ float tbuf[PF_RB * COLS];
+    const PfLayout& L = P.L;
+    const int ncb = (DOWN ? P.H : P.I) / COLS;
+    const int per_tile = DOWN ? ncb : 2 * ncb;
+    const int t = blockIdx.x / per_tile, rem = blockIdx.x - (blockIdx.x / per_tile) * per_tile;
+    if (t >= pat<int>(P.scratch, L.meta)[1]) return;
+    const int e = pat<int>(P.scratch, L.tile_e)[t];
+    if ((P.ebits ? (int)P.ebits[e] : P.bits) != BITS) return;
+    const int proj = DOWN ? 0 : rem / ncb, cb = DOWN ? rem : rem - (rem / ncb) * ncb;
+    const int row0 = pat<int>(P.scratch, L.tile_r0)[t];
+    const int nrows = pat<int>(P.scratch, L.tile_n)[t];
+    const int K = DOWN ? P.I : P.H, N = DOWN ? P.H : P.I;
+    const uint16_t* A = DOWN ? pat<uint16_t>(P.scratch, L.AD)
+                             : pat<uint16_t>(P.scratch, L.Xh) + (size_t)proj * P.P * P.H;
+    const int16_t* tr = reinterpret_cast<const int16_t*>((DOWN ? P.dt : (proj ? P.ut : P.gt))[e]);
+    const uint16_t* svh = reinterpret_cast<const uint16_t*>((DOWN ? P.dsv : (proj ? P.usv : P.gsv))[e]);
+    float* out = DOWN ? pat<float>(P.scratch, L.D) : pat<float>(P.scratch, L.GU) + (size_t)proj * P.P * P.I;
+    pf_tile<BITS, CB>(A, row0, nrows, tr, svh, K, N, cb, out, tbuf);
+}
+
+// Launcher of the grouped GEMM for one bit width (exl3_prefill_inst.hip).
+template <int BITS>
+int launch_pf_gemm(const PfParams& P, int codebook, bool down, int blocks, hipStream_t stream);
+
+}  // namespace prefill
+}  // namespace exl3

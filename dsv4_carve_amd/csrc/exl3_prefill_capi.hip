@@ -1,0 +1,277 @@
+// C ABI of the routed-MoE prefill path (grouped GEMMs over tokens routed to
+// the same expert):
+//   exl3_moe_prefill_scratch_bytes, exl3_moe_prefill  <- exllamav3_ext.exl3_moe
+//   for many rows (recipe-lna/vllm_exl3_exl3.py.lna:1597-1704, its fat-chunk
+//   path) and LinearEXL3.reconstruct_hgemm (recipe-lna/exllamav3/exl3.py.lna:161-218)
+#include <cmath>
+#include <mutex>
+
+#include "exl3_prefill.hpp"
+
+namespace exl3 {
+namespace prefill {
+
+// ---------------------------------------------------------------- 1. plan (one workgroup of 1024 threads)
+
+// Exclusive scan of n ints in LDS by wave 0 (64 at a time, carrying the sum).
+__device__ __forceinline__ void wave0_scan(int* v, int n, int* total) {
+    if (threadIdx.x >= WAVE) return;
+    const int lane = threadIdx.x;
+    int carry = 0;
+    for (int i0 = 0; i0 < n; i0 += WAVE) {
+        const int x = i0 + lane < n ? v[i0 + lane] : 0;
+        int s = x;
+#pragma unroll
+        for (int d = 1; d < WAVE; d <<= 1) {
+            const int y = __shfl_up(s, d, WAVE);
+            if (lane >= d) s += y;
+        }
+        if (i0 + lane < n) v[i0 + lane] = carry + s - x;
+        carry += __shfl(s, WAVE - 1, WAVE);
+    }
+    if (lane == 0) *total = carry;
+}
+
+__global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
+    __shared__ int cnt[PF_MAX_EXPERTS + 1];
+    __shared__ int off[PF_MAX_EXPERTS + 1];
+    __shared__ int tof[PF_MAX_EXPERTS + 1];
+    __shared__ int totals[2];
+    const PfLayout& L = P.L;
+    const int tid = threadIdx.x, nt = blockDim.x;
+    for (int e = tid; e < P.E; e += nt) cnt[e] = 0;
+    __syncthreads();
+    for (int s = tid; s < P.P; s += nt) {
+        const int e = P.ids[s];
+        if (e >= 0 && e < P.E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    for (int e = tid; e < P.E; e += nt) {
+        off[e] = cnt[e];
+        tof[e] = (cnt[e] + PF_RB - 1) / PF_RB;
+    }
+    __syncthreads();
+    wave0_scan(off, P.E, &totals[0]);
+    wave0_scan(tof, P.E, &totals[1]);
+    __syncthreads();
+    int* eoff = pat<int>(P.scratch, L.eoff);
+    int* toff = pat<int>(P.scratch, L.toff);
+    int* tile_e = pat<int>(P.scratch, L.tile_e);
+    int* tile_r0 = pat<int>(P.scratch, L.tile_r0);
+    int* tile_n = pat<int>(P.scratch, L.tile_n);
+    for (int e = tid; e < P.E; e += nt) {
+        eoff[e] = off[e];
+        toff[e] = tof[e];
+        const int c = cnt[e];
+        for (int j = 0; j * PF_RB < c; ++j) {
+            tile_e[tof[e] + j] = e;
+            tile_r0[tof[e] + j] = off[e] + j * PF_RB;
+            tile_n[tof[e] + j] = min(PF_RB, c - j * PF_RB);
+        }
+    }
+    if (tid == 0) {
+        eoff[P.E] = totals[0];
+        toff[P.E] = totals[1];
+        pat<int>(P.scratch, L.meta)[0] = totals[0];
+        pat<int>(P.scratch, L.meta)[1] = totals[1];
+    }
+    __syncthreads();
+    // place the pairs: any order within an expert (a row's result does not
+    // depend on its position in the tile; the gather sums in slot order)
+    for (int e = tid; e < P.E; e += nt) cnt[e] = off[e];
+    __syncthreads();
+    int* pair_slot = pat<int>(P.scratch, L.pair_slot);
+    int* pos = pat<int>(P.scratch, L.pos);
+    for (int s = tid; s < P.P; s += nt) {
+        const int e = P.ids[s];
+        int p = -1;
+        if (e >= 0 && e < P.E) {
+            p = atomicAdd(&cnt[e], 1);
+            pair_slot[p] = s;
+        }
+        pos[s] = p;
+    }
+}
+
+// ---------------------------------------------------------------- 2. input rotation (one wave per pair and projection)
+
+__global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
+    const PfLayout& L = P.L;
+    const int p = blockIdx.x >> 1, proj = blockIdx.x & 1;
+    if (p >= pat<int>(P.scratch, L.meta)[0]) return;
+    const int lane = threadIdx.x;
+    const int s = pat<int>(P.scratch, L.pair_slot)[p];
+    const int tok = s / P.topk, e = P.ids[s];
+    const uint16_t* suh = reinterpret_cast<const uint16_t*>((proj ? P.usu : P.gsu)[e]);
+    const uint32_t* xr = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (size_t)tok * P.H);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(pat<uint16_t>(P.scratch, L.Xh) + ((size_t)proj * P.P + p) * P.H);
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(suh);
+    for (int b = 0; b < P.H / 128; ++b) {
+        uint32_t v2 = xr[64 * b + lane];
+        const uint32_t s2 = sp[64 * b + lane];
+        if (P.x_kind != 0)
+            v2 = (uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 & 0xffffu))) |
+                 ((uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 >> 16))) << 16);
+        float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 & 0xffffu) * f16_bits_to_f32(s2 & 0xffffu)));
+        float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 >> 16) * f16_bits_to_f32(s2 >> 16)));
+        fwht128_x2(v0, v1);
+        dst[64 * b + lane] = (uint32_t)f32_to_f16_bits(v0 * HAD_NORM) | ((uint32_t)f32_to_f16_bits(v1 * HAD_NORM) << 16);
+    }
+}
+
+// ---------------------------------------------------------------- 4. activation + down input rotation (one wave per pair)
+
+__global__ __launch_bounds__(64) void pf_act_kernel(PfParams P) {
+    const PfLayout& L = P.L;
+    const int p = blockIdx.x;
+    if (p >= pat<int>(P.scratch, L.meta)[0]) return;
+    const int lane = threadIdx.x;
+    const int e = P.ids[pat<int>(P.scratch, L.pair_slot)[p]];
+    const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I;
+    const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I;
+    const uint16_t* dsu = reinterpret_cast<const uint16_t*>(P.dsu[e]);
+    uint16_t* AD = pat<uint16_t>(P.scratch, L.AD) + (size_t)p * P.I;
+    const int col = 128 * (lane >> 5) + 4 * (lane & 31);
+    for (int c0 = 0; c0 < P.I; c0 += COLS) {
+        const float4_t g4 = *reinterpret_cast<const float4_t*>(G + c0 + col);
+        const float4_t u4 = *reinterpret_cast<const float4_t*>(U + c0 + col);
+        float dv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float gg = g4[i], uu = u4[i];
+            if (gg > P.limit) gg = P.limit;
+            if (uu < -P.limit) uu = -P.limit;
+            if (uu > P.limit) uu = P.limit;
+            const uint16_t act = f32_to_f16_bits((gg / (1.0f + expf(-gg))) * uu);
+            dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[c0 + col + i])));
+        }
+        fwht128_x4(dv);
+        uint2 packed;
+        packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
+        packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
+        *reinterpret_cast<uint2*>(AD + c0 + col) = packed;
+    }
+}
+
+// ---------------------------------------------------------------- 6. gather (one wave per token and 256-column block)
+
+__global__ __launch_bounds__(64) void pf_gather_kernel(PfParams P) {
+    const PfLayout& L = P.L;
+    const int ncb = P.H / COLS;
+    const int tok = blockIdx.x / ncb, cb = blockIdx.x - (blockIdx.x / ncb) * ncb;
+    const int lane = threadIdx.x;
+    const int col = cb * COLS + 4 * lane;
+    const int* pos = pat<int>(P.scratch, L.pos);
+    const float* D = pat<float>(P.scratch, L.D);
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < P.topk; ++j) {
+        const int p = pos[tok * P.topk + j];
+        if (p < 0) continue;
+        const float wt = P.w[tok * P.topk + j];
+        const float4_t d = *reinterpret_cast<const float4_t*>(D + (size_t)p * P.H + col);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt * d[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)tok * P.H + col + i, P.out_kind, s4[i]);
+}
+
+
+template <> int launch_pf_gemm<1>(const PfParams&, int, bool, int, hipStream_t);
+template <> int launch_pf_gemm<2>(const PfParams&, int, bool, int, hipStream_t);
+template <> int launch_pf_gemm<3>(const PfParams&, int, bool, int, hipStream_t);
+template <> int launch_pf_gemm<4>(const PfParams&, int, bool, int, hipStream_t);
+template <> int launch_pf_gemm<5>(const PfParams&, int, bool, int, hipStream_t);
+template <> int launch_pf_gemm<6>(const PfParams&, int, bool, int, hipStream_t);
+template <> int launch_pf_gemm<7>(const PfParams&, int, bool, int, hipStream_t);
+template <> int launch_pf_gemm<8>(const PfParams&, int, bool, int, hipStream_t);
+
+// Grouped GEMM over every width in `mask` (one launch each).
+static int launch_widths(const PfParams& P, uint32_t mask, int codebook, bool down, int blocks, hipStream_t s) {
+    int (*const fn[9])(const PfParams&, int, bool, int, hipStream_t) = {
+        nullptr, &launch_pf_gemm<1>, &launch_pf_gemm<2>, &launch_pf_gemm<3>, &launch_pf_gemm<4>,
+        &launch_pf_gemm<5>, &launch_pf_gemm<6>, &launch_pf_gemm<7>, &launch_pf_gemm<8>};
+    for (int b = 1; b <= 8; ++b)
+        if (mask & (1u << b)) {
+            const int rc = fn[b](P, codebook, down, blocks, s);
+            if (rc) return rc;
+        }
+    return 0;
+}
+
+}  // namespace prefill
+}  // namespace exl3
+
+using namespace exl3;
+using namespace exl3::prefill;
+
+extern "C" {
+
+int64_t exl3_moe_prefill_scratch_bytes(int64_t tokens, int64_t hidden, int64_t intermediate, int64_t topk,
+                                       int64_t n_experts) {
+    clear_error();
+    if (tokens < 1 || topk < 1 || topk > PF_MAX_TOPK || tokens * topk > PF_MAX_PAIRS)
+        return fail("tokens * topk must be in 1..65536 with topk in 1..9");
+    if (hidden <= 0 || hidden % COLS || intermediate <= 0 || intermediate % COLS)
+        return fail("hidden and intermediate must be positive multiples of 256");
+    if (n_experts < 1 || n_experts > PF_MAX_EXPERTS) return fail("expert count out of range (1..2048)");
+    return pf_layout(tokens * topk, hidden, intermediate, n_experts).total;
+}
+
+int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t tokens, int64_t hidden,
+                     int64_t intermediate, int64_t n_experts, int64_t topk,
+                     const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                     const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                     const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                     const int32_t* expert_ids, const float* routing_weights,
+                     const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                     float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    clear_error();
+    if (!x || !out || !expert_ids || !routing_weights || !scratch) return fail("null pointer");
+    if (!gate_trellis || !gate_suh || !gate_svh || !up_trellis || !up_suh || !up_svh || !down_trellis ||
+        !down_suh || !down_svh)
+        return fail("null pointer table");
+    if (x_kind != 0 && x_kind != 1) return fail("x must be fp16 or bf16");
+    if (out_kind < OUT_F16 || out_kind > OUT_F32) return fail("out must be fp16, bf16 or fp32");
+    const int64_t need = exl3_moe_prefill_scratch_bytes(tokens, hidden, intermediate, topk, n_experts);
+    if (need < 0) return (int)need;
+    if (!(swiglu_limit > 0.0f) || !std::isfinite(swiglu_limit)) return fail("requires a finite positive SwiGLU limit");
+    if (codebook < CB_3INST || codebook > CB_MUL1) return fail("codebook must be 0, 1 or 2");
+    uint32_t mask;
+    if (expert_bits) {
+        mask = (uint32_t)bits_mask;
+        if (mask == 0 || (mask & ~0x1FEu)) return fail("bits_mask must name widths in 1..8");
+    } else {
+        if (bits < 1 || bits > 8) return fail("bits must be in 1..8");
+        mask = 1u << bits;
+    }
+    if (scratch_bytes < need) return fail("scratch too small (see exl3_moe_prefill_scratch_bytes)");
+
+    PfParams P;
+    P.x = x; P.x_kind = x_kind; P.out = out; P.out_kind = out_kind;
+    P.T = (int)tokens; P.H = (int)hidden; P.I = (int)intermediate; P.E = (int)n_experts; P.topk = (int)topk;
+    P.P = (int)(tokens * topk);
+    P.gt = gate_trellis; P.gsu = gate_suh; P.gsv = gate_svh;
+    P.ut = up_trellis; P.usu = up_suh; P.usv = up_svh;
+    P.dt = down_trellis; P.dsu = down_suh; P.dsv = down_svh;
+    P.ids = expert_ids; P.w = routing_weights;
+    P.ebits = expert_bits; P.bits = bits;
+    P.limit = swiglu_limit;
+    P.scratch = reinterpret_cast<char*>(scratch);
+    P.L = pf_layout(P.P, hidden, intermediate, n_experts);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    int rc;
+    hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(1024), 0, s, P);
+    if ((rc = check_launch())) return rc;
+    hipLaunchKernelGGL(pf_rotate_kernel, dim3(2 * P.P), dim3(WAVE), 0, s, P);
+    if ((rc = check_launch())) return rc;
+    const int64_t tiles = P.L.max_tiles;
+    if ((rc = launch_widths(P, mask, codebook, false, (int)(tiles * 2 * (intermediate / COLS)), s))) return rc;
+    hipLaunchKernelGGL(pf_act_kernel, dim3(P.P), dim3(WAVE), 0, s, P);
+    if ((rc = check_launch())) return rc;
+    if ((rc = launch_widths(P, mask, codebook, true, (int)(tiles * (hidden / COLS)), s))) return rc;
+    hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)(tokens * (hidden / COLS))), dim3(WAVE), 0, s, P);
+    return check_launch();
+}
+
+}  // extern "C"

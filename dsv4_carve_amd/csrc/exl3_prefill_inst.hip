@@ -1,0 +1,31 @@
+// Instantiates the grouped-GEMM kernels of the routed-MoE prefill path for one
+// bit width (EXL3_BITS, set by the build), every codebook, both directions.
+#include "exl3_prefill.hpp"
+
+#ifndef EXL3_BITS
+#error "EXL3_BITS must be defined"
+#endif
+
+namespace exl3 {
+namespace prefill {
+
+template <>
+int launch_pf_gemm<EXL3_BITS>(const PfParams& P, int codebook, bool down, int blocks, hipStream_t stream) {
+    constexpr int B = EXL3_BITS;
+    auto go = [&](auto cbc) {
+        constexpr int C = decltype(cbc)::value;
+        if (down)
+            hipLaunchKernelGGL((pf_gemm_kernel<B, C, true>), dim3(blocks), dim3(WAVE), 0, stream, P);
+        else
+            hipLaunchKernelGGL((pf_gemm_kernel<B, C, false>), dim3(blocks), dim3(WAVE), 0, stream, P);
+    };
+    switch (codebook) {
+        case CB_MCG: go(std::integral_constant<int, CB_MCG>{}); break;
+        case CB_3INST: go(std::integral_constant<int, CB_3INST>{}); break;
+        default: go(std::integral_constant<int, CB_MUL1>{}); break;
+    }
+    return check_launch();
+}
+
+}  // namespace prefill
+}  // namespace exl3

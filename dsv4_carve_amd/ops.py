@@ -124,6 +124,25 @@ def _moe_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, expert_b
         _ptr(scratch), scratch.numel(), _stream(x.device)))
 
 
+_LIB.define("moe_prefill(Tensor x, Tensor(a!) out, Tensor gate_trellis, Tensor gate_suh, Tensor gate_svh, "
+            "Tensor up_trellis, Tensor up_suh, Tensor up_svh, Tensor down_trellis, Tensor down_suh, "
+            "Tensor down_svh, Tensor expert_ids, Tensor routing_weights, Tensor? expert_bits, int bits, "
+            "int bits_mask, int codebook, float swiglu_limit, int hidden, int intermediate, "
+            "Tensor(b!) scratch) -> ()")
+
+
+def _prefill_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, expert_bits, bits, bits_mask,
+                  codebook, limit, hidden, intermediate, scratch):
+    L = _lib.load()
+    _lib.check(L.exl3_moe_prefill(
+        _ptr(x), X_KIND[x.dtype], _ptr(out), OUT_KIND[out.dtype], x.shape[0], int(hidden), int(intermediate),
+        gt.numel(), ids.shape[1],
+        _ptr(gt), _ptr(gsu), _ptr(gsv), _ptr(ut), _ptr(usu), _ptr(usv), _ptr(dt), _ptr(dsu), _ptr(dsv),
+        _ptr(ids), _ptr(w), _ptr(expert_bits), int(bits), int(bits_mask), int(codebook), float(limit),
+        _ptr(scratch), scratch.numel(), _stream(x.device)))
+
+
+_LIB.impl("moe_prefill", _prefill_impl, "CUDA")
 _LIB.impl("dequant", _dequant_impl, "CUDA")
 _LIB.impl("gemm", _gemm_impl, "CUDA")
 _LIB.impl("moe_decode", _moe_impl, "CUDA")
@@ -371,3 +390,57 @@ def lna2_moe_info(bits: int) -> list[int]:
     cus, waves, width, max_m, max_pairs, _, _, ctrl, lds = moe_info()
     return [cus, waves, width, waves, width, 0, 1, max_m, lds, ctrl, lna2_moe_scratch_bytes(), max_m,
             max_pairs, 1]
+
+
+# ------------------------------------------------------------------ routed MoE, many tokens (prefill)
+
+
+def moe_prefill_scratch_bytes(tokens: int, hidden: int, intermediate: int, topk: int, n_experts: int) -> int:
+    return int(_lib.check(_lib.load().exl3_moe_prefill_scratch_bytes(tokens, hidden, intermediate, topk,
+                                                                      n_experts)))
+
+
+def moe_prefill_scratch(device: torch.device, tokens: int, hidden: int, intermediate: int, topk: int,
+                        n_experts: int) -> torch.Tensor:
+    """Shared per-device prefill scratch (grown outside capture; never needs zeroing)."""
+    return SCRATCH.get(device, "moe_prefill", moe_prefill_scratch_bytes(tokens, hidden, intermediate, topk,
+                                                                        n_experts))
+
+
+def moe_prefill(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Tensor,
+                routing_weights: torch.Tensor, *, intermediate: int, bits: int | None = None,
+                expert_bits: torch.Tensor | None = None, bits_mask: int | None = None,
+                codebook: int = CB_MCG, swiglu_limit: float = 10.0,
+                scratch: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed-expert layer over many tokens (grouped GEMMs): x [tokens, hidden]
+    -> out [tokens, hidden]; arguments as moe_decode, any number of tokens with
+    tokens * topk <= 65536."""
+    tabs = [tables[k] for k in MOE_TABLE_KEYS] if isinstance(tables, dict) else list(tables)
+    _check(len(tabs) == 9, "nine pointer tables are required")
+    _check(x.is_cuda and x.dtype in X_KIND and x.dim() == 2 and x.is_contiguous(),
+           "input must be contiguous HIP fp16/bf16 [tokens, hidden]")
+    T, hidden = x.shape
+    _check(out.is_cuda and out.device == x.device and tuple(out.shape) == (T, hidden) and out.is_contiguous()
+           and out.dtype in OUT_KIND, "output must be contiguous fp16/bf16/fp32 [tokens, hidden] on x's device")
+    _check(expert_ids.is_cuda and expert_ids.dtype == torch.int32 and expert_ids.is_contiguous() and
+           expert_ids.dim() == 2 and expert_ids.shape[0] == T, "expert_ids must be contiguous int32 [tokens, topk]")
+    _check(routing_weights.is_cuda and routing_weights.dtype == torch.float32 and
+           routing_weights.is_contiguous() and routing_weights.shape == expert_ids.shape,
+           "routing_weights must be contiguous fp32 [tokens, topk]")
+    n_experts = tabs[0].numel()
+    for t in tabs:
+        _check(t.is_cuda and t.device == x.device and t.dtype == torch.int64 and t.is_contiguous() and
+               t.numel() == n_experts, "pointer tables must be contiguous int64 [experts] on the input device")
+    if expert_bits is not None:
+        _check(expert_bits.is_cuda and expert_bits.dtype == torch.int8 and expert_bits.numel() == n_experts,
+               "expert_bits must be int8 [experts] on the device")
+        _check(bits_mask is not None and bits_mask > 0, "bits_mask is required with expert_bits")
+        b, mask = 0, int(bits_mask)
+    else:
+        _check(bits is not None and 1 <= int(bits) <= 8, "bits must be in 1..8")
+        b, mask = int(bits), 0
+    if scratch is None:
+        scratch = moe_prefill_scratch(x.device, T, hidden, intermediate, expert_ids.shape[1], n_experts)
+    torch.ops.exl3_amd.moe_prefill(x, out, *tabs, expert_ids, routing_weights, expert_bits, b, mask,
+                                   int(codebook), float(swiglu_limit), int(hidden), int(intermediate), scratch)
+    return out

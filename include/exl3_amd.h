@@ -91,6 +91,30 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
                     float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
 
 /*
+ * Routed-MoE layer for many tokens (prefill), same mathematics as
+ * exl3_moe_decode: tokens are routed by expert on the device and each expert's
+ * weights are decoded once per 32 routed rows, feeding fp16 MFMA with fp32
+ * accumulation (grouped GEMMs; six launches on `stream`, no host sync).
+ * Replaces exllamav3_ext.exl3_moe on the many-row path
+ * (recipe-lna/vllm_exl3_exl3.py.lna:1597-1704) and LinearEXL3.reconstruct_hgemm
+ * per expert (recipe-lna/exllamav3/exl3.py.lna:161-218), which dequantize whole
+ * weights to HBM first.  Arguments as exl3_moe_decode, with tokens in place of
+ * m (1 <= tokens * topk <= 65536, topk <= 9, n_experts <= 2048).  scratch:
+ * >= exl3_moe_prefill_scratch_bytes(...) bytes; no zeroing needed, nothing is
+ * kept between calls; one call at a time per scratch buffer.
+ */
+int64_t exl3_moe_prefill_scratch_bytes(int64_t tokens, int64_t hidden, int64_t intermediate, int64_t topk,
+                                       int64_t n_experts);
+int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t tokens, int64_t hidden,
+                     int64_t intermediate, int64_t n_experts, int64_t topk,
+                     const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                     const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                     const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                     const int32_t* expert_ids, const float* routing_weights,
+                     const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                     float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
+
+/*
  * Launch geometry for diagnostics (replaces lna2_moe_info,
  * recipe-lna/lna2/lna_moe_ticket.cu:494-505): writes up to n values
  * {cus, waves_per_launch, threads_per_wave, max_rows, max_pairs, step_k, cols,

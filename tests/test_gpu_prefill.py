@@ -1,0 +1,137 @@
+"""GPU parity of the routed-MoE prefill path (grouped GEMMs, exl3_moe_prefill)
+through the C ABI: against the oracle on small layers, with uniform and
+Zipf-skewed routing (experts with several 32-row tiles), invalid and duplicate
+ids, dtypes, a shared expert as an extra slot; against the decode kernel
+(itself checked against the oracle) at the full 256-expert shape, row by row.
+Tolerance: max-abs 2e-2, rel-L2 1e-3 against the oracle; decode vs prefill
+differ only by fp32 summation order (split-K partials vs one pass)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from dsv4_carve_amd import synth
+from oracle import oracle as O
+from tests.helpers import assert_close, rel_l2, to_dev
+from tests.test_gpu_moe import Layer
+
+pytestmark = pytest.mark.gpu
+
+LIMIT = 10.0
+
+
+def run_prefill(layer, x, ids, w, out_dtype=None, limit=LIMIT, uniform=False):
+    import torch
+    from dsv4_carve_amd import ops
+
+    dev = layer.ebits.device
+    xd = x if isinstance(x, torch.Tensor) else to_dev(x, dev)
+    out = torch.empty(xd.shape, dtype=out_dtype or torch.float32, device=dev)
+    widths = dict(bits=layer.bits[0]) if uniform else dict(expert_bits=layer.ebits, bits_mask=layer.mask)
+    ops.moe_prefill(xd, out, layer.tables, to_dev(ids.astype(np.int32), dev), to_dev(w.astype(np.float32), dev),
+                    intermediate=layer.I, swiglu_limit=limit, **widths)
+    return out
+
+
+@pytest.fixture(scope="module")
+def small(dev):
+    bits = [3, 2, 4, 3, 2, 2, 3, 4, 2, 3, 3, 2, 4, 2, 3, 2]
+    return Layer(dev, 16, 512, 256, bits, seed=23)
+
+
+@pytest.mark.parametrize("tokens", [1, 5, 17, 40, 130])
+@pytest.mark.parametrize("routing", ["uniform", "zipf"])
+def test_prefill_against_oracle(small, tokens, routing):
+    print(f"prefill {routing} tokens={tokens}", flush=True)
+    if routing == "uniform":
+        ids, w = synth.routing(tokens, 16, 6, seed=800 + tokens)
+    else:
+        ids, w = synth.zipf_routing(tokens, 16, 6, seed=801 + tokens)
+    x = synth.activations(tokens, 512, seed=802 + tokens)
+    got = run_prefill(small, x, ids, w).cpu().numpy()
+    assert_close(got, small.ref(x, ids, w), what=f"prefill {routing} T={tokens}")
+
+
+def test_prefill_hot_expert_many_tiles(small):
+    """Every token routes to expert 3 (4 tiles of 32 rows + a partial one) and
+    to one other expert; duplicate ids within a row count twice."""
+    T = 150
+    rng = np.random.default_rng(4)
+    ids = np.stack([np.array([3, rng.integers(0, 16), 3, rng.integers(0, 16)]) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, 4)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)          # routing weights are normalised per token
+    x = synth.activations(T, 512, seed=805)
+    got = run_prefill(small, x, ids, w).cpu().numpy()
+    assert_close(got, small.ref(x, ids, w), what="hot expert")
+
+
+def test_prefill_invalid_ids_and_zero_rows(small):
+    T = 33
+    rng = np.random.default_rng(6)
+    ids = rng.integers(-3, 20, size=(T, 5)).astype(np.int32)
+    ids[7] = -1                       # a token routed nowhere: exact zero
+    w = rng.random((T, 5)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    x = synth.activations(T, 512, seed=806)
+    got = run_prefill(small, x, ids, w).cpu().numpy()
+    assert np.all(got[7] == 0.0)
+    assert_close(got, small.ref(x, ids, w), what="invalid ids")
+
+
+@pytest.mark.parametrize("x_dtype,out_dtype", [("fp16", "bf16"), ("bf16", "fp16"), ("bf16", "fp32")])
+def test_prefill_dtypes(small, dev, x_dtype, out_dtype):
+    import torch
+
+    dt = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+    T = 24
+    ids, w = synth.zipf_routing(T, 16, 6, seed=807)
+    x = synth.activations(T, 512, seed=808)
+    xd = to_dev(x, dev).to(dt[x_dtype])
+    got = run_prefill(small, xd, ids, w, out_dtype=dt[out_dtype]).float().cpu().numpy()
+    x16 = xd.to(torch.float16).cpu().numpy()
+    ref = small.ref(x16, ids, w)
+    # a 16-bit output adds its own rounding (half an ulp: 2^-11 fp16, 2^-9 bf16)
+    slack = {"fp32": 0.0, "fp16": 1e-3, "bf16": 4e-3}[out_dtype]
+    assert_close(got, ref, max_abs=2e-2 + 8 * slack, rel=1e-3 + slack, what=f"{x_dtype}->{out_dtype}")
+
+
+def test_prefill_shared_expert_slot(dev):
+    layer = Layer(dev, 13, 512, 256, [3, 2] * 6 + [6], seed=34)
+    T = 45
+    ids, w = synth.zipf_routing(T, 12, 8, seed=809)
+    ids9 = np.concatenate([ids, np.full((T, 1), 12, np.int32)], axis=1)
+    w9 = np.concatenate([w, np.ones((T, 1), np.float32)], axis=1)
+    x = synth.activations(T, 512, seed=810)
+    got = run_prefill(layer, x, ids9, w9).cpu().numpy()
+    assert_close(got, layer.ref(x, ids9, w9), what="routed + shared, prefill")
+
+
+def test_prefill_uniform_width_and_repeat(dev):
+    import torch
+
+    layer = Layer(dev, 8, 256, 512, [2] * 8, seed=35)
+    T = 70
+    ids, w = synth.routing(T, 8, 3, seed=811)
+    x = synth.activations(T, 256, seed=812)
+    a = run_prefill(layer, x, ids, w, uniform=True)
+    b = run_prefill(layer, x, ids, w, uniform=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), "prefill is not bitwise repeatable"
+    assert_close(a.cpu().numpy(), layer.ref(x, ids, w), what="uniform K2")
+
+
+def test_prefill_matches_decode_at_full_shape(dev):
+    """256 experts, top-8, hidden 4096, intermediate 2048, 3/2-bit: 48 tokens in
+    one prefill call against three 16-row decode launches, row by row."""
+    from tests.test_gpu_moe import Layer as L
+
+    print("prefill vs decode at the full layer shape", flush=True)
+    layer = L(dev, 256, 4096, 2048, synth.mixed_bits(256), seed=2)
+    T = 48
+    ids, w = synth.zipf_routing(T, 256, 8, seed=813)
+    x = synth.activations(T, 4096, seed=814)
+    pre = run_prefill(layer, x, ids, w).cpu().numpy()
+    dec = np.concatenate([layer.run(x[i:i + 16], ids[i:i + 16], w[i:i + 16]).cpu().numpy() for i in (0, 16, 32)])
+    for r in range(T):
+        assert rel_l2(pre[r], dec[r]) < 1e-4, f"row {r}: prefill and decode differ"
