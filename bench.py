@@ -169,6 +169,51 @@ def time_dense(dev, k, n, bits, rows_list, steps=40):
     return res
 
 
+MFMA_PEAK_F16 = 2.5e15
+
+
+def time_prefill(layer, dev, tokens, topk, steps, warmup, seed):
+    """Prefill-shaped layer (grouped GEMMs): us per layer over `tokens` tokens
+    with Zipf(1.1) top-k routing, fresh routing each step from a pool of 4.
+    Returns (us, algorithmic flops, algorithmic bytes, mean distinct experts)."""
+    import torch
+    from dsv4_carve_amd import ops, synth
+
+    n_exp = len(layer.bits)
+    pool = [synth.zipf_routing(tokens, n_exp, topk, seed=seed + i) for i in range(4)]
+    ids = [torch.from_numpy(p[0]).to(dev) for p in pool]
+    wts = [torch.from_numpy(p[1]).to(dev) for p in pool]
+    x = torch.from_numpy(synth.activations(tokens, layer.hidden, seed=seed)).to(dev)
+    out = torch.empty((tokens, layer.hidden), dtype=torch.float32, device=dev)
+    scratch = ops.moe_prefill_scratch(dev, tokens, layer.hidden, layer.inter, topk, n_exp)
+
+    def launch(i):
+        ops.moe_prefill(x, out, layer.tables, ids[i % 4], wts[i % 4], intermediate=layer.inter,
+                        expert_bits=layer.ebits, bits_mask=layer.mask, scratch=scratch)
+
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for i in range(steps):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / steps
+    flops = float(np.mean([2.0 * 3 * layer.hidden * layer.inter * int(((p[0] >= 0) & (p[0] < n_exp)).sum())
+                           for p in pool]))
+    nbytes = float(np.mean([step_bytes(p[0], layer.bits, layer.hidden, layer.inter) for p in pool]))
+    distinct = float(np.mean([len(set(p[0].reshape(-1).tolist())) for p in pool]))
+    return us, flops, nbytes, distinct
+
+
 C3_LAYERS = 43
 
 
@@ -364,6 +409,13 @@ def main() -> int:
         extra["tp8_slice_h4096_i256_top6"] = tp
 
     if not a.no_extra:
+        usp, fl, bp, dist = time_prefill(layer, dev, 512, TOPK, 10, 2, seed=4242)
+        extra["prefill_512_tokens_zipf1.1"] = {
+            "us_per_layer": round(usp, 1), "tokens_per_s": round(512 / (usp * 1e-6), 0),
+            "tflops": round(fl / (usp * 1e-6) / 1e12, 2), "mfma_frac_fp16": round(fl / (usp * 1e-6) / MFMA_PEAK_F16, 4),
+            "GBps": round(bp / (usp * 1e-6) / 1e9, 1), "hbm_frac": round(bp / (usp * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+            "distinct_experts": dist, "algorithmic_gflop": round(fl / 1e9, 1), "bytes": int(bp)}
+        print(f"[bench] prefill 512 tokens: {extra['prefill_512_tokens_zipf1.1']}", file=sys.stderr, flush=True)
         us3, b3 = time_stack(dev, 16, 4, 1)
         extra["stack_43_layers_routed_plus_shared_rows16"] = {
             "us_per_step": round(us3, 1), "GBps": round(b3 / (us3 * 1e-6) / 1e9, 1),

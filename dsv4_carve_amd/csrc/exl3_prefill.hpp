@@ -36,12 +36,26 @@ constexpr int PF_MAX_PAIRS = 65536;
 struct PfLayout {
     int64_t meta, eoff, toff, tile_e, tile_r0, tile_n, pair_slot, pos, Xh, GU, AD, D, total;
     int64_t max_tiles;
+    int ks_up, ks_down;     // k-splits: GU is [ks_up][2][pairs][I], D is [ks_down][pairs][H]
 };
 
 __host__ __device__ inline int64_t pf_al(int64_t v) { return (v + 255) / 256 * 256; }
 
+// k-splits of the gate/up (K = hidden) and down (K = intermediate) GEMMs: as
+// many as keep an even number of 64-row steps per part, up to 4 and 2.  Each
+// part writes its own fp32 output (the output Hadamard and svh are linear, so
+// they apply per part); the activation and gather kernels add the parts in
+// order, so results do not depend on scheduling.
+inline int pf_ksplit(int64_t K, int cap) {
+    int ks = cap;
+    while (ks > 1 && K % (2 * STEP_K * ks)) ks /= 2;
+    return ks;
+}
+
 inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
     PfLayout L;
+    L.ks_up = pf_ksplit(H, 4);
+    L.ks_down = pf_ksplit(I, 2);
     L.max_tiles = E + (pairs + PF_RB - 1) / PF_RB;
     int64_t o = 0;
     L.meta = o;      o = pf_al(o + 64);
@@ -53,9 +67,9 @@ inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
     L.pair_slot = o; o = pf_al(o + pairs * 4);
     L.pos = o;       o = pf_al(o + pairs * 4);
     L.Xh = o;        o = pf_al(o + 2 * pairs * H * 2);
-    L.GU = o;        o = pf_al(o + 2 * pairs * I * 4);
+    L.GU = o;        o = pf_al(o + (int64_t)L.ks_up * 2 * pairs * I * 4);
     L.AD = o;        o = pf_al(o + pairs * I * 2);
-    L.D = o;         o = pf_al(o + pairs * H * 4);
+    L.D = o;         o = pf_al(o + (int64_t)L.ks_down * pairs * H * 4);
     L.total = o;
     return L;
 }
@@ -123,18 +137,18 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
 // y = (H c / sqrt(128)) * svh written as fp32 to out + (row0 + i) * N.
 template <int BITS, int CB>
 __device__ __forceinline__ void pf_tile(const uint16_t* A, int row0, int nrows, const int16_t* trellis, const uint16_t* svh,
-                        int K, int N, int cb, float* out, float* tbuf) {
+                        int K, int k0, int nsteps, int N, int cb, float* out, float* tbuf) {
     const int lane = threadIdx.x;
     const int g = lane >> 4, c = lane & 15;
     const int n16 = N / 16;
-    const u32x4_t* tp = tile_ptr<BITS>(trellis, n16, 0, cb * 16);
+    const u32x4_t* tp = tile_ptr<BITS>(trellis, n16, k0 / 16, cb * 16);
     const size_t tstep = (size_t)4 * n16 * tile_vecs<BITS>();
     // A rows of this lane: c and c + 16 (zero beyond nrows); k-slice g of each
     // step.  Every load reads a valid row and a dead row is zeroed after, so
     // the loop has no branches (the accumulators stay put in registers).
     const bool live0 = c < nrows, live1 = c + 16 < nrows;
-    const u32x4_t* a0 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live0 ? c : 0)) * K + 16 * g);
-    const u32x4_t* a1 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live1 ? c + 16 : 0)) * K + 16 * g);
+    const u32x4_t* a0 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live0 ? c : 0)) * K + k0 + 16 * g);
+    const u32x4_t* a1 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live1 ? c + 16 : 0)) * K + k0 + 16 * g);
     const uint32_t m0 = live0 ? 0xffffffffu : 0u, m1 = live1 ? 0xffffffffu : 0u;
     const int astep = STEP_K / 8;        // 16-byte vectors per 64 k
 
@@ -142,7 +156,7 @@ __device__ __forceinline__ void pf_tile(const uint16_t* A, int row0, int nrows, 
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[0][i] = acc[1][i] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-    const int nsteps = K / STEP_K;       // even (K % 128 == 0)
+    // nsteps (64 k-rows each, from k0) is even
     TileRegs<BITS> t0, t1;
     u32x4_t ac[2][2];
     auto load_a = [&](int s) {
@@ -188,8 +202,8 @@ __device__ __forceinline__ void pf_tile(const uint16_t* A, int row0, int nrows, 
     }
 }
 
-// gate/up (DOWN = false): blockIdx = (tile, projection, column block of I);
-// down (DOWN = true): blockIdx = (tile, column block of H).  One launch per bit
+// gate/up (DOWN = false): blockIdx = (tile, projection, column block of I,
+// k-part); down (DOWN = true): blockIdx = (tile, column block of H, k-part).  One launch per bit
 // width present (one width per kernel keeps the registers at two waves per
 // SIMD); blocks past the planned tile count or of another width return at once.
 template <int BITS, int CB, bool DOWN>
@@ -197,21 +211,27 @@ __global__ __launch_bounds__(64) void pf_gemm_kernel(PfParams P) {
     __shared__ float tbuf[PF_RB * COLS];
     const PfLayout& L = P.L;
     const int ncb = (DOWN ? P.H : P.I) / COLS;
-    const int per_tile = DOWN ? ncb : 2 * ncb;
-    const int t = blockIdx.x / per_tile, rem = blockIdx.x - (blockIdx.x / per_tile) * per_tile;
+    const int KS = DOWN ? L.ks_down : L.ks_up;
+    const int per_tile = (DOWN ? ncb : 2 * ncb) * KS;
+    const int t = blockIdx.x / per_tile;
+    int rem = blockIdx.x - t * per_tile;
     if (t >= pat<int>(P.scratch, L.meta)[1]) return;
     const int e = pat<int>(P.scratch, L.tile_e)[t];
     if ((P.ebits ? (int)P.ebits[e] : P.bits) != BITS) return;
+    const int ks = rem % KS;
+    rem /= KS;
     const int proj = DOWN ? 0 : rem / ncb, cb = DOWN ? rem : rem - (rem / ncb) * ncb;
     const int row0 = pat<int>(P.scratch, L.tile_r0)[t];
     const int nrows = pat<int>(P.scratch, L.tile_n)[t];
     const int K = DOWN ? P.I : P.H, N = DOWN ? P.H : P.I;
+    const int kpart = K / KS;
     const uint16_t* A = DOWN ? pat<uint16_t>(P.scratch, L.AD)
                              : pat<uint16_t>(P.scratch, L.Xh) + (size_t)proj * P.P * P.H;
     const int16_t* tr = reinterpret_cast<const int16_t*>((DOWN ? P.dt : (proj ? P.ut : P.gt))[e]);
     const uint16_t* svh = reinterpret_cast<const uint16_t*>((DOWN ? P.dsv : (proj ? P.usv : P.gsv))[e]);
-    float* out = DOWN ? pat<float>(P.scratch, L.D) : pat<float>(P.scratch, L.GU) + (size_t)proj * P.P * P.I;
-    pf_tile<BITS, CB>(A, row0, nrows, tr, svh, K, N, cb, out, tbuf);
+    float* out = DOWN ? pat<float>(P.scratch, L.D) + (size_t)ks * P.P * P.H
+                      : pat<float>(P.scratch, L.GU) + ((size_t)ks * 2 + proj) * P.P * P.I;
+    pf_tile<BITS, CB>(A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out, tbuf);
 }
 
 // Launcher of the grouped GEMM for one bit width (exl3_prefill_inst.hip).

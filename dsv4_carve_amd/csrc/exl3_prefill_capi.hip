@@ -129,12 +129,17 @@ __global__ __launch_bounds__(64) void pf_act_kernel(PfParams P) {
     const int e = P.ids[pat<int>(P.scratch, L.pair_slot)[p]];
     const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I;
     const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I;
+    const size_t kstride = (size_t)2 * P.P * P.I;     // between k-parts
     const uint16_t* dsu = reinterpret_cast<const uint16_t*>(P.dsu[e]);
     uint16_t* AD = pat<uint16_t>(P.scratch, L.AD) + (size_t)p * P.I;
     const int col = 128 * (lane >> 5) + 4 * (lane & 31);
     for (int c0 = 0; c0 < P.I; c0 += COLS) {
-        const float4_t g4 = *reinterpret_cast<const float4_t*>(G + c0 + col);
-        const float4_t u4 = *reinterpret_cast<const float4_t*>(U + c0 + col);
+        float4_t g4 = *reinterpret_cast<const float4_t*>(G + c0 + col);
+        float4_t u4 = *reinterpret_cast<const float4_t*>(U + c0 + col);
+        for (int ks = 1; ks < L.ks_up; ++ks) {      // k-parts added in order
+            g4 += *reinterpret_cast<const float4_t*>(G + ks * kstride + c0 + col);
+            u4 += *reinterpret_cast<const float4_t*>(U + ks * kstride + c0 + col);
+        }
         float dv[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -168,7 +173,9 @@ __global__ __launch_bounds__(64) void pf_gather_kernel(PfParams P) {
         const int p = pos[tok * P.topk + j];
         if (p < 0) continue;
         const float wt = P.w[tok * P.topk + j];
-        const float4_t d = *reinterpret_cast<const float4_t*>(D + (size_t)p * P.H + col);
+        float4_t d = *reinterpret_cast<const float4_t*>(D + (size_t)p * P.H + col);
+        for (int ks = 1; ks < L.ks_down; ++ks)      // k-parts added in order
+            d += *reinterpret_cast<const float4_t*>(D + ((size_t)ks * P.P + p) * P.H + col);
 #pragma unroll
         for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt * d[i];
     }
@@ -266,10 +273,11 @@ int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t
     hipLaunchKernelGGL(pf_rotate_kernel, dim3(2 * P.P), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
     const int64_t tiles = P.L.max_tiles;
-    if ((rc = launch_widths(P, mask, codebook, false, (int)(tiles * 2 * (intermediate / COLS)), s))) return rc;
+    if ((rc = launch_widths(P, mask, codebook, false, (int)(tiles * 2 * (intermediate / COLS) * P.L.ks_up), s)))
+        return rc;
     hipLaunchKernelGGL(pf_act_kernel, dim3(P.P), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
-    if ((rc = launch_widths(P, mask, codebook, true, (int)(tiles * (hidden / COLS)), s))) return rc;
+    if ((rc = launch_widths(P, mask, codebook, true, (int)(tiles * (hidden / COLS) * P.L.ks_down), s))) return rc;
     hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)(tokens * (hidden / COLS))), dim3(WAVE), 0, s, P);
     return check_launch();
 }

@@ -50,6 +50,7 @@ SWIGLU_LIMIT_DEFAULT = 10.0
 AUTO_RECONSTRUCT_THRESHOLD = 144
 MAX_RECONSTRUCT_SLICE_N = 32768
 MOE_TABLE_KEYS = ops.MOE_TABLE_KEYS
+PREFILL_MAX_PAIRS = 65536
 
 
 # ---------------------------------------------------------------- linear
@@ -204,7 +205,7 @@ def moe_kernel_strict() -> int:
         return 0
 
 
-_MOE_CALLS = {"lna2": 0, "loop": 0}
+_MOE_CALLS = {"lna2": 0, "prefill": 0, "loop": 0}
 _LNA2_REJECT_LOGGED: set[str] = set()
 _LNA2_ACTIVE_LOGGED = False
 
@@ -423,11 +424,12 @@ def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
     hidden = int(getattr(layer, "_exl3_hidden_size", -1))
     inter = int(getattr(layer, "_exl3_intermediate_local", -1))
     topk = int(ids.shape[-1])
-    if (not x2d.is_cuda or x2d.dim() != 2 or not 1 <= int(x2d.shape[0]) <= lna2_max_rows()
-            or int(x2d.shape[1]) != hidden or hidden % 256 or inter % 256 or not 1 <= topk <= 8
-            or x2d.dtype not in (torch.float16, torch.bfloat16) or not float(limit) > 0.0):
-        _lna2_log_reject("geometry x=%s dtype=%s max_rows=%d hidden=%s inter=%s topk=%s limit=%s" % (
-            tuple(x2d.shape), x2d.dtype, lna2_max_rows(), hidden, inter, topk, limit))
+    rows = int(x2d.shape[0]) if x2d.dim() == 2 else -1
+    if (not x2d.is_cuda or x2d.dim() != 2 or rows < 1 or rows * topk > PREFILL_MAX_PAIRS
+            or int(x2d.shape[1]) != hidden or hidden % 256 or inter % 256 or hidden > 16384 or inter > 16384
+            or not 1 <= topk <= 9 or x2d.dtype not in (torch.float16, torch.bfloat16) or not float(limit) > 0.0):
+        _lna2_log_reject("geometry x=%s dtype=%s hidden=%s inter=%s topk=%s limit=%s" % (
+            tuple(x2d.shape), x2d.dtype, hidden, inter, topk, limit))
         return None
     ptrs = getattr(layer, "_exl3_ptrs", None)
     if not isinstance(ptrs, dict) or any(k not in ptrs for k in MOE_TABLE_KEYS):
@@ -439,13 +441,18 @@ def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
     local = map_topk_to_local(ids, len(inners), expert_map).reshape(ids.shape)
     safe_ids = local.to(torch.int32).contiguous()
     route_w = weights.reshape(local.shape).to(torch.float32).contiguous()
-    scratch = _lna2_scratch_for(layer, x2d.device)
     x_in = x2d if x2d.is_contiguous() else x2d.contiguous()
     out = torch.empty_like(x_in)
-    ops.moe_decode(x_in, out, ptrs, safe_ids, route_w, intermediate=inter,
-                   expert_bits=layer._exl3_bits_table, bits_mask=layer._exl3_bits_mask,
-                   codebook=layer._exl3_codebook, swiglu_limit=float(limit), scratch=scratch)
-    _MOE_CALLS["lna2"] += 1
+    kw = dict(intermediate=inter, expert_bits=layer._exl3_bits_table, bits_mask=layer._exl3_bits_mask,
+              codebook=layer._exl3_codebook, swiglu_limit=float(limit))
+    if rows <= lna2_max_rows():
+        ops.moe_decode(x_in, out, ptrs, safe_ids, route_w, scratch=_lna2_scratch_for(layer, x2d.device), **kw)
+        _MOE_CALLS["lna2"] += 1
+    else:
+        # many rows: the grouped-GEMM prefill path (the reference falls back to
+        # exllamav3's fused exl3_moe here, vllm_exl3_exl3.py.lna:1597-1704)
+        ops.moe_prefill(x_in, out, ptrs, safe_ids, route_w, **kw)
+        _MOE_CALLS["prefill"] += 1
     return out
 
 
@@ -476,7 +483,7 @@ def apply_exl3_experts(x, topk_ids, topk_weights, layer, *, limit: float = SWIGL
             layer._exl3_lna2_error = repr(exc)
             logger.warning("LNA2 dispatch failed; falling back: %s", exc)
         if res is not None:
-            layer._exl3_last_apply = "lna2"
+            layer._exl3_last_apply = "lna2" if int(x2d.shape[0]) <= lna2_max_rows() else "prefill"
             _lna2_log_active()
             return res.to(dtype=x.dtype).reshape(x.shape)
     out = apply_exl3_python_loop(x2d, ids, weights, inners, expert_map, limit)

@@ -169,20 +169,39 @@ def test_apply_experts_expert_map(dev, experts, monkeypatch):
         del experts.layer.expert_map
 
 
-def test_apply_experts_declines_large_batches(dev, experts, monkeypatch):
+def test_apply_experts_large_batches_use_prefill(dev, experts, monkeypatch):
+    """Above 16 rows the routed path switches to the prefill kernel (no decline,
+    so strict level 2 does not raise); the loop backend still serves them."""
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", "lna2")
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "2")
+    ids, w = synth.routing(40, 12, 6, seed=90)
+    x = synth.activations(40, 512, seed=91)
+    V.reset_moe_kernel_call_counts()
+    y = V.apply_exl3_experts(to_dev(x, dev), to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
+    assert experts.layer._exl3_last_apply == "prefill" and V.moe_kernel_call_counts()["prefill"] == 1
+    assert_close(y.float().cpu().numpy(), experts.ref(x, ids, w), max_abs=2e-2 + 8e-3)
+    monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", "loop")
+    y2 = V.apply_exl3_experts(to_dev(x, dev), to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
+    assert experts.layer._exl3_last_apply == "loop"
+    assert_close(y2.float().cpu().numpy(), experts.ref(x, ids, w), max_abs=2e-2 + 8e-3)
+
+
+def test_apply_experts_declines_bad_geometry(dev, experts, monkeypatch):
     from dsv4_carve_amd import vllm_exl3 as V
 
     monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", "lna2")
     monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "0")
-    ids, w = synth.routing(20, 12, 6, seed=90)
-    x = synth.activations(20, 512, seed=91)
-    y = V.apply_exl3_experts(to_dev(x, dev), to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
-    assert experts.layer._exl3_last_apply == "loop"
+    ids, w = synth.routing(3, 12, 6, seed=92)
+    x = synth.activations(3, 512, seed=93)
+    xf = to_dev(x, dev).float()                     # fp32 input: the kernels take fp16/bf16
+    y = V.apply_exl3_experts(xf, to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
+    assert experts.layer._exl3_last_apply == "loop" and y.dtype == xf.dtype
     assert any("geometry" in r for r in V.moe_kernel_declined_reasons())
-    assert_close(y.float().cpu().numpy(), experts.ref(x, ids, w), max_abs=2e-2 + 8e-3)
     monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "2")
     with pytest.raises(RuntimeError, match="STRICT=2"):
-        V.apply_exl3_experts(to_dev(x, dev), to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
+        V.apply_exl3_experts(xf, to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
 
 
 def test_stale_pointer_tables_decline(dev, monkeypatch):
