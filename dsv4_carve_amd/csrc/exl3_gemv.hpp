@@ -84,12 +84,17 @@ using TileRegs = TileBuf<2 * BITS>;
 template <int BITS>
 constexpr int tile_vecs() { return 2 * BITS; }      // 32*BITS bytes per tile
 
+// A lane's tile is 32*BITS contiguous bytes read as 16-byte pieces; the lanes
+// of a k-slice read neighbouring tiles, so every piece instruction touches the
+// same cache lines.  Default-policy loads keep those lines in L1 for the
+// remaining pieces (non-temporal loads re-fetch them from L2 each time, which
+// measured ~1.4x slower for the whole decode).
 template <int BITS, int CAP>
 __device__ __forceinline__ void load_tile(TileBuf<CAP>& t, const u32x4_t* p) {
     static_assert(CAP >= 2 * BITS, "tile buffer too small");
     gptr_t<u32x4_t> q = as_global(p);
 #pragma unroll
-    for (int i = 0; i < 2 * BITS; ++i) t.v[i] = __builtin_nontemporal_load(q + i);
+    for (int i = 0; i < 2 * BITS; ++i) t.v[i] = q[i];
 }
 
 // ---------------------------------------------------------------- MFMA step
