@@ -11,12 +11,19 @@
 //     block) sums them in fixed order, applies the output Hadamard + svh, the
 //     clamped SwiGLU, the down projection's suh + input Hadamard, stores the
 //     fp16 down input and publishes an epoch flag.
+//   * Gate/up tickets come from one counter per XCD class (class c hands out
+//     c, c+C, c+2C, ...; a wave draws from its own XCD's class, hardware
+//     XCC_ID, then from the others), which spreads the launch-time burst of
+//     first draws over eight counters.  Down and gather tickets come from one
+//     counter, drawn only after the drawing wave saw every class spent.
 //   * A down item spins on the flags of the column blocks it reads; a gather
-//     item on the flag of its H-block.  What it waits for has a smaller ticket,
-//     and every ticket comes from the one counter, drawn by a running wave: a
-//     smaller ticket is held by a running wave or already done, and those never
-//     wait on larger ones.  So every wait ends whatever the number of resident
-//     waves (other kernels may hold CUs; no co-residency is assumed).
+//     item on the flag of its H-block.  Gate/up items never wait, and every
+//     one of them was drawn by a running wave before any down or gather item
+//     was drawn; down and gather items wait only on items with smaller tickets
+//     of the one ordered counter (or on gate/up items).  So everything waited
+//     for is held by a running wave or done, and every wait ends whatever the
+//     number of resident waves (other kernels may hold CUs; no co-residency
+//     or dispatch order is assumed).
 //   * down items write partials; the last arriver of a (group, H-block) applies
 //     the output Hadamard + svh; the last group to finish an H-block gathers the
 //     block of `out` in top-k slot order (fp32) and casts once.
@@ -38,6 +45,10 @@ constexpr int MAX_SLOTS = MAX_M * MAX_TOPK;   // also the bound on groups and pa
 constexpr int MAX_EXPERTS = 2048;             // route-plan bitmask capacity
 constexpr int MAX_BLOCKS = 64;                // hidden/256 and intermediate/256 (both <= 16384)
 constexpr int NSTEP_CAP = 8;
+constexpr int MAX_CLASSES = 8;                // gate/up ticket classes, one per XCD
+// Gate/up ticket counters, one per class, each in its own 4 KB so concurrent
+// atomics on different classes do not serialise on one line or channel.
+constexpr int64_t CLASS_STRIDE = 4096;
 
 // Steps (64 k-rows each) per item: a power of two in 2..8 dividing k/64.  The
 // host starts from 8 and halves while the items would not give every resident
@@ -52,7 +63,7 @@ __host__ __device__ inline int item_steps(int k, int64_t units, int64_t waves) {
 
 struct Layout {
     int nI, nH, SA, SB, stepsA, stepsB;
-    int64_t ctrl, cntA, doneA, cntB, cntG, doneB, PA, DI, PB, DC, total;
+    int64_t ctrl, cls, cntA, doneA, cntB, cntG, doneB, PA, DI, PB, DC, total;
 };
 
 __host__ __device__ inline int64_t al(int64_t v) { return (v + 255) / 256 * 256; }
@@ -73,7 +84,8 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     // every counter is back at zero after a launch and every flag holds an
     // older epoch, whichever shape used the slot last.
     int64_t o = 0;
-    L.ctrl = o;  o += 256;
+    L.ctrl = o;  o += CLASS_STRIDE;
+    L.cls = o;   o += MAX_CLASSES * CLASS_STRIDE;
     L.cntA = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
     L.doneA = o; o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
     L.cntB = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
@@ -90,11 +102,13 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
 
 // Control words at the head of the scratch buffer.
 struct Ctrl {
-    int ticket;
     int retire;
     int epoch;
-    int error;
+    int error;                     // nonzero: a wait gave up (see wait_flag)
+    int later;                     // down and gather items, in order (see draw_ticket)
 };
+static_assert(sizeof(Ctrl) <= 256, "control words fit their slot");
+
 
 struct Params {
     const void* x; int x_kind;
@@ -109,6 +123,7 @@ struct Params {
     char* scratch;
     Layout L;
     int64_t trace_off;   // start of the phase-trace region (EXL3_TRACE builds)
+    int nclass;          // ticket classes: the XCD count, or 1 for small grids
 };
 
 template <typename T>
@@ -228,13 +243,50 @@ __device__ __forceinline__ int wave_atomic_add(int* p, int v) {
 
 // Spins until a device-scope flag reaches `target`.  The producer set it after
 // completing the device-scope stores it publishes, so reads that follow (also
-// device-scope) see that data.
-__device__ __forceinline__ void wait_flag(int* flag, int target) {
+// device-scope) see that data.  Every wait ends by construction (see the
+// scheduler notes at the top); the poll bound (~2^24 polls, several seconds)
+// only turns a broken invariant into an error word instead of a hung GPU.
+__device__ __forceinline__ void wait_flag(int* flag, int target, int* err) {
     if (threadIdx.x == 0) {
-        while (__hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target)
+        for (uint32_t n = 0; __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target; ++n) {
+            if (n == (1u << 24)) {
+                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
             __builtin_amdgcn_s_sleep(2);
+        }
     }
     __syncthreads();
+}
+
+// Hardware id of the XCD this wave runs on (HW_REG_XCC_ID, bits 3:0).
+__device__ __forceinline__ int xcc_id() {
+    return (int)__builtin_amdgcn_s_getreg((4 - 1) << 11 | 0 << 6 | 20) & 15;
+}
+
+// Next ticket.  Gate/up tickets [0, nA): class c hands out c, c + C, c + 2C,
+// ... (C = nclass); a wave draws from the class of its own XCD and, once that
+// is spent, from the others in turn (`home` remembers where it found work;
+// -1 once every class is spent).  Only then does it draw down and gather
+// tickets [nA, total) from the one counter `later`, in order.  So every
+// gate/up ticket is drawn, by a running wave, before the first later ticket.
+__device__ __forceinline__ int draw_ticket(Ctrl* ctrl, char* cls, int nclass, int& home, int nA, int total) {
+    if (home >= 0) {
+        for (int k = 0; k < nclass; ++k) {
+            int c = home + k;
+            if (c >= nclass) c -= nclass;
+            int* ctr = reinterpret_cast<int*>(cls + c * CLASS_STRIDE);
+            // a plain look first: a spent class costs no atomic
+            if (c + nclass * __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nA) continue;
+            const int t = c + nclass * wave_atomic_add(ctr, 1);
+            if (t < nA) {
+                home = c;
+                return t;
+            }
+        }
+        home = -1;
+    }
+    return nA + wave_atomic_add(&ctrl->later, 1);
 }
 
 __device__ __forceinline__ void reset_counter(int* p) {
@@ -361,7 +413,8 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
 
     // wait for the gate/up column blocks this chunk reads
     int* doneA = at<int>(P.scratch, L.doneA) + g * MAX_BLOCKS;
-    for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c) wait_flag(doneA + c, epoch + 1);
+    for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c)
+        wait_flag(doneA + c, epoch + 1, &at<Ctrl>(P.scratch, L.ctrl)->error);
     tr(EV_B_WAITED);
 
     const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
@@ -415,7 +468,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
 __device__ void item_g(const Params& P, const Plan& pl, int t, int epoch, Tracer& tr) {
     const Layout& L = P.L;
     const int cb = t / P.m, row = t - (t / P.m) * P.m;
-    wait_flag(at<int>(P.scratch, L.doneB) + cb, epoch + 1);
+    wait_flag(at<int>(P.scratch, L.doneB) + cb, epoch + 1, &at<Ctrl>(P.scratch, L.ctrl)->error);
     const int lane = threadIdx.x;
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
     const float* DC = at<float>(P.scratch, L.DC);
@@ -519,7 +572,11 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
 
     // Ticket order: gate/up items, down items, gather items; every ticket is
     // drawn from the counter by the wave that will run it.
-    for (int t = wave_atomic_add(&ctrl->ticket, 1); t < total; t = wave_atomic_add(&ctrl->ticket, 1)) {
+    const int nclass = P.nclass;
+    int home = nclass > 1 ? xcc_id() % nclass : 0;
+    char* cls = P.scratch + L.cls;
+    for (int t = draw_ticket(ctrl, cls, nclass, home, nA, total); t < total;
+         t = draw_ticket(ctrl, cls, nclass, home, nA, total)) {
         if (t < nA) {
             tr(EV_A_BEGIN, t);
             item_a<MASK, CB>(P, pl, xa, t, epoch, tr);
@@ -538,7 +595,10 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
     if (threadIdx.x == 0) {
         const int r = atomicAdd(&ctrl->retire, 1);
         if (r == (int)gridDim.x - 1) {
-            __hip_atomic_store(&ctrl->ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int c = 0; c < nclass; ++c)
+                __hip_atomic_store(reinterpret_cast<int*>(cls + c * CLASS_STRIDE), 0, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&ctrl->later, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&ctrl->retire, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(&ctrl->epoch, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

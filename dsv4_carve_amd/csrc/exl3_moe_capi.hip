@@ -147,6 +147,11 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
 
     const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB) + (int64_t)L.nH * m;
     const int waves = (int)(items < resident ? items : resident);
+    // one gate/up ticket class per XCD (32 CUs each on this part); any class
+    // count is correct, this one only spreads the first draws
+    const int cus = device_cus();
+    const int nxcd = (cus >= 64 && cus % 32 == 0) ? cus / 32 : 1;
+    P.nclass = nxcd <= MAX_CLASSES ? nxcd : MAX_CLASSES;
     return kInstances[idx].launch(P, waves, lds_kb, reinterpret_cast<hipStream_t>(stream));
 }
 
