@@ -351,6 +351,9 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
     }
 
 
+EXTRA_LEGS = ("sweep", "tp8", "prefill", "stack", "dense")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -359,10 +362,16 @@ def main() -> int:
     ap.add_argument("--rows", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extra", action="store_true", help="only the headline measurement")
+    ap.add_argument("--extra", default=",".join(EXTRA_LEGS),
+                    help="comma-separated extra measurements to run: " + ", ".join(EXTRA_LEGS))
     ap.add_argument("--eager", action="store_true", help="launch the timed steps one by one (no graph)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="end with one device-to-device copy of this many MiB (HBM counter calibration)")
     a = ap.parse_args()
+    legs = set() if a.no_extra else {x for x in a.extra.split(",") if x}
+    if legs - set(EXTRA_LEGS):
+        print(f"unknown --extra legs: {sorted(legs - set(EXTRA_LEGS))}", file=sys.stderr)
+        return 2
     if a.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {a.gpus}); "
               "the layer fits one MI355X and value is that GPU's throughput.", file=sys.stderr)
@@ -384,7 +393,7 @@ def main() -> int:
     print(f"[bench] rows={a.rows}: {us:.1f} us/layer, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
     extra = {}
-    if not a.no_extra:
+    if "sweep" in legs:
         sweep = {}
         for m in (1, 2, 4, 8, 16):
             u, b = time_layer(layer, dev, m, TOPK, 40, 3, seed=m)
@@ -394,6 +403,7 @@ def main() -> int:
                              "warm_us": round(uw, 2), "warm_GBps": round(bw / (uw * 1e-6) / 1e9, 1)}
             print(f"[bench] sweep m={m}: {sweep[str(m)]}", file=sys.stderr, flush=True)
         extra["rows_sweep"] = sweep
+    if "tp8" in legs:
         # The reference's own geometry: one GPU's share of the layer under TP8
         # (hidden 4096, intermediate 256, top-6, all experts at one width).
         tp = {}
@@ -408,7 +418,7 @@ def main() -> int:
             torch.cuda.empty_cache()
         extra["tp8_slice_h4096_i256_top6"] = tp
 
-    if not a.no_extra:
+    if "prefill" in legs:
         usp, fl, bp, dist = time_prefill(layer, dev, 512, TOPK, 10, 2, seed=4242)
         extra["prefill_512_tokens_zipf1.1"] = {
             "us_per_layer": round(usp, 1), "tokens_per_s": round(512 / (usp * 1e-6), 0),
@@ -416,12 +426,14 @@ def main() -> int:
             "GBps": round(bp / (usp * 1e-6) / 1e9, 1), "hbm_frac": round(bp / (usp * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "distinct_experts": dist, "algorithmic_gflop": round(fl / 1e9, 1), "bytes": int(bp)}
         print(f"[bench] prefill 512 tokens: {extra['prefill_512_tokens_zipf1.1']}", file=sys.stderr, flush=True)
+    if "stack" in legs:
         us3, b3 = time_stack(dev, 16, 4, 1)
         extra["stack_43_layers_routed_plus_shared_rows16"] = {
             "us_per_step": round(us3, 1), "GBps": round(b3 / (us3 * 1e-6) / 1e9, 1),
             "frac": round(b3 / (us3 * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes_per_step": int(b3)}
         print(f"[bench] 43-layer stack: {extra['stack_43_layers_routed_plus_shared_rows16']}", file=sys.stderr,
               flush=True)
+    if "dense" in legs:
         dense = {}
         for (k, n) in DENSE_SHAPES:
             for b in DENSE_BITS:

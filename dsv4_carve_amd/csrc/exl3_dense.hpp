@@ -186,7 +186,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     for (int m = 0; m < R; ++m) {
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         if (ok) {
-            const float4_t t = sum_partials(partials + (size_t)m * N + col, (size_t)R * N, n_kc);
+            const float4_t t = sum_partials(partials + (size_t)m * N, (uint32_t)col * 4u, (size_t)R * N, n_kc);
             v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
         }
         fwht128_x4(v);

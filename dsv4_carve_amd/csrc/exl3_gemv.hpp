@@ -202,56 +202,6 @@ __device__ __forceinline__ void st_dev4(float* p, float4_t v) {
 __device__ __forceinline__ void st_dev2(uint32_t* p, uint2 v) {
     asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
 }
-// Eight 16-byte device-scope loads issued back to back and the wait for them,
-// in one asm statement: the destinations are defined only when the data is
-// there, so the compiler cannot place a use (or a copy) of one before it.
-// Early-clobber outputs keep every destination apart from the addresses.
-__device__ __forceinline__ void ld_dev4_x8(float4_t (&v)[8], const float* const (&p)[8]) {
-    asm volatile(
-        "global_load_dwordx4 %0, %8, off sc1\n\t"
-        "global_load_dwordx4 %1, %9, off sc1\n\t"
-        "global_load_dwordx4 %2, %10, off sc1\n\t"
-        "global_load_dwordx4 %3, %11, off sc1\n\t"
-        "global_load_dwordx4 %4, %12, off sc1\n\t"
-        "global_load_dwordx4 %5, %13, off sc1\n\t"
-        "global_load_dwordx4 %6, %14, off sc1\n\t"
-        "global_load_dwordx4 %7, %15, off sc1\n\t"
-        "s_waitcnt vmcnt(0)"
-        : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]), "=&v"(v[6]),
-          "=&v"(v[7])
-        : "v"(p[0]), "v"(p[1]), "v"(p[2]), "v"(p[3]), "v"(p[4]), "v"(p[5]), "v"(p[6]), "v"(p[7])
-        : "memory");
-}
-
-// Sixteen such loads (two sets of eight) and one wait, as above.
-__device__ __forceinline__ void ld_dev4_x16(float4_t (&a)[8], float4_t (&b)[8], const float* const (&pa)[8],
-                                            const float* const (&pb)[8]) {
-    asm volatile(
-        "global_load_dwordx4 %0, %16, off sc1\n\t"
-        "global_load_dwordx4 %1, %17, off sc1\n\t"
-        "global_load_dwordx4 %2, %18, off sc1\n\t"
-        "global_load_dwordx4 %3, %19, off sc1\n\t"
-        "global_load_dwordx4 %4, %20, off sc1\n\t"
-        "global_load_dwordx4 %5, %21, off sc1\n\t"
-        "global_load_dwordx4 %6, %22, off sc1\n\t"
-        "global_load_dwordx4 %7, %23, off sc1\n\t"
-        "global_load_dwordx4 %8, %24, off sc1\n\t"
-        "global_load_dwordx4 %9, %25, off sc1\n\t"
-        "global_load_dwordx4 %10, %26, off sc1\n\t"
-        "global_load_dwordx4 %11, %27, off sc1\n\t"
-        "global_load_dwordx4 %12, %28, off sc1\n\t"
-        "global_load_dwordx4 %13, %29, off sc1\n\t"
-        "global_load_dwordx4 %14, %30, off sc1\n\t"
-        "global_load_dwordx4 %15, %31, off sc1\n\t"
-        "s_waitcnt vmcnt(0)"
-        : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(a[4]), "=&v"(a[5]), "=&v"(a[6]),
-          "=&v"(a[7]), "=&v"(b[0]), "=&v"(b[1]), "=&v"(b[2]), "=&v"(b[3]), "=&v"(b[4]), "=&v"(b[5]),
-          "=&v"(b[6]), "=&v"(b[7])
-        : "v"(pa[0]), "v"(pa[1]), "v"(pa[2]), "v"(pa[3]), "v"(pa[4]), "v"(pa[5]), "v"(pa[6]), "v"(pa[7]),
-          "v"(pb[0]), "v"(pb[1]), "v"(pb[2]), "v"(pb[3]), "v"(pb[4]), "v"(pb[5]), "v"(pb[6]), "v"(pb[7])
-        : "memory");
-}
-
 // Completes this wave's outstanding memory operations (its device-scope data
 // stores included) before anything that follows, e.g. the counter or flag
 // update that hands the data to another wave.
@@ -259,24 +209,43 @@ __device__ __forceinline__ void publish_fence() {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 }
 
-// Sums two independent sets of `count` partials (a and b) in index order with
-// up to 16 loads in flight (8 of each per batch).
-__device__ __forceinline__ void sum_partials2(const float* a, const float* b, size_t stride, int count,
-                                              float4_t& sa, float4_t& sb) {
+// Device-scope 16-byte loads through a raw buffer resource.  The sc1 policy
+// makes them coherent at device scope, like the sc1 stores above; unlike
+// an asm block, the compiler tracks their completion itself, so a batch of any
+// size is in flight at once and each value is waited for where it is used.
+// The base address must be uniform across the wave; the lane's offset goes in
+// `voff` and a per-load offset in `soff` (bytes, below 2 GiB in total).
+constexpr int CPOL_SC1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float4_t ld_dev4_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL_SC1));
+}
+// No memory access is moved across this point by the compiler (loads that
+// read published data stay after the counter or flag that published it).
+__device__ __forceinline__ void compiler_barrier() { asm volatile("" ::: "memory"); }
+
+// Sums two independent sets of `count` fp32 partial vectors in index order:
+// a[i * stride], b[i * stride] at byte offset `voff` (the lane's columns) from
+// the uniform bases a and b.  Up to 32 loads (16 of each) are in flight.
+__device__ __forceinline__ void sum_partials2(const float* a, const float* b, uint32_t voff, size_t stride,
+                                              int count, float4_t& sa, float4_t& sb) {
+    compiler_barrier();
+    const __amdgpu_buffer_rsrc_t ra = dev_rsrc(a), rb = dev_rsrc(b);
+    const uint32_t st = (uint32_t)(stride * sizeof(float));
     sa = float4_t{0.f, 0.f, 0.f, 0.f};
     sb = sa;
-    for (int i0 = 0; i0 < count; i0 += 8) {
-        float4_t va[8], vb[8];
-        const float* qa[8];
-        const float* qb[8];
+    for (int i0 = 0; i0 < count; i0 += 16) {
+        float4_t va[16], vb[16];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            qa[j] = a + (size_t)min(i0 + j, count - 1) * stride;
-            qb[j] = b + (size_t)min(i0 + j, count - 1) * stride;
-        }
-        ld_dev4_x16(va, vb, qa, qb);
+        for (int j = 0; j < 16; ++j)
+            if (i0 + j < count) {
+                va[j] = ld_dev4_buf(ra, voff, (uint32_t)(i0 + j) * st);
+                vb[j] = ld_dev4_buf(rb, voff, (uint32_t)(i0 + j) * st);
+            }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 16; ++j)
             if (i0 + j < count) {
                 sa += va[j];
                 sb += vb[j];
@@ -284,18 +253,20 @@ __device__ __forceinline__ void sum_partials2(const float* a, const float* b, si
     }
 }
 
-// Sums `count` fp32 partial vectors p[i * stride] (float4 per lane) in index
-// order; loads are issued in batches of 8 so their latencies overlap.
-__device__ __forceinline__ float4_t sum_partials(const float* p, size_t stride, int count) {
+// Sums `count` fp32 partial vectors p[i * stride] at byte offset `voff` from
+// the uniform base p, in index order, with up to 32 loads in flight.
+__device__ __forceinline__ float4_t sum_partials(const float* p, uint32_t voff, size_t stride, int count) {
+    compiler_barrier();
+    const __amdgpu_buffer_rsrc_t r = dev_rsrc(p);
+    const uint32_t st = (uint32_t)(stride * sizeof(float));
     float4_t acc = {0.f, 0.f, 0.f, 0.f};
-    for (int i0 = 0; i0 < count; i0 += 8) {
-        float4_t v[8];
-        const float* q[8];
+    for (int i0 = 0; i0 < count; i0 += 32) {
+        float4_t v[32];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) q[j] = p + (size_t)min(i0 + j, count - 1) * stride;
-        ld_dev4_x8(v, q);
+        for (int j = 0; j < 32; ++j)
+            if (i0 + j < count) v[j] = ld_dev4_buf(r, voff, (uint32_t)(i0 + j) * st);
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 32; ++j)
             if (i0 + j < count) acc += v[j];
     }
     return acc;

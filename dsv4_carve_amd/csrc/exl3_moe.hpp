@@ -4,7 +4,7 @@
 // recipe-lna/lna2/lna_moe_ticket.cu:5-12).
 //
 // Scheduler (re-derived for 256 CUs, no grid barrier, no co-residency assumption):
-//   * Persistent single-wave workgroups draw tickets from one atomic counter.
+//   * Persistent single-wave workgroups run items in ticket order.
 //   * Ticket order: every gate/up item of every active expert, then every
 //     down item.  Item = (expert group, projection, 256-column block, k-chunk).
 //   * gate/up items write fp32 partials; the last arriver of a (group, column
@@ -24,6 +24,12 @@
 //     for is held by a running wave or done, and every wait ends whatever the
 //     number of resident waves (other kernels may hold CUs; no co-residency
 //     or dispatch order is assumed).
+//   * A wave draws its next ticket while it finishes the current item, but
+//     only once that item is past its last wait: the item it holds ahead
+//     starts after a finite amount of work, so the argument above still holds
+//     (the smallest unfinished ticket is always some wave's current item, and
+//     everything it waits for is smaller).  The first ticket is drawn while
+//     the route plan is built.
 //   * down items write partials; the last arriver of a (group, H-block) applies
 //     the output Hadamard + svh; the last group to finish an H-block gathers the
 //     block of `out` in top-k slot order (fp32) and casts once.
@@ -49,6 +55,8 @@ constexpr int MAX_CLASSES = 8;                // gate/up ticket classes, one per
 // Gate/up ticket counters, one per class, each in its own 4 KB so concurrent
 // atomics on different classes do not serialise on one line or channel.
 constexpr int64_t CLASS_STRIDE = 4096;
+// Each completion counter and flag in its own 256 bytes.
+constexpr int64_t WORD_STRIDE = 256;
 
 // Steps (64 k-rows each) per item: a power of two in 2..8 dividing k/64.  The
 // host starts from 8 and halves while the items would not give every resident
@@ -84,13 +92,13 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     // every counter is back at zero after a launch and every flag holds an
     // older epoch, whichever shape used the slot last.
     int64_t o = 0;
-    L.ctrl = o;  o += CLASS_STRIDE;
+    L.ctrl = o;  o += 3 * CLASS_STRIDE;
     L.cls = o;   o += MAX_CLASSES * CLASS_STRIDE;
-    L.cntA = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
-    L.doneA = o; o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
-    L.cntB = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * 4;
-    L.cntG = o;  o += (int64_t)MAX_BLOCKS * 4;
-    L.doneB = o; o += (int64_t)MAX_BLOCKS * 4;
+    L.cntA = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * WORD_STRIDE;
+    L.doneA = o; o += (int64_t)MAX_SLOTS * MAX_BLOCKS * WORD_STRIDE;
+    L.cntB = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * WORD_STRIDE;
+    L.cntG = o;  o += (int64_t)MAX_BLOCKS * WORD_STRIDE;
+    L.doneB = o; o += (int64_t)MAX_BLOCKS * WORD_STRIDE;
     o = al(o);
     L.PA = o;    o = al(o + P * 2 * L.SA * I * 4);
     L.DI = o;    o = al(o + P * I * 2);
@@ -100,14 +108,17 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     return L;
 }
 
-// Control words at the head of the scratch buffer.
+// Control words at the head of the scratch buffer.  The two counters every
+// wave updates sit 4 KB apart and away from the words that are only read.
 struct Ctrl {
-    int retire;
     int epoch;
     int error;                     // nonzero: a wait gave up (see wait_flag)
+    int pad0[1022];
     int later;                     // down and gather items, in order (see draw_ticket)
+    int pad1[1023];
+    int retire;
 };
-static_assert(sizeof(Ctrl) <= 256, "control words fit their slot");
+static_assert(sizeof(Ctrl) <= 3 * CLASS_STRIDE, "control words fit their slot");
 
 
 struct Params {
@@ -128,6 +139,10 @@ struct Params {
 
 template <typename T>
 __device__ __forceinline__ T* at(char* base, int64_t off) { return reinterpret_cast<T*>(base + off); }
+// Counter or flag i of the array at `off` (one per WORD_STRIDE bytes).
+__device__ __forceinline__ int* word(char* base, int64_t off, int i) {
+    return reinterpret_cast<int*>(base + off + (int64_t)i * WORD_STRIDE);
+}
 
 // ---------------------------------------------------------------- phase tracing
 //
@@ -141,7 +156,7 @@ constexpr int TRACE_EVENTS = 128;
 constexpr int TRACE_WAVES = 4096;
 enum TraceEvent : uint32_t {
     EV_START = 1, EV_PLAN, EV_A_BEGIN, EV_A_MMA, EV_A_END, EV_EPI_A_END, EV_B_BEGIN, EV_B_WAITED,
-    EV_B_MMA, EV_B_END, EV_EPI_B_END, EV_GATHER_END, EV_RETIRE
+    EV_B_MMA, EV_B_END, EV_EPI_B_END, EV_GATHER_END, EV_RETIRE, EV_STORED, EV_FENCED
 };
 inline int64_t trace_bytes() { return EXL3_TRACE ? (int64_t)TRACE_WAVES * TRACE_EVENTS * 8 + 256 : 0; }
 
@@ -246,6 +261,9 @@ __device__ __forceinline__ int wave_atomic_add(int* p, int v) {
 // device-scope) see that data.  Every wait ends by construction (see the
 // scheduler notes at the top); the poll bound (~2^24 polls, several seconds)
 // only turns a broken invariant into an error word instead of a hung GPU.
+#ifndef EXL3_POLL_SLEEP
+#define EXL3_POLL_SLEEP 2
+#endif
 __device__ __forceinline__ void wait_flag(int* flag, int target, int* err) {
     if (threadIdx.x == 0) {
         for (uint32_t n = 0; __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target; ++n) {
@@ -253,7 +271,7 @@ __device__ __forceinline__ void wait_flag(int* flag, int target, int* err) {
                 __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
-            __builtin_amdgcn_s_sleep(2);
+            __builtin_amdgcn_s_sleep(EXL3_POLL_SLEEP);
         }
     }
     __syncthreads();
@@ -271,23 +289,63 @@ __device__ __forceinline__ int xcc_id() {
 // tickets [nA, total) from the one counter `later`, in order.  So every
 // gate/up ticket is drawn, by a running wave, before the first later ticket.
 __device__ __forceinline__ int draw_ticket(Ctrl* ctrl, char* cls, int nclass, int& home, int nA, int total) {
-    if (home >= 0) {
-        for (int k = 0; k < nclass; ++k) {
-            int c = home + k;
-            if (c >= nclass) c -= nclass;
-            int* ctr = reinterpret_cast<int*>(cls + c * CLASS_STRIDE);
-            // a plain look first: a spent class costs no atomic
-            if (c + nclass * __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= nA) continue;
-            const int t = c + nclass * wave_atomic_add(ctr, 1);
-            if (t < nA) {
-                home = c;
-                return t;
-            }
+    while (home >= 0) {
+        // One look at every class, the loads in flight together: a spent
+        // class costs no atomic.  A failed atomic leaves its class spent for
+        // good, so this loop ends after at most nclass draws.
+        int v[MAX_CLASSES];
+#pragma unroll
+        for (int k = 0; k < MAX_CLASSES; ++k)
+            if (k < nclass)
+                v[k] = __hip_atomic_load(reinterpret_cast<int*>(cls + k * CLASS_STRIDE), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t avail = 0;
+#pragma unroll
+        for (int k = 0; k < MAX_CLASSES; ++k)
+            if (k < nclass && k + nclass * v[k] < nA) avail |= 1u << k;
+        if (!avail) {
+            home = -1;
+            break;
         }
-        home = -1;
+        const uint32_t from_home = avail >> home;       // first open class at or after home, cyclically
+        const int c = from_home ? home + __ffs((int)from_home) - 1 : __ffs((int)avail) - 1;
+        const int t = c + nclass * wave_atomic_add(reinterpret_cast<int*>(cls + c * CLASS_STRIDE), 1);
+        if (t < nA) {
+            home = c;
+            return t;
+        }
     }
     return nA + wave_atomic_add(&ctrl->later, 1);
 }
+
+// The next ticket, drawn while the current item runs.  A gate/up item (which
+// never waits) draws at its start; a down item once its waits are over.  So
+// the draw's latency overlaps the item, and a ticket held ahead never waits
+// behind a wait of its holder.  A wave on a gate/up item draws from its
+// class; a wave past every class draws from `later`, in order, as draw_ticket
+// would.  `want` is set by the scheduler only while enough tickets remain
+// that the draw is likely to succeed (an empty draw is one more atomic on a
+// contended counter).  The value is read after the item.
+struct NextTicket {
+    int* ctr = nullptr;      // counter drawn from, null if none was issued
+    bool later = false;
+    bool want = false;
+    int old = 0;
+    __device__ __forceinline__ void issue(Ctrl* ctrl, char* cls, int home) {
+        if (!want) return;
+        later = home < 0;
+        ctr = later ? &ctrl->later : reinterpret_cast<int*>(cls + home * CLASS_STRIDE);
+        if (threadIdx.x == 0) old = atomicAdd(ctr, 1);
+    }
+    // The drawn ticket, or -1 when none was drawn or the class was spent.
+    __device__ __forceinline__ int take(int home, int nclass, int nA) {
+        if (!ctr) return -1;
+        const int v = __shfl(old, 0, WAVE);
+        const int t = later ? nA + v : home + nclass * v;
+        ctr = nullptr;
+        return later || t < nA ? t : -1;
+    }
+};
 
 __device__ __forceinline__ void reset_counter(int* p) {
     if (threadIdx.x == 0) __hip_atomic_store(p, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -320,7 +378,7 @@ __device__ __forceinline__ void load_half4(uint16_t (&v)[4], int64_t addr, int c
 // gate/up item: (group g, projection p, 256-column block cb, k-chunk kc)
 template <int B, int CB>
 __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int p, int cb, int kc,
-                            int epoch, Tracer& tr) {
+                            int epoch, Tracer& tr, NextTicket& nt, int home) {
     const Layout& L = P.L;
     const int e = pl.gexp[g], pb = pl.gpair[g];
     const uint32_t mask = pl.gmask[g];
@@ -328,6 +386,7 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     const int kchunk = L.stepsA * STEP_K;
     const int k0 = kc * kchunk;
 
+    nt.issue(at<Ctrl>(P.scratch, L.ctrl), P.scratch + L.cls, home);
     // step-0 weights are in flight while the input rotation runs
     const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]), P.I / 16, k0 / 16,
                                     cb * 16);
@@ -350,8 +409,10 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     const size_t ld = (size_t)2 * L.SA * P.I;
     store_partials(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, ld, R, COLS,
                    reinterpret_cast<float*>(xa));
+    tr(EV_STORED);
     publish_fence();
-    int* cnt = at<int>(P.scratch, L.cntA) + g * MAX_BLOCKS + cb;
+    tr(EV_FENCED);
+    int* cnt = word(P.scratch, L.cntA, g * MAX_BLOCKS + cb);
     const bool last = wave_atomic_add(cnt, 1) == 2 * L.SA - 1;
     tr(EV_A_END, last);
     if (!last) return;
@@ -368,8 +429,8 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     for (int r = 0; r < R; ++r) {
         const int pair = pb + r;
         float4_t ga, ua;
-        sum_partials2(PA + (size_t)(pair * 2 + 0) * L.SA * P.I + col, PA + (size_t)(pair * 2 + 1) * L.SA * P.I + col,
-                      P.I, L.SA, ga, ua);
+        sum_partials2(PA + (size_t)(pair * 2 + 0) * L.SA * P.I, PA + (size_t)(pair * 2 + 1) * L.SA * P.I,
+                      (uint32_t)col * 4u, P.I, L.SA, ga, ua);
         float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
         fwht128_x4(gv);
         fwht128_x4(uv);
@@ -391,7 +452,7 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     reset_counter(cnt);
     publish_fence();
     if (lane == 0)
-        __hip_atomic_store(at<int>(P.scratch, L.doneA) + g * MAX_BLOCKS + cb, epoch + 1, __ATOMIC_RELAXED,
+        __hip_atomic_store(word(P.scratch, L.doneA, g * MAX_BLOCKS + cb), epoch + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     tr(EV_EPI_A_END);
 }
@@ -399,7 +460,7 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
 // down item: (group g, 256-column block cb of hidden, k-chunk kc of intermediate)
 template <int B, int CB>
 __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int cb, int kc, int epoch,
-                            Tracer& tr) {
+                            Tracer& tr, NextTicket& nt) {
     const Layout& L = P.L;
     const int e = pl.gexp[g], pb = pl.gpair[g];
     const uint32_t mask = pl.gmask[g];
@@ -412,10 +473,10 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     load_tile<B>(first, tp);
 
     // wait for the gate/up column blocks this chunk reads
-    int* doneA = at<int>(P.scratch, L.doneA) + g * MAX_BLOCKS;
     for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c)
-        wait_flag(doneA + c, epoch + 1, &at<Ctrl>(P.scratch, L.ctrl)->error);
+        wait_flag(word(P.scratch, L.doneA, g * MAX_BLOCKS + c), epoch + 1, &at<Ctrl>(P.scratch, L.ctrl)->error);
     tr(EV_B_WAITED);
+    nt.issue(at<Ctrl>(P.scratch, L.ctrl), P.scratch + L.cls, -1);
 
     const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
     for (int r = 0; r < R; ++r) copy_row(DI + (size_t)(pb + r) * P.I + k0, xa, r, kchunk / 128, NSTEP_CAP);
@@ -428,8 +489,10 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     float* PB = at<float>(P.scratch, L.PB);
     store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS,
                    reinterpret_cast<float*>(xa));
+    tr(EV_STORED);
     publish_fence();
-    int* cnt = at<int>(P.scratch, L.cntB) + g * MAX_BLOCKS + cb;
+    tr(EV_FENCED);
+    int* cnt = word(P.scratch, L.cntB, g * MAX_BLOCKS + cb);
     const bool last = wave_atomic_add(cnt, 1) == L.SB - 1;
     tr(EV_B_END, last);
     if (!last) return;
@@ -442,7 +505,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     float* DC = at<float>(P.scratch, L.DC);
     for (int r = 0; r < R; ++r) {
         const int pair = pb + r;
-        const float4_t t = sum_partials(PB + (size_t)pair * L.SB * P.H + col, P.H, L.SB);
+        const float4_t t = sum_partials(PB + (size_t)pair * L.SB * P.H, (uint32_t)col * 4u, P.H, L.SB);
         float v[4] = {t[0], t[1], t[2], t[3]};
         fwht128_x4(v);
         float4_t o;
@@ -452,7 +515,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     }
     reset_counter(cnt);
     publish_fence();
-    int* cg = at<int>(P.scratch, L.cntG) + cb;
+    int* cg = word(P.scratch, L.cntG, cb);
     const bool done = wave_atomic_add(cg, 1) == pl.U - 1;
     tr(EV_EPI_B_END, done);
     if (!done) return;
@@ -460,7 +523,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     reset_counter(cg);
     publish_fence();
     if (lane == 0)
-        __hip_atomic_store(at<int>(P.scratch, L.doneB) + cb, epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(word(P.scratch, L.doneB, cb), epoch + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // gather item: (H block cb, row) -- out[row][block] = sum over the row's top-k
@@ -468,28 +531,26 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
 __device__ void item_g(const Params& P, const Plan& pl, int t, int epoch, Tracer& tr) {
     const Layout& L = P.L;
     const int cb = t / P.m, row = t - (t / P.m) * P.m;
-    wait_flag(at<int>(P.scratch, L.doneB) + cb, epoch + 1, &at<Ctrl>(P.scratch, L.ctrl)->error);
+    wait_flag(word(P.scratch, L.doneB, cb), epoch + 1, &at<Ctrl>(P.scratch, L.ctrl)->error);
     const int lane = threadIdx.x;
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    const float* DC = at<float>(P.scratch, L.DC);
-    static_assert(MAX_TOPK <= 16, "one batch of slot loads");
-    float4_t d[2][8];
-    float wt[16];
-    const float* q[2][8];
+    compiler_barrier();
+    const __amdgpu_buffer_rsrc_t dc = dev_rsrc(at<float>(P.scratch, L.DC));
+    float4_t d[MAX_TOPK];
+    float wt[MAX_TOPK];
+    int pr[MAX_TOPK];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {             // every slot's load issued first
-        const int pair = j < P.topk ? pl.slotpair[row * P.topk + j] : -1;
-        wt[j] = pair >= 0 ? P.w[row * P.topk + j] : 0.f;
-        q[j >> 3][j & 7] = DC + (size_t)(pair >= 0 ? pair : 0) * P.H + col;
+    for (int j = 0; j < MAX_TOPK; ++j) {       // every slot's load issued first
+        pr[j] = j < P.topk ? pl.slotpair[row * P.topk + j] : -1;
+        wt[j] = pr[j] >= 0 ? P.w[row * P.topk + j] : 0.f;
+        if (pr[j] >= 0) d[j] = ld_dev4_buf(dc, (uint32_t)col * 4u, (uint32_t)pr[j] * (uint32_t)P.H * 4u);
     }
-    if (P.topk <= 8) ld_dev4_x8(d[0], q[0]);
-    else ld_dev4_x16(d[0], d[1], q[0], q[1]);
     float s4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < MAX_TOPK; ++j) {       // fp32 sum in top-k slot order
-        if (j >= P.topk || pl.slotpair[row * P.topk + j] < 0) continue;
+        if (pr[j] < 0) continue;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[j >> 3][j & 7][i];
+        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[j][i];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
@@ -514,7 +575,8 @@ __device__ __forceinline__ void dispatch_bits(int bits, int* err, F&& body) {
 }
 
 template <uint32_t MASK, int CB>
-__device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch, Tracer& tr) {
+__device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch, Tracer& tr, NextTicket& nt,
+                       int home) {
     const Layout& L = P.L;
     const int per_g = 2 * L.nI * L.SA;
     const int g = t / per_g;
@@ -523,19 +585,19 @@ __device__ void item_a(const Params& P, const Plan& pl, uint16_t* xa, int t, int
     rem -= p * L.nI * L.SA;
     const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
     dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
-        item_a_body<decltype(BI)::value, CB>(P, pl, xa, g, p, cb, kc, epoch, tr);
+        item_a_body<decltype(BI)::value, CB>(P, pl, xa, g, p, cb, kc, epoch, tr, nt, home);
     });
 }
 
 template <uint32_t MASK, int CB>
-__device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch, Tracer& tr) {
+__device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int epoch, Tracer& tr, NextTicket& nt) {
     const Layout& L = P.L;
     const int per_g = L.nH * L.SB;
     const int g = t / per_g;
     const int rem = t - g * per_g;
     const int cb = rem / L.SB, kc = rem - (rem / L.SB) * L.SB;
     dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
-        item_b_body<decltype(BI)::value, CB>(P, pl, xa, g, cb, kc, epoch, tr);
+        item_b_body<decltype(BI)::value, CB>(P, pl, xa, g, cb, kc, epoch, tr, nt);
     });
 }
 
@@ -549,7 +611,7 @@ inline int moe_lds_kb(int64_t m, int64_t n_experts) {
 }
 
 template <uint32_t MASK, int CB>
-__global__ __launch_bounds__(64) void moe_kernel(Params P) {
+__global__ __launch_bounds__(64, 2) void moe_kernel(Params P) {   // 2 waves per SIMD: <= 256 registers
     extern __shared__ __align__(16) uint16_t xa[];   // moe_lds_kb(m, E) KB
     __shared__ Plan pl;
     const Layout& L = P.L;
@@ -558,6 +620,14 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
     tr(EV_START);
     Ctrl* ctrl = at<Ctrl>(P.scratch, L.ctrl);
     const int epoch = __hip_atomic_load(&ctrl->epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int nclass = P.nclass;
+    int home = nclass > 1 ? xcc_id() % nclass : 0;
+    char* cls = P.scratch + L.cls;
+    // The first ticket is drawn from this wave's class while the plan is built
+    // (a ticket past the gate/up items only means the class is spent).
+    NextTicket nt;
+    nt.want = true;
+    nt.issue(ctrl, cls, home);
 
     build_plan(P, pl, reinterpret_cast<char*>(xa));
     tr(EV_PLAN);
@@ -572,21 +642,23 @@ __global__ __launch_bounds__(64) void moe_kernel(Params P) {
 
     // Ticket order: gate/up items, down items, gather items; every ticket is
     // drawn from the counter by the wave that will run it.
-    const int nclass = P.nclass;
-    int home = nclass > 1 ? xcc_id() % nclass : 0;
-    char* cls = P.scratch + L.cls;
-    for (int t = draw_ticket(ctrl, cls, nclass, home, nA, total); t < total;
-         t = draw_ticket(ctrl, cls, nclass, home, nA, total)) {
+    int t = nt.take(home, nclass, nA);
+    if (t < 0) t = draw_ticket(ctrl, cls, nclass, home, nA, total);
+    const int ahead = (int)gridDim.x;      // draw ahead while this many tickets remain beyond t
+    while (t < total) {
+        nt.want = t + ahead < (t < nA ? nA : total);
         if (t < nA) {
             tr(EV_A_BEGIN, t);
-            item_a<MASK, CB>(P, pl, xa, t, epoch, tr);
+            item_a<MASK, CB>(P, pl, xa, t, epoch, tr, nt, home);
         } else if (t < nAB) {
             tr(EV_B_BEGIN, t - nA);
-            item_b<MASK, CB>(P, pl, xa, t - nA, epoch, tr);
+            item_b<MASK, CB>(P, pl, xa, t - nA, epoch, tr, nt);
         } else {
             item_g(P, pl, t - nAB, epoch, tr);
         }
         __syncthreads();   // xa is rewritten by the next item
+        t = nt.take(home, nclass, nA);
+        if (t < 0) t = draw_ticket(ctrl, cls, nclass, home, nA, total);
     }
 
     // Retire; the last wave out resets the queue and advances the epoch.
