@@ -166,7 +166,7 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     __syncthreads();
 
     float4_t acc[16];
-    mma_steps<BITS, CB>(first, tp, N / 16, nsteps, xa, GEMV_NSTEP_CAP, R, acc);
+    mma_steps<BITS, CB, false>(first, tp, N / 16, nsteps, xa, GEMV_NSTEP_CAP, R, acc);
 
     const int cols = min(COLS, N - cb * COLS);
     store_partials(acc, partials + (size_t)kc * R * N + cb * COLS, N, R, cols, reinterpret_cast<float*>(xa));

@@ -146,7 +146,13 @@ __device__ __forceinline__ const u32x4_t* tile_ptr(const int16_t* trellis, int n
 // caller with load_tile(first, tile_ptr(...)) so the loads overlap whatever the
 // caller does meanwhile).  xa: LDS A tile for this item (see xa_index).  Lanes
 // whose n-tile is past the matrix decode a valid tile; their columns are dropped.
-template <int BITS, int CB, int CAP>
+// AHEAD: the load two steps ahead is issued unconditionally (the last
+// iteration reloads the last step, which L1/L2 still hold).  Behind a branch,
+// the compiler's wait before the next step's decode has to cover both paths
+// and waits for those loads as soon as they are issued; unconditional, they
+// stay in flight, at the price of the registers that keeps live (the short
+// dense chunks keep more waves resident without it).
+template <int BITS, int CB, bool AHEAD, int CAP>
 __device__ __forceinline__ void mma_steps(TileBuf<CAP>& first, const u32x4_t* p, int n16, int nsteps,
                                           const uint16_t* xa, int nsteps_cap, int R, float4_t (&acc)[16]) {
     const int lane = threadIdx.x & (WAVE - 1);
@@ -167,7 +173,8 @@ __device__ __forceinline__ void mma_steps(TileBuf<CAP>& first, const u32x4_t* p,
             for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, c, s, nsteps_cap, g, r, live);
             mma_tile<BITS, CB>(first.words(), A, acc);
         }
-        if (s + 2 < nsteps) load_tile<BITS>(first, p + (s + 2) * step);
+        if constexpr (AHEAD) load_tile<BITS>(first, p + min(s + 2, nsteps - 1) * step);
+        else if (s + 2 < nsteps) load_tile<BITS>(first, p + (s + 2) * step);
         {
             half8_t A[4];
 #pragma unroll

@@ -402,7 +402,7 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     __syncthreads();
 
     float4_t acc[16];
-    mma_steps<B, CB>(first, tp, P.I / 16, L.stepsA, xa, NSTEP_CAP, R, acc);
+    mma_steps<B, CB, true>(first, tp, P.I / 16, L.stepsA, xa, NSTEP_CAP, R, acc);
     tr(EV_A_MMA);
 
     float* PA = at<float>(P.scratch, L.PA);
@@ -483,7 +483,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     __syncthreads();
 
     float4_t acc[16];
-    mma_steps<B, CB>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
+    mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
     tr(EV_B_MMA);
 
     float* PB = at<float>(P.scratch, L.PB);
