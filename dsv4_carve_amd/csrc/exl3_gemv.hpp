@@ -100,15 +100,14 @@ __device__ __forceinline__ void load_tile(TileBuf<CAP>& t, const u32x4_t* p) {
 // ---------------------------------------------------------------- MFMA step
 
 // Builds the duplicated A operand for k-group r of this lane from the LDS tile.
-__device__ __forceinline__ half8_t a_operand(const uint16_t* xa, int m, int s, int nsteps_cap,
-                                             int g, int r, bool live) {
-    uint2 v = make_uint2(0u, 0u);
-    if (live) v = *reinterpret_cast<const uint2*>(xa + ((m * nsteps_cap + s) * 4 + g) * 16 + r * 4);
+__device__ __forceinline__ half8_t a_operand(const uint16_t* xa, int m, int s, int nsteps_cap, int g, int r) {
+    const uint2 v = *reinterpret_cast<const uint2*>(xa + ((m * nsteps_cap + s) * 4 + g) * 16 + r * 4);
+    // one byte permute per register: (lo, lo) and (hi, hi) of each word
     u32x4_t d;
-    d[0] = (v.x & 0xffffu) | (v.x << 16);
-    d[1] = (v.x >> 16) | (v.x & 0xffff0000u);
-    d[2] = (v.y & 0xffffu) | (v.y << 16);
-    d[3] = (v.y >> 16) | (v.y & 0xffff0000u);
+    d[0] = __builtin_amdgcn_perm(v.x, v.x, 0x01000100u);
+    d[1] = __builtin_amdgcn_perm(v.x, v.x, 0x03020302u);
+    d[2] = __builtin_amdgcn_perm(v.y, v.y, 0x01000100u);
+    d[3] = __builtin_amdgcn_perm(v.y, v.y, 0x03020302u);
     return __builtin_bit_cast(half8_t, d);
 }
 
@@ -158,7 +157,8 @@ __device__ __forceinline__ void mma_steps(TileBuf<CAP>& first, const u32x4_t* p,
     const int lane = threadIdx.x & (WAVE - 1);
     const int g = lane >> 4, c = lane & 15;
     const size_t step = (size_t)4 * n16 * tile_vecs<BITS>();
-    const bool live = c < R;
+    // A rows >= R repeat row R-1 (a valid row, no branch): their outputs are never stored
+    const int arow = min(c, R - 1);
 
 #pragma unroll
     for (int i = 0; i < 16; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -170,7 +170,7 @@ __device__ __forceinline__ void mma_steps(TileBuf<CAP>& first, const u32x4_t* p,
         {
             half8_t A[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, c, s, nsteps_cap, g, r, live);
+            for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, arow, s, nsteps_cap, g, r);
             mma_tile<BITS, CB>(first.words(), A, acc);
         }
         if constexpr (AHEAD) load_tile<BITS>(first, p + min(s + 2, nsteps - 1) * step);
@@ -178,7 +178,7 @@ __device__ __forceinline__ void mma_steps(TileBuf<CAP>& first, const u32x4_t* p,
         {
             half8_t A[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, c, s + 1, nsteps_cap, g, r, live);
+            for (int r = 0; r < 4; ++r) A[r] = a_operand(xa, arow, s + 1, nsteps_cap, g, r);
             mma_tile<BITS, CB>(second.words(), A, acc);
         }
     }
