@@ -98,11 +98,12 @@ __device__ __forceinline__ T* pat(char* base, int64_t off) { return reinterpret_
 // 2r+9 (the order mma_tile's windows use), each twice (lo/hi addends).
 __device__ __forceinline__ half8_t a_from_words(const u32x4_t& lo, const u32x4_t& hi, int r) {
     const uint32_t a = lo[r & 3], b = hi[r & 3];
+    // one byte permute per register: (lo, lo) and (hi, hi) of each word
     u32x4_t d;
-    d[0] = (a & 0xffffu) | (a << 16);
-    d[1] = (a >> 16) | (a & 0xffff0000u);
-    d[2] = (b & 0xffffu) | (b << 16);
-    d[3] = (b >> 16) | (b & 0xffff0000u);
+    d[0] = __builtin_amdgcn_perm(a, a, 0x01000100u);
+    d[1] = __builtin_amdgcn_perm(a, a, 0x03020302u);
+    d[2] = __builtin_amdgcn_perm(b, b, 0x01000100u);
+    d[3] = __builtin_amdgcn_perm(b, b, 0x03020302u);
     return __builtin_bit_cast(half8_t, d);
 }
 
@@ -135,21 +136,24 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
 // One (tile, 256-column block) of C[rows, N] = A[rows, K] . Wq[K, N], rows of A
 // at A + (row0 + i) * K (fp16, already rotated), i < nrows <= 32; epilogue
 // y = (H c / sqrt(128)) * svh written as fp32 to out + (row0 + i) * N.
+// Called by both waves of a block (`wave` 0 or 1; `valid` false: no item, but
+// the wave still takes part in the block's barriers); `tbuf` (32 rows x 256
+// fp32) is shared by the two waves, which use it in turn.
 template <int BITS, int CB>
-__device__ __forceinline__ void pf_tile(const uint16_t* A, int row0, int nrows, const int16_t* trellis, const uint16_t* svh,
-                        int K, int k0, int nsteps, int N, int cb, float* out, float* tbuf) {
-    const int lane = threadIdx.x;
+__device__ __forceinline__ void pf_tile(bool valid, int wave, const uint16_t* A, int row0, int nrows,
+                                        const int16_t* trellis, const uint16_t* svh, int K, int k0, int nsteps,
+                                        int N, int cb, float* out, float* tbuf) {
+    const int lane = threadIdx.x & (WAVE - 1);
     const int g = lane >> 4, c = lane & 15;
     const int n16 = N / 16;
     const u32x4_t* tp = tile_ptr<BITS>(trellis, n16, k0 / 16, cb * 16);
     const size_t tstep = (size_t)4 * n16 * tile_vecs<BITS>();
-    // A rows of this lane: c and c + 16 (zero beyond nrows); k-slice g of each
-    // step.  Every load reads a valid row and a dead row is zeroed after, so
-    // the loop has no branches (the accumulators stay put in registers).
-    const bool live0 = c < nrows, live1 = c + 16 < nrows;
-    const u32x4_t* a0 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live0 ? c : 0)) * K + k0 + 16 * g);
-    const u32x4_t* a1 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + (live1 ? c + 16 : 0)) * K + k0 + 16 * g);
-    const uint32_t m0 = live0 ? 0xffffffffu : 0u, m1 = live1 ? 0xffffffffu : 0u;
+    // A rows of this lane: c and c + 16, k-slice g of each step.  A row past
+    // nrows reads row nrows - 1 instead (valid memory, no branch in the loop):
+    // its accumulator rows are never written out.
+    const int ra0 = min(c, nrows - 1), ra1 = min(c + 16, nrows - 1);
+    const u32x4_t* a0 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + max(ra0, 0)) * K + k0 + 16 * g);
+    const u32x4_t* a1 = reinterpret_cast<const u32x4_t*>(A + (size_t)(row0 + max(ra1, 0)) * K + k0 + 16 * g);
     const int astep = STEP_K / 8;        // 16-byte vectors per 64 k
 
     float4_t acc[2][16];
@@ -160,11 +164,11 @@ __device__ __forceinline__ void pf_tile(const uint16_t* A, int row0, int nrows, 
     TileRegs<BITS> t0, t1;
     u32x4_t ac[2][2];
     auto load_a = [&](int s) {
-        ac[0][0] = a0[s * astep] & m0; ac[0][1] = a0[s * astep + 1] & m0;
-        ac[1][0] = a1[s * astep] & m1; ac[1][1] = a1[s * astep + 1] & m1;
+        ac[0][0] = a0[s * astep]; ac[0][1] = a0[s * astep + 1];
+        ac[1][0] = a1[s * astep]; ac[1][1] = a1[s * astep + 1];
     };
-    load_tile<BITS>(t0, tp);
-    for (int s = 0; s < nsteps; s += 2) {
+    if (valid) load_tile<BITS>(t0, tp);
+    for (int s = 0; s < (valid ? nsteps : 0); s += 2) {
         load_tile<BITS>(t1, tp + (s + 1) * tstep);
         load_a(s);
         mma_tile2<BITS, CB>(t0.words(), ac, acc);
@@ -174,55 +178,69 @@ __device__ __forceinline__ void pf_tile(const uint16_t* A, int row0, int nrows, 
         mma_tile2<BITS, CB>(t1.words(), ac, acc);
     }
 
-    // epilogue: both row blocks transposed through LDS at once (the
-    // accumulators die here), then one output row per pass
+    // epilogue, one wave of the block after the other: both row blocks
+    // transposed through LDS at once (the accumulators die here), then one
+    // output row per pass
     const int col = 128 * (lane >> 5) + 4 * (lane & 31);
-    __syncthreads();
+    for (int w = 0; w < 2; ++w) {
+        __syncthreads();                          // tbuf is free
+        if (wave == w && valid) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+            for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float4_t* t = reinterpret_cast<float4_t*>(tbuf + (16 * rb + 4 * g + i) * COLS + 16 * c);
+                for (int i = 0; i < 4; ++i) {
+                    float4_t* t = reinterpret_cast<float4_t*>(tbuf + (16 * rb + 4 * g + i) * COLS + 16 * c);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                t[q] = float4_t{acc[rb][4 * q][i], acc[rb][4 * q + 1][i], acc[rb][4 * q + 2][i], acc[rb][4 * q + 3][i]};
+                    for (int q = 0; q < 4; ++q)
+                        t[q] = float4_t{acc[rb][4 * q][i], acc[rb][4 * q + 1][i], acc[rb][4 * q + 2][i],
+                                        acc[rb][4 * q + 3][i]};
+                }
         }
-    __syncthreads();
-    float sv[4];
+        __syncthreads();
+        if (wave == w && valid) {
+            float sv[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sv[e] = f16_bits_to_f32(svh[cb * COLS + col + e]);
-    for (int row = 0; row < nrows; ++row) {
-        const float4_t v4 = reinterpret_cast<const float4_t*>(tbuf + row * COLS)[col / 4];
-        float v[4] = {v4[0], v4[1], v4[2], v4[3]};
-        fwht128_x4(v);
-        float4_t o;
+            for (int e = 0; e < 4; ++e) sv[e] = f16_bits_to_f32(svh[cb * COLS + col + e]);
+            for (int row = 0; row < nrows; ++row) {
+                const float4_t v4 = reinterpret_cast<const float4_t*>(tbuf + row * COLS)[col / 4];
+                float v[4] = {v4[0], v4[1], v4[2], v4[3]};
+                fwht128_x4(v);
+                float4_t o;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = v[e] * HAD_NORM * sv[e];
-        *reinterpret_cast<float4_t*>(out + (size_t)(row0 + row) * N + cb * COLS + col) = o;
+                for (int e = 0; e < 4; ++e) o[e] = v[e] * HAD_NORM * sv[e];
+                *reinterpret_cast<float4_t*>(out + (size_t)(row0 + row) * N + cb * COLS + col) = o;
+            }
+        }
     }
 }
 
-// gate/up (DOWN = false): blockIdx = (tile, projection, column block of I,
-// k-part); down (DOWN = true): blockIdx = (tile, column block of H, k-part).  One launch per bit
-// width present (one width per kernel keeps the registers at two waves per
-// SIMD); blocks past the planned tile count or of another width return at once.
+// Items: gate/up (DOWN = false) = (tile, projection, column block of I,
+// k-part); down (DOWN = true) = (tile, column block of H, k-part).  Two waves
+// per block, item 2 * blockIdx + wave each, sharing one 32 KB transpose
+// buffer (16 KB per wave leaves the LDS room for two waves per SIMD).  One
+// launch per bit width present (one width per kernel keeps the registers at
+// two waves per SIMD); items past the planned tile count or of another width
+// are skipped, and a block with none returns at once.
 template <int BITS, int CB, bool DOWN>
-__global__ __launch_bounds__(64) void pf_gemm_kernel(PfParams P) {
+__global__ __launch_bounds__(2 * WAVE) void pf_gemm_kernel(PfParams P) {
     __shared__ float tbuf[PF_RB * COLS];
     const PfLayout& L = P.L;
     const int ncb = (DOWN ? P.H : P.I) / COLS;
     const int KS = DOWN ? L.ks_down : L.ks_up;
     const int per_tile = (DOWN ? ncb : 2 * ncb) * KS;
-    const int t = blockIdx.x / per_tile;
-    int rem = blockIdx.x - t * per_tile;
-    if (t >= pat<int>(P.scratch, L.meta)[1]) return;
-    const int e = pat<int>(P.scratch, L.tile_e)[t];
-    if ((P.ebits ? (int)P.ebits[e] : P.bits) != BITS) return;
+    const int wave = threadIdx.x / WAVE;
+    const int item = 2 * blockIdx.x + wave;
+    const int t = item / per_tile;
+    int rem = item - t * per_tile;
+    bool valid = t < pat<int>(P.scratch, L.meta)[1];
+    const int e = valid ? pat<int>(P.scratch, L.tile_e)[t] : 0;
+    valid = valid && (P.ebits ? (int)P.ebits[e] : P.bits) == BITS;
+    if (!__syncthreads_or(valid)) return;
     const int ks = rem % KS;
     rem /= KS;
     const int proj = DOWN ? 0 : rem / ncb, cb = DOWN ? rem : rem - (rem / ncb) * ncb;
-    const int row0 = pat<int>(P.scratch, L.tile_r0)[t];
-    const int nrows = pat<int>(P.scratch, L.tile_n)[t];
+    const int row0 = valid ? pat<int>(P.scratch, L.tile_r0)[t] : 0;
+    const int nrows = valid ? pat<int>(P.scratch, L.tile_n)[t] : 0;
     const int K = DOWN ? P.I : P.H, N = DOWN ? P.H : P.I;
     const int kpart = K / KS;
     const uint16_t* A = DOWN ? pat<uint16_t>(P.scratch, L.AD)
@@ -231,7 +249,7 @@ __global__ __launch_bounds__(64) void pf_gemm_kernel(PfParams P) {
     const uint16_t* svh = reinterpret_cast<const uint16_t*>((DOWN ? P.dsv : (proj ? P.usv : P.gsv))[e]);
     float* out = DOWN ? pat<float>(P.scratch, L.D) + (size_t)ks * P.P * P.H
                       : pat<float>(P.scratch, L.GU) + ((size_t)ks * 2 + proj) * P.P * P.I;
-    pf_tile<BITS, CB>(A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out, tbuf);
+    pf_tile<BITS, CB>(valid, wave, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out, tbuf);
 }
 
 // Launcher of the grouped GEMM for one bit width (exl3_prefill_inst.hip).

@@ -12,12 +12,14 @@ namespace prefill {
 template <>
 int launch_pf_gemm<EXL3_BITS>(const PfParams& P, int codebook, bool down, int blocks, hipStream_t stream) {
     constexpr int B = EXL3_BITS;
+    // `blocks` items, two per workgroup
+    const unsigned grid = (unsigned)((blocks + 1) / 2);
     auto go = [&](auto cbc) {
         constexpr int C = decltype(cbc)::value;
         if (down)
-            hipLaunchKernelGGL((pf_gemm_kernel<B, C, true>), dim3(blocks), dim3(WAVE), 0, stream, P);
+            hipLaunchKernelGGL((pf_gemm_kernel<B, C, true>), dim3(grid), dim3(2 * WAVE), 0, stream, P);
         else
-            hipLaunchKernelGGL((pf_gemm_kernel<B, C, false>), dim3(blocks), dim3(WAVE), 0, stream, P);
+            hipLaunchKernelGGL((pf_gemm_kernel<B, C, false>), dim3(grid), dim3(2 * WAVE), 0, stream, P);
     };
     switch (codebook) {
         case CB_MCG: go(std::integral_constant<int, CB_MCG>{}); break;
