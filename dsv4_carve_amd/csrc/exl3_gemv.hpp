@@ -216,18 +216,22 @@ __device__ __forceinline__ void publish_fence() {
     asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
 }
 
-// Device-scope 16-byte loads through a raw buffer resource.  The sc1 policy
-// makes them coherent at device scope, like the sc1 stores above; unlike
-// an asm block, the compiler tracks their completion itself, so a batch of any
-// size is in flight at once and each value is waited for where it is used.
-// The base address must be uniform across the wave; the lane's offset goes in
-// `voff` and a per-load offset in `soff` (bytes, below 2 GiB in total).
+// 16-byte loads through a raw buffer resource.  With the sc1 policy they are
+// coherent at device scope, like the sc1 stores above (data another wave of
+// the same launch published); with the default policy (0) they are plain
+// cached loads, for data an earlier launch wrote.  Unlike an asm block, the
+// compiler tracks their completion itself, so a batch of any size is in
+// flight at once and each value is waited for where it is used.  The base
+// address must be uniform across the wave; the lane's offset goes in `voff`
+// and a per-load offset in `soff` (bytes, below 2 GiB in total).
 constexpr int CPOL_SC1 = 16;
+constexpr int CPOL_PLAIN = 0;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t dev_rsrc(const void* base) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }
+template <int CPOL = CPOL_SC1>
 __device__ __forceinline__ float4_t ld_dev4_buf(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-    return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL_SC1));
+    return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, CPOL));
 }
 // No memory access is moved across this point by the compiler (loads that
 // read published data stay after the counter or flag that published it).
@@ -236,6 +240,7 @@ __device__ __forceinline__ void compiler_barrier() { asm volatile("" ::: "memory
 // Sums two independent sets of `count` fp32 partial vectors in index order:
 // a[i * stride], b[i * stride] at byte offset `voff` (the lane's columns) from
 // the uniform bases a and b.  Up to 32 loads (16 of each) are in flight.
+template <int CPOL = CPOL_SC1>
 __device__ __forceinline__ void sum_partials2(const float* a, const float* b, uint32_t voff, size_t stride,
                                               int count, float4_t& sa, float4_t& sb) {
     compiler_barrier();
@@ -248,8 +253,8 @@ __device__ __forceinline__ void sum_partials2(const float* a, const float* b, ui
 #pragma unroll
         for (int j = 0; j < 16; ++j)
             if (i0 + j < count) {
-                va[j] = ld_dev4_buf(ra, voff, (uint32_t)(i0 + j) * st);
-                vb[j] = ld_dev4_buf(rb, voff, (uint32_t)(i0 + j) * st);
+                va[j] = ld_dev4_buf<CPOL>(ra, voff, (uint32_t)(i0 + j) * st);
+                vb[j] = ld_dev4_buf<CPOL>(rb, voff, (uint32_t)(i0 + j) * st);
             }
 #pragma unroll
         for (int j = 0; j < 16; ++j)
@@ -262,6 +267,7 @@ __device__ __forceinline__ void sum_partials2(const float* a, const float* b, ui
 
 // Sums `count` fp32 partial vectors p[i * stride] at byte offset `voff` from
 // the uniform base p, in index order, with up to 32 loads in flight.
+template <int CPOL = CPOL_SC1>
 __device__ __forceinline__ float4_t sum_partials(const float* p, uint32_t voff, size_t stride, int count) {
     compiler_barrier();
     const __amdgpu_buffer_rsrc_t r = dev_rsrc(p);
@@ -271,7 +277,7 @@ __device__ __forceinline__ float4_t sum_partials(const float* p, uint32_t voff, 
         float4_t v[32];
 #pragma unroll
         for (int j = 0; j < 32; ++j)
-            if (i0 + j < count) v[j] = ld_dev4_buf(r, voff, (uint32_t)(i0 + j) * st);
+            if (i0 + j < count) v[j] = ld_dev4_buf<CPOL>(r, voff, (uint32_t)(i0 + j) * st);
 #pragma unroll
         for (int j = 0; j < 32; ++j)
             if (i0 + j < count) acc += v[j];
@@ -363,13 +369,14 @@ __device__ __forceinline__ void had_in_row(const void* x, size_t x_off, int x_ki
 
 // Copies `nblocks` (<= 4) already-rotated fp16 blocks of one row, written by
 // other waves, into the LDS A tile.
+template <bool DEV = true>
 __device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int m, int nblocks, int nsteps_cap) {
     const int lane = threadIdx.x & (WAVE - 1);
     uint32_t v[HAD_MAX_BLOCKS];
     const uint32_t* sp = reinterpret_cast<const uint32_t*>(src) + lane;
 #pragma unroll
     for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
-        if (b < nblocks) v[b] = ld_dev(sp + 64 * b);
+        if (b < nblocks) v[b] = DEV ? ld_dev(sp + 64 * b) : sp[64 * b];
 #pragma unroll
     for (int b = 0; b < HAD_MAX_BLOCKS; ++b) {
         if (b >= nblocks) break;
@@ -384,7 +391,9 @@ __device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int 
 // with device-scope stores (another wave reduces them).  The MFMA result
 // layout (lane = n-tile + 16 * row group, register = column in the tile) is
 // transposed through LDS (`tbuf`, >= R KB, free at this point) so every store
-// instruction writes one contiguous 1 KB row.
+// instruction writes one contiguous 1 KB row.  DEV: device-scope stores (the
+// reader runs in the same launch); otherwise plain stores (a later launch).
+template <bool DEV = true>
 __device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float* dst, size_t ld, int R,
                                                int cols_valid, float* tbuf) {
     const int lane = threadIdx.x & (WAVE - 1);
@@ -402,8 +411,11 @@ __device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float*
     }
     __syncthreads();
     if (4 * lane < cols_valid)
-        for (int row = 0; row < R; ++row)
-            st_dev4(dst + (size_t)row * ld + 4 * lane, reinterpret_cast<const float4_t*>(tbuf + row * COLS)[lane]);
+        for (int row = 0; row < R; ++row) {
+            const float4_t v = reinterpret_cast<const float4_t*>(tbuf + row * COLS)[lane];
+            if constexpr (DEV) st_dev4(dst + (size_t)row * ld + 4 * lane, v);
+            else *reinterpret_cast<float4_t*>(dst + (size_t)row * ld + 4 * lane) = v;
+        }
 }
 
 }  // namespace exl3

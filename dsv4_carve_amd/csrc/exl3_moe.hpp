@@ -71,8 +71,9 @@ __host__ __device__ inline int item_steps(int k, int64_t units, int64_t waves) {
 
 struct Layout {
     int nI, nH, SA, SB, stepsA, stepsB;
-    int64_t ctrl, cls, cntA, doneA, cntB, cntG, doneB, PA, DI, PB, DC, total;
+    int64_t ctrl, cls, cntA, doneA, cntB, cntG, doneB, plan, PA, DI, PB, DC, total;
 };
+constexpr int64_t PLAN_BYTES = 4096;          // the route plan, saved for the phased launches
 
 __host__ __device__ inline int64_t al(int64_t v) { return (v + 255) / 256 * 256; }
 
@@ -99,6 +100,7 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     L.cntB = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * WORD_STRIDE;
     L.cntG = o;  o += (int64_t)MAX_BLOCKS * WORD_STRIDE;
     L.doneB = o; o += (int64_t)MAX_BLOCKS * WORD_STRIDE;
+    L.plan = o;  o += PLAN_BYTES;
     o = al(o);
     L.PA = o;    o = al(o + P * 2 * L.SA * I * 4);
     L.DI = o;    o = al(o + P * I * 2);
@@ -191,6 +193,7 @@ struct Plan {
     int8_t gbits[MAX_SLOTS];
     int16_t slotpair[MAX_SLOTS]; // pair of slot (row*topk + j), -1 if invalid
 };
+static_assert(sizeof(Plan) <= PLAN_BYTES && sizeof(Plan) % 4 == 0, "plan fits its scratch slot");
 
 // Expert-major row bitmask, then a wave-wide exclusive scan over experts
 // (lna_moe_ticket.cu:167-214 computes the same plan with block scans).
@@ -370,23 +373,25 @@ __device__ __forceinline__ void load_half4(uint16_t (&v)[4], int64_t addr, int c
     v[3] = (uint16_t)(b >> 16);
 }
 
-// ---------------------------------------------------------------- items
+// ---------------------------------------------------------------- item parts
+//
+// Shared by the two schedules: the ticket kernel (one launch; DEV = true:
+// device-scope stores and loads, the data handed over inside the launch) and
+// the phased launches for small batches (DEV = false: plain stores and loads,
+// each phase a launch of its own).  Item bodies are instantiated once per bit
+// width; the kernels dispatch on the expert's width at item granularity (a
+// uniform branch per wave).
 
-// Item bodies are instantiated once per bit width; the kernel dispatches on the
-// expert's width at item granularity (a uniform branch per wave).
-
-// gate/up item: (group g, projection p, 256-column block cb, k-chunk kc)
-template <int B, int CB>
-__device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int p, int cb, int kc,
-                            int epoch, Tracer& tr, NextTicket& nt, int home) {
+// gate/up partial sums of (expert e, pairs pb.., rows `mask`, projection p,
+// 256-column block cb, k-chunk kc).
+template <int B, int CB, bool DEV>
+__device__ __forceinline__ void gateup_partials(const Params& P, int e, int pb, uint32_t mask, uint16_t* xa, int p,
+                                                int cb, int kc, Tracer& tr) {
     const Layout& L = P.L;
-    const int e = pl.gexp[g], pb = pl.gpair[g];
-    const uint32_t mask = pl.gmask[g];
     const int R = __popc(mask);
     const int kchunk = L.stepsA * STEP_K;
     const int k0 = kc * kchunk;
 
-    nt.issue(at<Ctrl>(P.scratch, L.ctrl), P.scratch + L.cls, home);
     // step-0 weights are in flight while the input rotation runs
     const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]), P.I / 16, k0 / 16,
                                     cb * 16);
@@ -406,31 +411,31 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     tr(EV_A_MMA);
 
     float* PA = at<float>(P.scratch, L.PA);
-    const size_t ld = (size_t)2 * L.SA * P.I;
-    store_partials(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, ld, R, COLS,
-                   reinterpret_cast<float*>(xa));
-    tr(EV_STORED);
-    publish_fence();
-    tr(EV_FENCED);
-    int* cnt = word(P.scratch, L.cntA, g * MAX_BLOCKS + cb);
-    const bool last = wave_atomic_add(cnt, 1) == 2 * L.SA - 1;
-    tr(EV_A_END, last);
-    if (!last) return;
+    store_partials<DEV>(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, (size_t)2 * L.SA * P.I, R,
+                        COLS, reinterpret_cast<float*>(xa));
+}
 
-    // Last arriver: gate/up epilogue for (group g, column block cb).
-    const int lane = threadIdx.x;
+// gate/up finish of (expert e, pairs pb..pb+R-1, column block cb): the split-K
+// sums in chunk order, output Hadamard + svh, clamped SwiGLU, fp16, the down
+// projection's suh and input Hadamard; stores the fp16 down input DI.
+template <bool DEV>
+__device__ __forceinline__ void gateup_finish(const Params& P, int e, int pb, int R, int cb) {
+    const Layout& L = P.L;
+    const int lane = threadIdx.x & (WAVE - 1);
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
     // scales first: their loads are in flight during the partial sums
     uint16_t gsv[4], usv[4], dsu[4];
     load_half4(gsv, P.gsv[e], col);
     load_half4(usv, P.usv[e], col);
     load_half4(dsu, P.dsu[e], col);
+    const float* PA = at<float>(P.scratch, L.PA);
     uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
     for (int r = 0; r < R; ++r) {
         const int pair = pb + r;
         float4_t ga, ua;
-        sum_partials2(PA + (size_t)(pair * 2 + 0) * L.SA * P.I, PA + (size_t)(pair * 2 + 1) * L.SA * P.I,
-                      (uint32_t)col * 4u, P.I, L.SA, ga, ua);
+        sum_partials2<DEV ? CPOL_SC1 : CPOL_PLAIN>(PA + (size_t)(pair * 2 + 0) * L.SA * P.I,
+                                                  PA + (size_t)(pair * 2 + 1) * L.SA * P.I, (uint32_t)col * 4u, P.I,
+                                                  L.SA, ga, ua);
         float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
         fwht128_x4(gv);
         fwht128_x4(uv);
@@ -447,11 +452,70 @@ __device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g
         uint2 packed;
         packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
         packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
-        st_dev2(reinterpret_cast<uint32_t*>(DI + (size_t)pair * P.I + col), packed);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(DI + (size_t)pair * P.I + col);
+        if constexpr (DEV) st_dev2(dst, packed);
+        else *reinterpret_cast<uint2*>(dst) = packed;
     }
+}
+
+// down partial sums of (pairs pb..pb+R-1, 256-column block cb of hidden,
+// k-chunk kc of intermediate); `first` holds the step-0 tile of `tp`.
+template <int B, int CB, bool DEV>
+__device__ __forceinline__ void down_partials(const Params& P, int pb, int R, uint16_t* xa, int cb, int kc,
+                                              TileRegs<B>& first, const u32x4_t* tp, Tracer& tr) {
+    const Layout& L = P.L;
+    const int kchunk = L.stepsB * STEP_K;
+    const int k0 = kc * kchunk;
+    const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
+    for (int r = 0; r < R; ++r) copy_row<DEV>(DI + (size_t)(pb + r) * P.I + k0, xa, r, kchunk / 128, NSTEP_CAP);
+    __syncthreads();
+
+    float4_t acc[16];
+    mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
+    tr(EV_B_MMA);
+
+    float* PB = at<float>(P.scratch, L.PB);
+    store_partials<DEV>(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS,
+                        reinterpret_cast<float*>(xa));
+}
+
+// Down output of one pair for the lane's four columns `col` (expert scales
+// dsv): the split-K sum in chunk order, output Hadamard, svh (fp32).
+template <int CPOL>
+__device__ __forceinline__ float4_t down_value(const Params& P, int pair, const uint16_t (&dsv)[4], int col) {
+    const Layout& L = P.L;
+    const float4_t t = sum_partials<CPOL>(at<float>(P.scratch, L.PB) + (size_t)pair * L.SB * P.H,
+                                          (uint32_t)col * 4u, P.H, L.SB);
+    float v[4] = {t[0], t[1], t[2], t[3]};
+    fwht128_x4(v);
+    float4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = v[i] * HAD_NORM * f16_bits_to_f32(dsv[i]);
+    return o;
+}
+
+// ---------------------------------------------------------------- ticket items
+
+// gate/up item: (group g, projection p, 256-column block cb, k-chunk kc)
+template <int B, int CB>
+__device__ void item_a_body(const Params& P, const Plan& pl, uint16_t* xa, int g, int p, int cb, int kc,
+                            int epoch, Tracer& tr, NextTicket& nt, int home) {
+    const Layout& L = P.L;
+    nt.issue(at<Ctrl>(P.scratch, L.ctrl), P.scratch + L.cls, home);
+    gateup_partials<B, CB, true>(P, pl.gexp[g], pl.gpair[g], pl.gmask[g], xa, p, cb, kc, tr);
+    tr(EV_STORED);
+    publish_fence();
+    tr(EV_FENCED);
+    int* cnt = word(P.scratch, L.cntA, g * MAX_BLOCKS + cb);
+    const bool last = wave_atomic_add(cnt, 1) == 2 * L.SA - 1;
+    tr(EV_A_END, last);
+    if (!last) return;
+
+    // Last arriver: gate/up finish for (group g, column block cb), then the flag.
+    gateup_finish<true>(P, pl.gexp[g], pl.gpair[g], __popc(pl.gmask[g]), cb);
     reset_counter(cnt);
     publish_fence();
-    if (lane == 0)
+    if (threadIdx.x == 0)
         __hip_atomic_store(word(P.scratch, L.doneA, g * MAX_BLOCKS + cb), epoch + 1, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
     tr(EV_EPI_A_END);
@@ -463,8 +527,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
                             Tracer& tr, NextTicket& nt) {
     const Layout& L = P.L;
     const int e = pl.gexp[g], pb = pl.gpair[g];
-    const uint32_t mask = pl.gmask[g];
-    const int R = __popc(mask);
+    const int R = __popc(pl.gmask[g]);
     const int kchunk = L.stepsB * STEP_K;
     const int k0 = kc * kchunk;
 
@@ -478,17 +541,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     tr(EV_B_WAITED);
     nt.issue(at<Ctrl>(P.scratch, L.ctrl), P.scratch + L.cls, -1);
 
-    const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
-    for (int r = 0; r < R; ++r) copy_row(DI + (size_t)(pb + r) * P.I + k0, xa, r, kchunk / 128, NSTEP_CAP);
-    __syncthreads();
-
-    float4_t acc[16];
-    mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
-    tr(EV_B_MMA);
-
-    float* PB = at<float>(P.scratch, L.PB);
-    store_partials(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS,
-                   reinterpret_cast<float*>(xa));
+    down_partials<B, CB, true>(P, pb, R, xa, cb, kc, first, tp, tr);
     tr(EV_STORED);
     publish_fence();
     tr(EV_FENCED);
@@ -503,16 +556,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
     uint16_t dsv[4];
     load_half4(dsv, P.dsv[e], col);
     float* DC = at<float>(P.scratch, L.DC);
-    for (int r = 0; r < R; ++r) {
-        const int pair = pb + r;
-        const float4_t t = sum_partials(PB + (size_t)pair * L.SB * P.H, (uint32_t)col * 4u, P.H, L.SB);
-        float v[4] = {t[0], t[1], t[2], t[3]};
-        fwht128_x4(v);
-        float4_t o;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) o[i] = v[i] * HAD_NORM * f16_bits_to_f32(dsv[i]);
-        st_dev4(DC + (size_t)pair * P.H + col, o);
-    }
+    for (int r = 0; r < R; ++r) st_dev4(DC + (size_t)(pb + r) * P.H + col, down_value<CPOL_SC1>(P, pb + r, dsv, col));
     reset_counter(cnt);
     publish_fence();
     int* cg = word(P.scratch, L.cntG, cb);
@@ -677,9 +721,109 @@ __global__ __launch_bounds__(64, 2) void moe_kernel(Params P) {   // 2 waves per
     }
 }
 
+// ---------------------------------------------------------------- phased launches
+//
+// Small batches: four launches instead of one, each a plain grid with one
+// item per workgroup -- gate/up partials; the gate/up finish of every
+// (group, column block); down partials; down finish + gather per (H block,
+// row).  The launch boundaries order the data (plain stores and loads).  With
+// little work to overlap them, a boundary (about 2 us in a graph) is cheaper
+// than the ticket kernel's chains of device-scope stores, counters, flag polls
+// and loads.  Same items, same sums in the same order: the results are
+// bitwise those of the ticket kernel.
+
+__device__ __forceinline__ void save_plan(const Plan& pl, Plan* dst) {
+    const int* s = reinterpret_cast<const int*>(&pl);
+    int* d = reinterpret_cast<int*>(dst);
+    for (int i = threadIdx.x; i < (int)(sizeof(Plan) / 4); i += WAVE) d[i] = s[i];
+}
+
+// Launch 1: item = (group, projection, column block of I, k-chunk); every
+// workgroup builds the route plan, the first one saves it for launches 2-4.
+template <uint32_t MASK, int CB>
+__global__ __launch_bounds__(64, 2) void moe_phase_gateup(Params P) {
+    extern __shared__ __align__(16) uint16_t xa[];   // moe_lds_kb(m, E) KB
+    __shared__ Plan pl;
+    const Layout& L = P.L;
+    build_plan(P, pl, reinterpret_cast<char*>(xa));
+    if (blockIdx.x == 0) save_plan(pl, at<Plan>(P.scratch, L.plan));
+    const int per_g = 2 * L.nI * L.SA;
+    const int g = blockIdx.x / per_g;
+    if (g >= pl.U) return;
+    int rem = blockIdx.x - g * per_g;
+    const int p = rem / (L.nI * L.SA);
+    rem -= p * L.nI * L.SA;
+    const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
+    Tracer tr;
+    dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
+        gateup_partials<decltype(BI)::value, CB, false>(P, pl.gexp[g], pl.gpair[g], pl.gmask[g], xa, p, cb, kc, tr);
+    });
+}
+
+// Launch 2: item = (group, column block of I).
+template <int DUMMY = 0>
+__global__ __launch_bounds__(64) void moe_phase_act(Params P) {
+    const Layout& L = P.L;
+    const Plan* pl = at<Plan>(P.scratch, L.plan);
+    const int g = blockIdx.x / L.nI, cb = blockIdx.x - (blockIdx.x / L.nI) * L.nI;
+    if (g >= pl->U) return;
+    gateup_finish<false>(P, pl->gexp[g], pl->gpair[g], __popc(pl->gmask[g]), cb);
+}
+
+// Launch 3: item = (group, column block of H, k-chunk of I).
+template <uint32_t MASK, int CB>
+__global__ __launch_bounds__(64, 2) void moe_phase_down(Params P) {
+    extern __shared__ __align__(16) uint16_t xa[];   // moe_lds_kb(m, E) KB
+    const Layout& L = P.L;
+    const Plan* pl = at<Plan>(P.scratch, L.plan);
+    const int per_g = L.nH * L.SB;
+    const int g = blockIdx.x / per_g;
+    if (g >= pl->U) return;
+    const int rem = blockIdx.x - g * per_g;
+    const int cb = rem / L.SB, kc = rem - (rem / L.SB) * L.SB;
+    const int e = pl->gexp[g], pb = pl->gpair[g], R = __popc(pl->gmask[g]);
+    Tracer tr;
+    dispatch_bits<MASK>(pl->gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
+        constexpr int B = decltype(BI)::value;
+        const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[e]), P.H / 16,
+                                        kc * L.stepsB * STEP_K / 16, cb * 16);
+        TileRegs<B> first;
+        load_tile<B>(first, tp);
+        down_partials<B, CB, false>(P, pb, R, xa, cb, kc, first, tp, tr);
+    });
+}
+
+// Launch 4: item = (column block of H, row): each slot's down output (finish
+// of its pair) summed in top-k slot order (fp32), one cast.
+template <int DUMMY = 0>
+__global__ __launch_bounds__(64) void moe_phase_finish(Params P) {
+    const Layout& L = P.L;
+    const Plan* pl = at<Plan>(P.scratch, L.plan);
+    const int cb = blockIdx.x / P.m, row = blockIdx.x - (blockIdx.x / P.m) * P.m;
+    const int lane = threadIdx.x;
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < P.topk; ++j) {
+        const int pair = pl->slotpair[row * P.topk + j];
+        if (pair < 0) continue;
+        uint16_t dsv[4];
+        load_half4(dsv, P.dsv[P.ids[row * P.topk + j]], col);
+        const float4_t o = down_value<CPOL_PLAIN>(P, pair, dsv, col);
+        const float w = P.w[row * P.topk + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + w * o[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)row * P.H + col + i, P.out_kind, s4[i]);
+}
+
 // Launcher for one (bit-width mask, codebook) instantiation; defined in exl3_moe_inst.hip.
 template <uint32_t MASK, int CB>
 int launch_moe(const Params& P, int waves, int lds_kb, hipStream_t stream);
+
+// The four phased launches (grids from the group bound `groups`).
+template <uint32_t MASK, int CB>
+int launch_phased(const Params& P, int groups, int lds_kb, hipStream_t stream);
 
 template <uint32_t MASK, int CB>
 int moe_waves_per_cu(int lds_kb);

@@ -4,6 +4,7 @@
 //   exl3_moe_max_rows       <- lna2_moe_max_rows       :484
 //   exl3_moe_info           <- lna2_moe_info           :494-505
 #include <math.h>
+#include <stdlib.h>
 
 #include "exl3_moe.hpp"
 
@@ -20,6 +21,7 @@ namespace moe {
 
 #define EXL3_DECL(M, C)                                                          \
     template <> int launch_moe<M, C>(const Params&, int, int, hipStream_t);     \
+    template <> int launch_phased<M, C>(const Params&, int, int, hipStream_t);  \
     template <> int moe_waves_per_cu<M, C>(int);
 EXL3_MOE_INSTANCES(EXL3_DECL)
 #undef EXL3_DECL
@@ -28,10 +30,11 @@ struct Instance {
     uint32_t mask;
     int cb;
     int (*launch)(const Params&, int, int, hipStream_t);
+    int (*phased)(const Params&, int, int, hipStream_t);
     int (*waves)(int);
 };
 
-#define EXL3_ENTRY(M, C) {M, C, &launch_moe<M, C>, &moe_waves_per_cu<M, C>},
+#define EXL3_ENTRY(M, C) {M, C, &launch_moe<M, C>, &launch_phased<M, C>, &moe_waves_per_cu<M, C>},
 static const Instance kInstances[] = {EXL3_MOE_INSTANCES(EXL3_ENTRY)};
 #undef EXL3_ENTRY
 
@@ -46,6 +49,20 @@ static int cached_waves(int idx, int lds_kb) {
     std::lock_guard<std::mutex> lock(mu);
     if (!cache[dev][idx][lds_kb]) cache[dev][idx][lds_kb] = kInstances[idx].waves(lds_kb);
     return cache[dev][idx][lds_kb];
+}
+
+// Schedule choice.  The phased launches win while the layer is short: below
+// about PHASED_STEPS_PER_WAVE decode steps (64 x 256 weights) per resident
+// wave the ticket kernel has too little work to hide its device-scope
+// hand-offs behind (measured on the 256-expert layer: phased faster up to 4
+// rows, even at 8, slower at 16; one GPU's TP8 share: phased faster at every
+// row count).  EXL3_MOE_PHASED_MAX_ROWS, when set, replaces the rule by a row
+// count (0: always the ticket kernel; 16: always the phased launches).
+constexpr int64_t PHASED_STEPS_PER_WAVE = 40;
+static bool use_phased(int64_t m, int64_t steps, int64_t resident) {
+    const char* v = getenv("EXL3_MOE_PHASED_MAX_ROWS");
+    if (v && *v) return m <= atoi(v);
+    return steps < PHASED_STEPS_PER_WAVE * resident;
 }
 
 }  // namespace moe
@@ -144,6 +161,10 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
     P.scratch = reinterpret_cast<char*>(scratch);
     P.L = L;
     P.trace_off = trace_off;
+
+    const int64_t steps = groups * (2LL * L.nI * (hidden / STEP_K) + (int64_t)L.nH * (intermediate / STEP_K));
+    if (use_phased(m, steps, resident))
+        return kInstances[idx].phased(P, (int)groups, lds_kb, reinterpret_cast<hipStream_t>(stream));
 
     const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB) + (int64_t)L.nH * m;
     const int waves = (int)(items < resident ? items : resident);

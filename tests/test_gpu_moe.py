@@ -5,9 +5,14 @@ route profiles unique/hot/zipf/boundary/within-row-dup/R_e16/cancel (:184-206),
 weights normal/zero/cancel (:209-216), inputs zero/real/amplified/clamp/large
 (:219-233), every row count, bitwise repeat (:296-298), a transposed-ids ABI
 check (:347-366) and a scratch-reuse replay (:369-393).  Tolerance is the fp
-bar (max-abs 2e-2, rel-L2 1e-3) against the oracle."""
+bar (max-abs 2e-2, rel-L2 1e-3) against the oracle.  Both schedules are
+covered: the phased launches (small batches) and the ticket kernel, each
+against the oracle and against each other (bitwise)."""
 
 from __future__ import annotations
+
+import contextlib
+import os
 
 import numpy as np
 import pytest
@@ -19,6 +24,22 @@ from tests.helpers import assert_close, rel_l2, to_dev
 pytestmark = pytest.mark.gpu
 
 LIMIT = 10.0
+PATH_KEY = "EXL3_MOE_PHASED_MAX_ROWS"
+
+
+@contextlib.contextmanager
+def moe_path(path):
+    """Forces the schedule the library picks by batch size: 'ticket' (one
+    launch) or 'phased' (four launches) at every row count."""
+    old = os.environ.get(PATH_KEY)
+    os.environ[PATH_KEY] = {"ticket": "0", "phased": "16"}[path]
+    try:
+        yield
+    finally:
+        if old is None:
+            os.environ.pop(PATH_KEY, None)
+        else:
+            os.environ[PATH_KEY] = old
 
 
 class Layer:
@@ -120,19 +141,42 @@ def check(layer, x16, ids, w, what, **kw):
     return got, ref
 
 
+@pytest.mark.parametrize("path", ["ticket", "phased"])
 @pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 7, 8, 15, 16])
-def test_rows_random_routes(small, m):
-    print(f"moe m={m}", flush=True)
+def test_rows_random_routes(small, m, path):
+    print(f"moe m={m} {path}", flush=True)
     ids, w = synth.routing(m, 16, 6, seed=100 + m)
-    check(small, inputs(m, "real"), ids, w, f"m={m}")
+    with moe_path(path):
+        check(small, inputs(m, "real"), ids, w, f"m={m} {path}")
 
 
+@pytest.mark.parametrize("path", ["ticket", "phased"])
 @pytest.mark.parametrize("profile", ["unique", "hot", "zipf", "boundary", "within-row-dup", "R_e16", "invalid"])
-def test_route_profiles(small, profile):
-    print(f"moe profile={profile}", flush=True)
-    for m in (1, 4, 16):
+def test_route_profiles(small, profile, path):
+    print(f"moe profile={profile} {path}", flush=True)
+    with moe_path(path):
+        for m in (1, 4, 16):
+            ids = route_ids(m, profile)
+            check(small, inputs(m, "real"), ids, route_weights(m, "normal"), f"{profile} m={m} {path}")
+
+
+@pytest.mark.parametrize("profile", ["zipf", "within-row-dup", "invalid"])
+def test_phased_equals_ticket_bitwise(small, profile):
+    """The two schedules run the same items and add in the same order: every
+    output bit agrees, at every batch size."""
+    import torch
+
+    for m in (1, 2, 5, 16):
+        print(f"phased vs ticket {profile} m={m}", flush=True)
         ids = route_ids(m, profile)
-        check(small, inputs(m, "real"), ids, route_weights(m, "normal"), f"{profile} m={m}")
+        w = route_weights(m, "normal")
+        x = inputs(m, "real")
+        with moe_path("ticket"):
+            a = small.run(x, ids, w)
+        with moe_path("phased"):
+            b = small.run(x, ids, w)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"{profile} m={m}: phased and ticket outputs differ"
 
 
 def test_cancel_and_zero_weights(small):
@@ -247,6 +291,21 @@ def test_c2_against_oracle(c2, m):
     got = c2.run(x, ids, w).cpu().numpy()
     ref = c2.ref(x, ids, w)
     assert_close(got, ref, what=f"C2 m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_c2_phased_equals_ticket(c2, m):
+    import torch
+
+    print(f"c2 phased vs ticket m={m}", flush=True)
+    ids, w = synth.routing(m, 256, 8, seed=1100 + m)
+    x = synth.activations(m, 4096, seed=1100 + m)
+    with moe_path("ticket"):
+        a = c2.run(x, ids, w)
+    with moe_path("phased"):
+        b = c2.run(x, ids, w)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b), f"C2 m={m}: phased and ticket outputs differ"
 
 
 def test_c2_size_independent_properties(c2, dev):
