@@ -793,23 +793,31 @@ __global__ __launch_bounds__(64, 2) void moe_phase_down(Params P) {
     });
 }
 
-// Launch 4: item = (column block of H, row): each slot's down output (finish
-// of its pair) summed in top-k slot order (fp32), one cast.
+// Launch 4: item = (column block of H, row), one wave per top-k slot: each
+// wave finishes its slot's down output (the split-K sum, output Hadamard,
+// svh), so every slot's loads are in flight at once; wave 0 then adds them in
+// top-k slot order (fp32) and casts once.
 template <int DUMMY = 0>
-__global__ __launch_bounds__(64) void moe_phase_finish(Params P) {
+__global__ __launch_bounds__(MAX_TOPK * WAVE) void moe_phase_finish(Params P) {
+    __shared__ float4_t slot_val[MAX_TOPK][WAVE];
     const Layout& L = P.L;
     const Plan* pl = at<Plan>(P.scratch, L.plan);
     const int cb = blockIdx.x / P.m, row = blockIdx.x - (blockIdx.x / P.m) * P.m;
-    const int lane = threadIdx.x;
+    const int j = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    float s4[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < P.topk; ++j) {
-        const int pair = pl->slotpair[row * P.topk + j];
-        if (pair < 0) continue;
+    const int pair = pl->slotpair[row * P.topk + j];
+    if (pair >= 0) {
         uint16_t dsv[4];
         load_half4(dsv, P.dsv[P.ids[row * P.topk + j]], col);
-        const float4_t o = down_value<CPOL_PLAIN>(P, pair, dsv, col);
-        const float w = P.w[row * P.topk + j];
+        slot_val[j][lane] = down_value<CPOL_PLAIN>(P, pair, dsv, col);
+    }
+    __syncthreads();
+    if (j != 0) return;
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < P.topk; ++k) {      // fp32 sum in top-k slot order
+        if (pl->slotpair[row * P.topk + k] < 0) continue;
+        const float w = P.w[row * P.topk + k];
+        const float4_t o = slot_val[k][lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) s4[i] = s4[i] + w * o[i];
     }

@@ -33,7 +33,7 @@ int launch_phased<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int groups, int l
     hipLaunchKernelGGL((moe_phase_down<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(groups * L.nH * L.SB), dim3(WAVE), lds,
                        stream, P);
     if ((rc = check_launch())) return rc;
-    hipLaunchKernelGGL((moe_phase_finish<0>), dim3(L.nH * P.m), dim3(WAVE), 0, stream, P);
+    hipLaunchKernelGGL((moe_phase_finish<0>), dim3(L.nH * P.m), dim3(P.topk * WAVE), 0, stream, P);
     return check_launch();
 }
 
