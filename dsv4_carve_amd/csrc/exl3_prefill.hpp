@@ -167,14 +167,17 @@ __device__ __forceinline__ void pf_tile(bool valid, int wave, const uint16_t* A,
         ac[0][0] = a0[s * astep]; ac[0][1] = a0[s * astep + 1];
         ac[1][0] = a1[s * astep]; ac[1][1] = a1[s * astep + 1];
     };
+    // Each step's A loads are issued before the next step's tile loads: the
+    // wait for A (needed at once) then leaves the tile prefetch in flight
+    // (loads complete in issue order, so A issued after it would wait for it).
     if (valid) load_tile<BITS>(t0, tp);
     for (int s = 0; s < (valid ? nsteps : 0); s += 2) {
-        load_tile<BITS>(t1, tp + (s + 1) * tstep);
         load_a(s);
+        load_tile<BITS>(t1, tp + (s + 1) * tstep);
         mma_tile2<BITS, CB>(t0.words(), ac, acc);
+        load_a(s + 1);
         // the last iteration reloads its own step (a valid address, unused)
         load_tile<BITS>(t0, tp + min(s + 2, nsteps - 1) * tstep);
-        load_a(s + 1);
         mma_tile2<BITS, CB>(t1.words(), ac, acc);
     }
 
