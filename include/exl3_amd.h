@@ -55,7 +55,7 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
               void* scratch, int64_t scratch_bytes, void* stream);
 
 /*
- * Routed-MoE decode layer, one launch: for every row r and top-k slot j with a
+ * Routed-MoE decode layer: for every row r and top-k slot j with a
  * valid expert e = expert_ids[r][j] (0 <= e < n_experts; others are skipped):
  *   g = had_out(had_in(x[r] . gate_suh[e]) . Wgate[e]) . gate_svh[e]   (fp32)
  *   u = same with up;  act = half(silu(min(g, L)) * clamp(u, -L, L))
@@ -77,7 +77,13 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
  *   scratch: >= exl3_moe_scratch_bytes(hidden, intermediate, topk) bytes, zeroed
  *     once before first use; self-resetting afterwards, and one buffer may
  *     serve layers of different shapes (its control words have fixed
- *     offsets).  One launch at a time per scratch buffer.
+ *     offsets).  One call at a time per scratch buffer.
+ * Schedule: one persistent ticket-kernel launch for long layers, four plain
+ * launches for short ones (below ~40 decode steps per resident wave); both
+ * give bitwise the same result.  The environment variable
+ * EXL3_MOE_PHASED_MAX_ROWS, when set, picks by row count instead (0: always
+ * the single launch).  Every launch is on `stream`; nothing is allocated or
+ * synchronised, so a call can be captured in a graph.
  */
 int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk);
 int exl3_moe_max_rows(void);
