@@ -108,6 +108,9 @@ __device__ __forceinline__ half8_t a_from_words(const u32x4_t& lo, const u32x4_t
 }
 
 // The 64 MFMAs of one decoded tile, each B operand applied to both row blocks.
+// Software-pipelined by one operand: row block 1's MFMA on the previous B is
+// issued halfway through decoding the next B, so no two MFMAs are adjacent
+// (back to back, the second waits for the matrix pipe).
 template <int BITS, int CB>
 __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[2][2], float4_t (&acc)[2][16]) {
     half8_t A0[4], A1[4];
@@ -116,21 +119,25 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
         A0[r] = a_from_words(a[0][0], a[0][1], r);
         A1[r] = a_from_words(a[1][0], a[1][1], r);
     }
-    static_for<16>([&](auto NI) {
-        constexpr int n = decltype(NI)::value;
-        static_for<4>([&](auto RI) {
-            constexpr int r = decltype(RI)::value;
-            constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
-            u32x4_t b;
-            b[0] = decode_pair<BITS, CB, T0 + 0>(W);
-            b[1] = decode_pair<BITS, CB, T0 + 1>(W);
-            b[2] = decode_pair<BITS, CB, T0 + 2>(W);
-            b[3] = decode_pair<BITS, CB, T0 + 3>(W);
-            const half8_t B = __builtin_bit_cast(half8_t, b);
-            acc[0][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[r], B, acc[0][n], 0, 0, 0);
-            acc[1][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[r], B, acc[1][n], 0, 0, 0);
-        });
+    half8_t Bprev;
+    static_for<64>([&](auto II) {
+        constexpr int i = decltype(II)::value;
+        constexpr int n = i / 4, r = i % 4;
+        constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+        u32x4_t b;
+        b[0] = decode_pair<BITS, CB, T0 + 0>(W);
+        b[1] = decode_pair<BITS, CB, T0 + 1>(W);
+        if constexpr (i > 0) {
+            constexpr int np = (i - 1) / 4, rp = (i - 1) % 4;
+            acc[1][np] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[rp], Bprev, acc[1][np], 0, 0, 0);
+        }
+        b[2] = decode_pair<BITS, CB, T0 + 2>(W);
+        b[3] = decode_pair<BITS, CB, T0 + 3>(W);
+        const half8_t B = __builtin_bit_cast(half8_t, b);
+        acc[0][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[r], B, acc[0][n], 0, 0, 0);
+        Bprev = B;
     });
+    acc[1][15] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[3], Bprev, acc[1][15], 0, 0, 0);
 }
 
 // One (tile, 256-column block) of C[rows, N] = A[rows, K] . Wq[K, N], rows of A
