@@ -121,6 +121,68 @@ def dense_bytes(k: int, n: int, bits: int, rows: int) -> int:
     return k * n * bits // 8 + 2 * (k + n) + rows * k * 2 + rows * n * 2
 
 
+# Same-input fans of one dense layer (6-bit): the h-fan (wq_a, wkv, compressor
+# wkv/wgate, indexer compressor x2 read the 4096-wide hidden state) and the
+# q_a-fan (wq_b and indexer.wq_b read the 1024-wide q latent).
+FANS = {"h_fan_4096_to_1024_512_1024_1024_256_256": (4096, [1024, 512, 1024, 1024, 256, 256], 6),
+        "q_a_fan_1024_to_32768_8192": (1024, [32768, 8192], 6)}
+
+
+def time_fan(dev, k, ns, bits, rows_list, steps=40):
+    """us per fan call, cold (distinct weight copies cycled so none is still in
+    the MALL): one fused exl3_gemm_group call, and the members' solo exl3_gemm
+    calls one after another."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(k * 131 + sum(ns) + bits)
+    wbytes = sum(k * n * bits // 8 for n in ns)
+    copies = max(2, -(-(600 << 20) // wbytes))
+
+    def member(n):
+        t = torch.randint(-32768, 32767, (k // 16, n // 16, 16 * bits), dtype=torch.int16, device=dev, generator=g)
+        suh = (torch.randint(0, 2, (k,), device=dev, generator=g) * 2 - 1).to(torch.float16)
+        svh = ((torch.randint(0, 2, (n,), device=dev, generator=g) * 2 - 1) *
+               (torch.rand(n, device=dev, generator=g) * 1.5 + 0.5) / k ** 0.5).to(torch.float16)
+        return t, suh, svh
+
+    pool = [[member(n) for n in ns] for _ in range(copies)]
+    res = {}
+    for rows in rows_list:
+        x = torch.randn((rows, k), device=dev, generator=g).to(torch.float16)
+        outs = [torch.empty((rows, n), dtype=torch.float32, device=dev) for n in ns]
+        for n in ns:
+            ops.prepare_gemm(dev, rows, k, n)
+        out = {}
+        calls = {"fused": lambda mem: ops.gemm_group(x, mem, outs=outs),
+                 "solo": lambda mem: [ops.gemm_into(x, t, su, sv, o) for (t, su, sv), o in zip(mem, outs)]}
+        for mode, call in calls.items():
+            order = [i % copies for i in range(steps)]
+            for i in order[:3]:
+                call(pool[i])
+            torch.cuda.synchronize()
+            stream = torch.cuda.Stream()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                for i in order:
+                    call(pool[i])
+            graph.replay()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            torch.cuda.synchronize()
+            out[mode] = a.elapsed_time(b) * 1000.0 / steps
+        nb = sum(dense_bytes(k, n, bits, rows) for n in ns)
+        res[str(rows)] = {"fused_us": round(out["fused"], 2), "solo_us": round(out["solo"], 2),
+                          "fused_GBps": round(nb / (out["fused"] * 1e-6) / 1e9, 1)}
+    del pool
+    torch.cuda.empty_cache()
+    return res
+
+
 def time_dense(dev, k, n, bits, rows_list, steps=40):
     """us per call of the trellis-decode GEMV for each row count, cold (cycling
     through > 512 MB of distinct weight copies, so no copy is still in the
@@ -351,7 +413,7 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
     }
 
 
-EXTRA_LEGS = ("sweep", "tp8", "prefill", "stack", "dense")
+EXTRA_LEGS = ("sweep", "tp8", "prefill", "stack", "dense", "fan")
 
 
 def main() -> int:
@@ -449,6 +511,13 @@ def main() -> int:
             extra["dense_4096x4096_K6_cpu"] = {"us": round(t * 1e6, 1), "cores": CB.threads(),
                                                "sample": "dequant + fp32 matmul per call, median of 5 after 1 warm-up"}
             print(f"[bench] dense cpu: {extra['dense_4096x4096_K6_cpu']}", file=sys.stderr, flush=True)
+
+    if "fan" in legs:
+        fans = {}
+        for name, (k, ns, b) in FANS.items():
+            fans[name] = time_fan(dev, k, ns, b, DENSE_ROWS)
+            print(f"[bench] fan {name}: {fans[name]}", file=sys.stderr, flush=True)
+        extra["dense_fan_cold"] = fans
 
     cpu = None
     if not a.no_cpu:

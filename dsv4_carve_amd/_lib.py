@@ -18,6 +18,8 @@ EXPORTS = (
     "exl3_dequant",
     "exl3_gemm_scratch_bytes",
     "exl3_gemm",
+    "exl3_gemm_group_scratch_bytes",
+    "exl3_gemm_group",
     "exl3_moe_scratch_bytes",
     "exl3_moe_max_rows",
     "exl3_moe_decode",
@@ -39,6 +41,8 @@ _SIGS = {
     "exl3_dequant": ([_P, _L, _L, _I, _I, _P, _P, _P, _P], _I),
     "exl3_gemm_scratch_bytes": ([_L, _L, _L], _L),
     "exl3_gemm": ([_P, _L, _L, _P, _L, _I, _I, _P, _P, _P, _I, _P, _L, _P], _I),
+    "exl3_gemm_group_scratch_bytes": ([_L, _L, _L, _P], _L),
+    "exl3_gemm_group": ([_P, _L, _L, _L, _P, _P, _P, _P, _P, _I, _P, _I, _P, _L, _P], _I),
     "exl3_moe_scratch_bytes": ([_L, _L, _L], _L),
     "exl3_moe_max_rows": ([], _I),
     "exl3_moe_decode": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,

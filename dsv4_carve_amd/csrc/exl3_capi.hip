@@ -4,6 +4,9 @@
 //   exl3_gemm               <- exl3_gemm        recipe-lna/exllamav3/exl3_gemm.cu.lna:336-364
 //                              (and the exl3_gemv entry, recipe-lna/lna2/bindings.cpp:135-148)
 //   exl3_gemm_scratch_bytes    scratch sizing for exl3_gemm
+//   exl3_gemm_group         <- exl3_mgemm with a broadcast A (same-input fan)
+//                              recipe-lna/vllm_exl3_exl3.py.lna:546-613
+//   exl3_gemm_group_scratch_bytes
 //   exl3_last_error            message of the last failed call on this thread
 #include "exl3_dense.hpp"
 
@@ -82,6 +85,92 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
                                c_kind, R, (int)n, p.n_kc);
             if ((rc = check_launch())) return rc;
         }
+    }
+    return 0;
+}
+
+// Fan scratch: per member, partials [n_kc][min(m, 16)][n_j] fp32, each member's
+// region 256-byte aligned.
+static int64_t fan_scratch(int64_t m, int64_t k, int64_t count, const int64_t* n_list, int cus, GemvPlan* plan,
+                           int64_t* offsets) {
+    int64_t total_cb = 0;
+    for (int64_t j = 0; j < count; ++j) total_cb += (n_list[j] + COLS - 1) / COLS;
+    const GemvPlan p = gemv_fan_plan(k, total_cb, cus);
+    const int64_t rows = m < MAX_ROWS ? m : MAX_ROWS;
+    int64_t o = 0;
+    for (int64_t j = 0; j < count; ++j) {
+        if (offsets) offsets[j] = o;
+        o = align_up(o + (int64_t)p.n_kc * rows * n_list[j] * 4, 256);
+    }
+    if (plan) *plan = p;
+    return o;
+}
+
+static int check_fan(int64_t m, int64_t k, int64_t count, const int64_t* n_list) {
+    if (m <= 0) return fail("m must be positive");
+    if (k <= 0 || k % 128) return fail("k must be a positive multiple of 128");
+    if (count < 1 || count > MAX_FAN) return fail("a fan has 1..8 matrices");
+    if (!n_list) return fail("null pointer");
+    for (int64_t j = 0; j < count; ++j)
+        if (n_list[j] <= 0 || n_list[j] % 128) return fail("every n must be a positive multiple of 128");
+    return 0;
+}
+
+int64_t exl3_gemm_group_scratch_bytes(int64_t m, int64_t k, int64_t count, const int64_t* n_list) {
+    clear_error();
+    if (int rc = check_fan(m, k, count, n_list)) return rc;
+    return fan_scratch(m, k, count, n_list, device_cus(), nullptr, nullptr);
+}
+
+int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, const int16_t* const* trellis,
+                    const uint16_t* const* suh, const uint16_t* const* svh, const int64_t* n_list,
+                    const int32_t* bits_list, int codebook, void* const* c, int c_kind, void* scratch,
+                    int64_t scratch_bytes, void* stream) {
+    clear_error();
+    if (int rc = check_fan(m, k, count, n_list)) return rc;
+    if (!a || !trellis || !suh || !svh || !bits_list || !c || !scratch) return fail("null pointer");
+    if (codebook < CB_3INST || codebook > CB_MUL1) return fail("codebook must be 0 (3inst), 1 (mcg) or 2 (mul1)");
+    if (c_kind < OUT_F16 || c_kind > OUT_F32) return fail("c_kind must be 0 (fp16), 1 (bf16) or 2 (fp32)");
+    uint32_t widths = 0;
+    for (int64_t j = 0; j < count; ++j) {
+        if (!trellis[j] || !suh[j] || !svh[j] || !c[j]) return fail("null pointer");
+        if (bits_list[j] < 1 || bits_list[j] > 8) return fail("bits must be in 1..8");
+        widths |= 1u << bits_list[j];
+    }
+    const int cus = device_cus();
+    GemvPlan p;
+    int64_t offsets[MAX_FAN];
+    if (scratch_bytes < fan_scratch(m, k, count, n_list, cus, &p, offsets)) return fail("scratch too small");
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const size_t c_elem = c_kind == OUT_F32 ? 4 : 2;
+    for (int64_t r0 = 0; r0 < m; r0 += MAX_ROWS) {
+        const int R = (int)(m - r0 < MAX_ROWS ? m - r0 : MAX_ROWS);
+        FanParams P{};
+        P.x = a + r0 * k;
+        P.R = R; P.K = (int)k; P.nsteps = p.nsteps; P.n_kc = p.n_kc; P.count = (int)count; P.out_kind = c_kind;
+        int blocks = 0, rblocks = 0;
+        for (int64_t j = 0; j < count; ++j) {
+            const int n_cb = (int)((n_list[j] + COLS - 1) / COLS);
+            P.trellis[j] = trellis[j]; P.suh[j] = suh[j]; P.svh[j] = svh[j];
+            P.out[j] = reinterpret_cast<char*>(c[j]) + (size_t)r0 * n_list[j] * c_elem;
+            P.partials[j] = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + offsets[j]);
+            P.N[j] = (int)n_list[j];
+            P.bits[j] = bits_list[j];
+            P.block0[j] = blocks;
+            P.rblock0[j] = rblocks;
+            blocks += n_cb * p.n_kc;
+            rblocks += n_cb * R;
+        }
+        P.block0[count] = blocks;
+        P.rblock0[count] = rblocks;
+        for (int b = 1; b <= 8; ++b) {
+            if (!(widths & (1u << b))) continue;
+            int rc = 0;
+            EXL3_BITS_SWITCH(b, rc = launch_gemv_fan<B_>(P, codebook, blocks, s));
+            if (rc) return rc;
+        }
+        hipLaunchKernelGGL((gemv_fan_reduce_kernel<16>), dim3(rblocks), dim3(64), 0, s, P);
+        if (int rc = check_launch()) return rc;
     }
     return 0;
 }

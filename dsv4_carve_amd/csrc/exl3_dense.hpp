@@ -143,20 +143,15 @@ inline int64_t gemv_scratch_bytes(int64_t rows, int64_t k, int64_t n, int cus) {
     return ctr + (int64_t)p.n_kc * (rows < 16 ? rows : 16) * n * 4;
 }
 
-// SPLIT: store the partials and stop (gemv_reduce_kernel finishes them);
-// otherwise the last arriver of each column block finishes it.
-template <int BITS, int CB, bool SPLIT>
-__global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x,
-                                                  const int16_t* __restrict__ trellis,
-                                                  const uint16_t* __restrict__ suh,
-                                                  const uint16_t* __restrict__ svh, void* __restrict__ out,
-                                                  int out_kind, int R, int K, int N, int nsteps, int n_kc,
-                                                  int* __restrict__ counters, float* __restrict__ partials) {
-    __shared__ uint16_t xa[MAX_ROWS * GEMV_NSTEP_CAP * STEP_K];
-    const int lane = threadIdx.x;
-    const int cb = blockIdx.x / n_kc, kc = blockIdx.x - cb * n_kc;
+// Partial sums of one (256-column block cb, k-chunk kc) item of
+// y = had_in(x) . Wq for rows 0..R-1, stored as fp32 to
+// partials[kc][row][N] (DEV: device-scope stores, read in the same launch;
+// otherwise plain stores, read by a later launch).  xa: the block's LDS.
+template <int BITS, int CB, bool DEV>
+__device__ __forceinline__ void gemv_partials(const uint16_t* __restrict__ x, const int16_t* __restrict__ trellis,
+                                              const uint16_t* __restrict__ suh, int R, int K, int N, int nsteps,
+                                              int cb, int kc, float* __restrict__ partials, uint16_t* xa) {
     const int k0 = kc * nsteps * STEP_K;
-
     // weights for step 0 are in flight while the input rotation runs
     const u32x4_t* tp = tile_ptr<BITS>(trellis, N / 16, k0 / 16, cb * 16);
     TileRegs<BITS> first;
@@ -169,7 +164,22 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     mma_steps<BITS, CB, false>(first, tp, N / 16, nsteps, xa, GEMV_NSTEP_CAP, R, acc);
 
     const int cols = min(COLS, N - cb * COLS);
-    store_partials(acc, partials + (size_t)kc * R * N + cb * COLS, N, R, cols, reinterpret_cast<float*>(xa));
+    store_partials<DEV>(acc, partials + (size_t)kc * R * N + cb * COLS, N, R, cols, reinterpret_cast<float*>(xa));
+}
+
+// SPLIT: store the partials and stop (gemv_reduce_kernel finishes them);
+// otherwise the last arriver of each column block finishes it.
+template <int BITS, int CB, bool SPLIT>
+__global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x,
+                                                  const int16_t* __restrict__ trellis,
+                                                  const uint16_t* __restrict__ suh,
+                                                  const uint16_t* __restrict__ svh, void* __restrict__ out,
+                                                  int out_kind, int R, int K, int N, int nsteps, int n_kc,
+                                                  int* __restrict__ counters, float* __restrict__ partials) {
+    __shared__ uint16_t xa[MAX_ROWS * GEMV_NSTEP_CAP * STEP_K];
+    const int lane = threadIdx.x;
+    const int cb = blockIdx.x / n_kc, kc = blockIdx.x - cb * n_kc;
+    gemv_partials<BITS, CB, !SPLIT>(x, trellis, suh, R, K, N, nsteps, cb, kc, partials, xa);
     if constexpr (SPLIT) return;
     publish_fence();
     int old = 0;
@@ -196,16 +206,14 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     if (lane == 0) __hip_atomic_store(&counters[cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Split-K finish, one wave per (256-column block, row): the partials of chunks
+// Split-K finish of (256-column block cb, row m): the partials of chunks
 // 0..n_kc-1 summed in chunk order (as the last-arriver path does), output
-// Hadamard, svh, store.  Runs after gemv_kernel<.., true> on the same stream,
-// so plain loads see its partials.
+// Hadamard, svh, store.  Plain loads: a previous launch wrote the partials.
 template <int BATCH>
-__global__ __launch_bounds__(64) void gemv_reduce_kernel(const float* __restrict__ partials,
-                                                         const uint16_t* __restrict__ svh, void* __restrict__ out,
-                                                         int out_kind, int R, int N, int n_kc) {
-    const int lane = threadIdx.x;
-    const int cb = blockIdx.x / R, m = blockIdx.x - (blockIdx.x / R) * R;
+__device__ __forceinline__ void gemv_reduce_block(const float* __restrict__ partials, const uint16_t* __restrict__ svh,
+                                                  void* __restrict__ out, int out_kind, int R, int N, int n_kc,
+                                                  int cb, int m) {
+    const int lane = threadIdx.x & (WAVE - 1);
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
     const bool ok = col < N;
     float v[4] = {0.f, 0.f, 0.f, 0.f};
@@ -230,6 +238,83 @@ __global__ __launch_bounds__(64) void gemv_reduce_kernel(const float* __restrict
             store_out(out, (size_t)m * N + col + e, out_kind, v[e] * HAD_NORM * f16_bits_to_f32(svh[col + e]));
 }
 
+// Split-K finish, one wave per (256-column block, row).  Runs after
+// gemv_kernel<.., true> on the same stream.
+template <int BATCH>
+__global__ __launch_bounds__(64) void gemv_reduce_kernel(const float* __restrict__ partials,
+                                                         const uint16_t* __restrict__ svh, void* __restrict__ out,
+                                                         int out_kind, int R, int N, int n_kc) {
+    const int cb = blockIdx.x / R, m = blockIdx.x - (blockIdx.x / R) * R;
+    gemv_reduce_block<BATCH>(partials, svh, out, out_kind, R, N, n_kc, cb, m);
+}
+
+// ---------------------------------------------------------------- same-input fan
+//
+// Several matrices that read the same input x (same K, each with its own
+// suh/svh, N, bit width and output): one launch of partial sums over all of
+// them per bit width present, then one split-K finish launch over all of them.
+// A matrix's items and sums are those of exl3_gemm at the fan's k-chunking.
+// Reference counterpart: exl3_mgemm with a broadcast A (bszm_in == 1),
+// recipe-lna/vllm_exl3_exl3.py.lna:546-613.
+
+constexpr int MAX_FAN = 8;
+
+struct FanParams {
+    const uint16_t* x;
+    int R, K, nsteps, n_kc, count, out_kind;
+    const int16_t* trellis[MAX_FAN];
+    const uint16_t* suh[MAX_FAN];
+    const uint16_t* svh[MAX_FAN];
+    void* out[MAX_FAN];
+    float* partials[MAX_FAN];
+    int N[MAX_FAN];
+    int bits[MAX_FAN];
+    int block0[MAX_FAN + 1];    // partial-sum items: member j owns [block0[j], block0[j+1])
+    int rblock0[MAX_FAN + 1];   // finish items: member j owns [rblock0[j], rblock0[j+1])
+};
+
+__device__ __forceinline__ int fan_member(const int (&first)[MAX_FAN + 1], int count, int blk) {
+    int j = 0;
+    while (j + 1 < count && blk >= first[j + 1]) ++j;
+    return j;
+}
+
+// Items of the members with bit width BITS; the other members' items return
+// at once (one launch per width present).
+template <int BITS, int CB>
+__global__ __launch_bounds__(64) void gemv_fan_kernel(FanParams P) {
+    __shared__ uint16_t xa[MAX_ROWS * GEMV_NSTEP_CAP * STEP_K];
+    const int j = fan_member(P.block0, P.count, blockIdx.x);
+    if (P.bits[j] != BITS) return;
+    const int local = blockIdx.x - P.block0[j];
+    const int cb = local / P.n_kc, kc = local - (local / P.n_kc) * P.n_kc;
+    gemv_partials<BITS, CB, false>(P.x, P.trellis[j], P.suh[j], P.R, P.K, P.N[j], P.nsteps, cb, kc,
+                                   P.partials[j], xa);
+}
+
+template <int BATCH>
+__global__ __launch_bounds__(64) void gemv_fan_reduce_kernel(FanParams P) {
+    const int j = fan_member(P.rblock0, P.count, blockIdx.x);
+    const int local = blockIdx.x - P.rblock0[j];
+    const int cb = local / P.R, m = local - (local / P.R) * P.R;
+    gemv_reduce_block<BATCH>(P.partials[j], P.svh[j], P.out[j], P.out_kind, P.R, P.N[j], P.n_kc, cb, m);
+}
+
+// k-chunking of a fan: as gemv_plan, over the column blocks of every member.
+inline GemvPlan gemv_fan_plan(int64_t k, int64_t total_cb, int cus) {
+    GemvPlan p;
+    p.n_cb = (int)total_cb;
+    const int ksteps = (int)(k / STEP_K);
+    int nsteps = GEMV_NSTEP_CAP;
+    while (nsteps > 2 && total_cb * (ksteps / nsteps) < 4LL * cus) nsteps /= 2;
+    while (ksteps % nsteps) nsteps /= 2;
+    if (nsteps < 2) nsteps = 2;
+    p.nsteps = nsteps;
+    p.n_kc = ksteps / nsteps;
+    p.split_reduce = true;
+    return p;
+}
+
 // ---------------------------------------------------------------- per-bit-width launchers
 
 struct DequantArgs {
@@ -245,5 +330,6 @@ struct GemvArgs {
 // Defined in exl3_dense_inst.hip, one translation unit per BITS.
 template <int BITS> int launch_dequant(const DequantArgs& a);
 template <int BITS> int launch_gemv(const GemvArgs& a);
+template <int BITS> int launch_gemv_fan(const FanParams& P, int codebook, int blocks, hipStream_t stream);
 
 }  // namespace exl3

@@ -52,4 +52,19 @@ int launch_gemv<EXL3_BITS>(const GemvArgs& a) {
     return check_launch();
 }
 
+template <>
+int launch_gemv_fan<EXL3_BITS>(const FanParams& P, int codebook, int blocks, hipStream_t stream) {
+    constexpr int B = EXL3_BITS;
+    auto go = [&](auto cbc) {
+        constexpr int C = decltype(cbc)::value;
+        hipLaunchKernelGGL((gemv_fan_kernel<B, C>), dim3(blocks), dim3(64), 0, stream, P);
+    };
+    switch (codebook) {
+        case CB_MCG: go(std::integral_constant<int, CB_MCG>{}); break;
+        case CB_3INST: go(std::integral_constant<int, CB_3INST>{}); break;
+        default: go(std::integral_constant<int, CB_MUL1>{}); break;
+    }
+    return check_launch();
+}
+
 }  // namespace exl3

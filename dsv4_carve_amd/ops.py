@@ -142,7 +142,29 @@ def _prefill_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, expe
         _ptr(scratch), scratch.numel(), _stream(x.device)))
 
 
+_LIB.define("gemm_group(Tensor a, Tensor[] b, Tensor(a!)[] c, Tensor[] suh, Tensor[] svh, int codebook, "
+            "Tensor(b!) scratch) -> ()")
+
+
+def _host_array(ctype, values):
+    return (ctype * len(values))(*values)
+
+
+def _gemm_group_impl(a, b, c, suh, svh, codebook, scratch):
+    import ctypes
+
+    L = _lib.load()
+    m, k = a.shape
+    count = len(b)
+    ns = _host_array(ctypes.c_int64, [int(t.shape[1]) * 16 for t in b])
+    bits = _host_array(ctypes.c_int32, [int(t.shape[2]) // 16 for t in b])
+    ptrs = lambda ts: _host_array(ctypes.c_void_p, [int(t.data_ptr()) for t in ts])
+    _lib.check(L.exl3_gemm_group(_ptr(a), m, k, count, ptrs(b), ptrs(suh), ptrs(svh), ns, bits, int(codebook),
+                                 ptrs(c), OUT_KIND[c[0].dtype], _ptr(scratch), scratch.numel(), _stream(a.device)))
+
+
 _LIB.impl("moe_prefill", _prefill_impl, "CUDA")
+_LIB.impl("gemm_group", _gemm_group_impl, "CUDA")
 _LIB.impl("dequant", _dequant_impl, "CUDA")
 _LIB.impl("gemm", _gemm_impl, "CUDA")
 _LIB.impl("moe_decode", _moe_impl, "CUDA")
@@ -233,6 +255,49 @@ def gemm(x: torch.Tensor, trellis: torch.Tensor, suh: torch.Tensor, svh: torch.T
          codebook: int = CB_MCG, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     c = torch.empty((x.shape[0], trellis.shape[1] * 16), dtype=out_dtype, device=x.device)
     return gemm_into(x, trellis, suh, svh, c, codebook)
+
+
+MAX_GROUP = 8
+
+
+def gemm_group_scratch(device: torch.device, m: int, k: int, ns) -> torch.Tensor:
+    import ctypes
+
+    arr = (ctypes.c_int64 * len(ns))(*[int(n) for n in ns])
+    nbytes = _lib.check(_lib.load().exl3_gemm_group_scratch_bytes(m, k, len(ns), arr))
+    return SCRATCH.get(device, "gemm_group", nbytes)
+
+
+def gemm_group(x: torch.Tensor, members, codebook: int = CB_MCG,
+               out_dtype: torch.dtype = torch.float32, outs=None) -> list[torch.Tensor]:
+    """One fused call for several EXL3 matrices that read the same input:
+    members = [(trellis, suh, svh), ...] (1..8, same in_features, any out
+    features and bit widths); returns [had_out(had_in(x*suh_j) @ Wq_j) * svh_j].
+    The role of exllamav3_ext.exl3_mgemm with a broadcast A
+    (recipe-lna/vllm_exl3_exl3.py.lna:546-613)."""
+    _check(x.dim() == 2 and x.dtype == torch.float16 and x.is_contiguous(), "x must be contiguous fp16 [m, k]")
+    _check(1 <= len(members) <= MAX_GROUP, "a group has 1..8 matrices")
+    m, k = x.shape
+    ts, us, vs, ns = [], [], [], []
+    for trellis, suh, svh in members:
+        _check_trellis(trellis)
+        n = trellis.shape[1] * 16
+        _check(trellis.shape[0] * 16 == k, "every member must read the input's feature dimension")
+        _check(n % 128 == 0 and k % 128 == 0, "in and out features must be multiples of 128")
+        _check(suh.dtype == torch.float16 and suh.numel() == k and suh.is_contiguous(), "suh must be fp16 [k]")
+        _check(svh.dtype == torch.float16 and svh.numel() == n and svh.is_contiguous(), "svh must be fp16 [n]")
+        for t in (trellis, suh, svh):
+            _check(t.device == x.device, "all tensors must be on the same device")
+        ts.append(trellis); us.append(suh); vs.append(svh); ns.append(n)
+    if outs is None:
+        outs = [torch.empty((m, n), dtype=out_dtype, device=x.device) for n in ns]
+    _check(len(outs) == len(ns), "one output per member")
+    for c, n in zip(outs, ns):
+        _check(c.dtype == outs[0].dtype and c.dtype in OUT_KIND and c.is_contiguous() and tuple(c.shape) == (m, n),
+               "outputs must be contiguous [m, n_j] of one dtype")
+    scratch = gemm_group_scratch(x.device, m, k, ns)
+    torch.ops.exl3_amd.gemm_group(x, ts, outs, us, vs, codebook, scratch)
+    return outs
 
 
 def exl3_gemm(A: torch.Tensor, B: torch.Tensor, C: torch.Tensor, suh: torch.Tensor | None,

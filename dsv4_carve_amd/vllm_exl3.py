@@ -13,6 +13,10 @@ error behaviour, so the plugin's dispatch code can switch to this package:
     selection by VLLM_EXL3_MOE_KERNEL, strict levels by VLLM_EXL3_MOE_STRICT,
     one-shot decline logging, per-backend call counters, the shared zeroed
     scratch, and the unique-expert LinearEXL3 loop.
+  * ``run_exl3_group`` and its helpers -- one fused call for the EXL3 shards
+    of a module that read the same input, by LNA_EXL3_DENSE_GROUP
+    (recipe-lna/vllm_exl3_exl3.py.lna:62-802; the cross-module T1 fans are
+    not built).
   * ``Exl3MoEMethod`` / ``Exl3LinearMethod`` -- create_weights /
     process_weights_after_loading / apply (recipe-lna/vllm_exl3_exl3.py.lna:2045-2307,
     2310-2853), importable without vLLM.
@@ -180,6 +184,176 @@ def execute_exl3_linear(x, trellis, suh, svh, mcg=None, mul1=None, *, out_dtype=
     """recipe-lna/vllm_exl3_exl3.py.lna:914-926."""
     inner = make_linear_exl3(trellis, suh, svh, mcg, mul1, out_dtype=torch.float16)
     return inner.forward(x.contiguous().half(), {}, out_dtype=out_dtype)
+
+
+# ---------------------------------------------------------------- dense groups (same-input fans)
+#
+# LNA_EXL3_DENSE_GROUP (recipe-lna/vllm_exl3_exl3.py.lna:121-135): 0 = off
+# (every shard its own call), 1 = T0 (the EXL3 shards of one module, which read
+# the same input, in one fused call), 2 = T1 (the reference's cross-module fans
+# with cached outputs; not built here: a module in a fan falls back to its own
+# T0 group with the reference's "T1 fan is not complete" decline).
+
+DENSE_GROUP_MAX_MATRICES = 8
+_DENSE_GROUP_STATS: dict[str, int] = {"t0_active": 0, "t1_active": 0, "fallback_total": 0, "prewarm_groups": 0}
+_DENSE_GROUP_FALLBACK_COUNTS: dict[str, int] = {}
+_DENSE_GROUP_CALL_COUNTS: dict[int, int] = {1: 0, 2: 0}
+_DENSE_GROUP_ACTIVE_LOGGED: set[str] = set()
+_DENSE_FAN_SUFFIXES = (".fused_wqa_wkv", ".indexer.compressor.fused_wkv_wgate", ".compressor.fused_wkv_wgate",
+                       ".indexer.wq_b", ".wq_b")
+
+
+def dense_group_mode() -> int:
+    """0 (off), 1 (T0) or 2 (T1); malformed values fail closed
+    (recipe-lna/vllm_exl3_exl3.py.lna:121-132)."""
+    raw = os.environ.get("LNA_EXL3_DENSE_GROUP", "0")
+    try:
+        mode = int(raw)
+    except (TypeError, ValueError):
+        _dense_group_fallback("config", f"invalid LNA_EXL3_DENSE_GROUP={raw!r}")
+        return 0
+    if mode not in (0, 1, 2):
+        _dense_group_fallback("config", f"unsupported LNA_EXL3_DENSE_GROUP={raw!r}")
+        return 0
+    return mode
+
+
+def dense_group_enabled() -> bool:
+    return dense_group_mode() != 0
+
+
+def _dense_group_fallback(reason: str, detail: str, group_id: str | None = None) -> None:
+    key = f"{reason}:{group_id or '*'}"
+    count = _DENSE_GROUP_FALLBACK_COUNTS.get(key, 0) + 1
+    _DENSE_GROUP_FALLBACK_COUNTS[key] = count
+    _DENSE_GROUP_STATS["fallback_total"] += 1
+    if count == 1:
+        logger.warning("DENSE_GROUP declined: %s: %s (group=%s)", reason, detail, group_id or "*")
+
+
+def _dense_group_active(mode: int, group_id: str) -> None:
+    _DENSE_GROUP_STATS["t0_active" if mode == 1 else "t1_active"] += 1
+    _DENSE_GROUP_CALL_COUNTS[mode] = _DENSE_GROUP_CALL_COUNTS.get(mode, 0) + 1
+    if group_id not in _DENSE_GROUP_ACTIVE_LOGGED:
+        _DENSE_GROUP_ACTIVE_LOGGED.add(group_id)
+        logger.info("DENSE_GROUP=%d ACTIVE for %s", mode, group_id)
+
+
+def dense_group_stats() -> dict[str, Any]:
+    return {**_DENSE_GROUP_STATS, "fallbacks": dict(_DENSE_GROUP_FALLBACK_COUNTS),
+            "active_groups": sorted(_DENSE_GROUP_ACTIVE_LOGGED)}
+
+
+def dense_group_call_counts() -> dict[int, int]:
+    return dict(_DENSE_GROUP_CALL_COUNTS)
+
+
+def reset_dense_group_state() -> None:
+    for key in _DENSE_GROUP_STATS:
+        _DENSE_GROUP_STATS[key] = 0
+    _DENSE_GROUP_FALLBACK_COUNTS.clear()
+    _DENSE_GROUP_ACTIVE_LOGGED.clear()
+    _DENSE_GROUP_CALL_COUNTS.update({1: 0, 2: 0})
+
+
+def _dense_group_members(linears: list, group_id: str) -> dict:
+    """Validated group descriptor (recipe-lna/vllm_exl3_exl3.py.lna:208-250): EXL3
+    members without bias, one codebook and in_features, out features multiples
+    of 128, at most eight.  Widths and output order are free here."""
+    if not linears:
+        raise ValueError("empty EXL3 group")
+    if not all(isinstance(lin, LinearEXL3) for lin in linears):
+        raise ValueError("non-EXL3 member")
+    if not all(lin.bias is None for lin in linears):
+        raise ValueError("a fused group never applies bias")
+    if len({lin.codebook for lin in linears}) != 1:
+        raise ValueError("mcg/mul1 must be uniform")
+    k = int(linears[0].in_features)
+    if not all(int(lin.in_features) == k for lin in linears):
+        raise ValueError("k must be uniform")
+    ns = [int(lin.out_features) for lin in linears]
+    if not all(n % 128 == 0 for n in ns) or k % 128:
+        raise ValueError(f"a fused group needs k and every n to be multiples of 128, k={k}, ns={ns}")
+    if len(ns) > DENSE_GROUP_MAX_MATRICES:
+        raise ValueError("dense group exceeds the matrix capacity")
+    return {"group_id": group_id, "members": [(lin.trellis, lin.suh, lin.svh) for lin in linears],
+            "codebook": linears[0].codebook, "k": k, "ns": ns}
+
+
+def build_exl3_dense_group(module) -> None:
+    """Build the module's group descriptor once after load (and before graph
+    capture).  Sentinels on ``_exl3_dense_group`` as in the reference
+    (recipe-lna/vllm_exl3_exl3.py.lna:508-545): missing = not yet checked,
+    None = checked and declined, dict = ready."""
+    if not dense_group_enabled() or hasattr(module, "_exl3_dense_group"):
+        return
+    linears = [lin for lin in getattr(module, "_exl3_linears", None) or [] if lin is not None]
+    if getattr(module, "_exl3_linear_bf16_shards", []) or len(linears) < 2:
+        module._exl3_dense_group = None
+        return
+    group_id = f"local:{getattr(module, 'prefix', '?')}:{id(module)}"
+    try:
+        module._exl3_dense_group = _dense_group_members(linears, group_id)
+    except ValueError as exc:
+        module._exl3_dense_group = None
+        _dense_group_fallback("registration", str(exc), group_id)
+
+
+def _in_dense_fan(module) -> bool:
+    prefix = getattr(module, "prefix", None) or ""
+    return any(prefix.endswith(sfx) for sfx in _DENSE_FAN_SUFFIXES)
+
+
+def run_exl3_group(module, x_fp16: torch.Tensor, out_dtype: torch.dtype = torch.float32, *,
+                   source_tensor: torch.Tensor | None = None) -> list:
+    """Forward every EXL3 shard of one module call on the same contiguous fp16
+    input (recipe-lna/vllm_exl3_exl3.py.lna:616-802).  With LNA_EXL3_DENSE_GROUP
+    = 1 (or 2) and the preconditions met, one fused same-input call replaces the
+    per-shard calls; any decline falls back to the per-linear forwards used when
+    the flag is off.  Returns one output per entry of module._exl3_linears, of
+    dtype `out_dtype`."""
+    del source_tensor            # keyed the reference's T1 output cache
+    linears = getattr(module, "_exl3_linears", None) or []
+    solo = lambda: [lin.forward(x_fp16, {}, out_dtype=out_dtype) for lin in linears]
+    mode = dense_group_mode()
+    if mode == 0:
+        return solo()
+    if len(linears) < 2:
+        _dense_group_fallback("registration", "no fused group is available for this single-shard module")
+        return solo()
+    if x_fp16.dtype is not torch.float16 or not x_fp16.is_contiguous() or x_fp16.dim() != 2:
+        _dense_group_fallback("input", "input must be contiguous 2D fp16")
+        return solo()
+    if out_dtype is not torch.float32:
+        _dense_group_fallback("dtype", f"unsupported C dtype {out_dtype}")
+        return solo()
+    m = x_fp16.shape[0]
+    if m > 16 or m < 1:
+        _dense_group_fallback("rows", f"rows={m} outside fused range 1..16")
+        return solo()
+    if mode == 2 and _in_dense_fan(module):
+        _dense_group_fallback("registration", "T1 fan is not complete; using the registered local T0 group",
+                              f"{getattr(module, 'prefix', '?')}:fan")
+    group = getattr(module, "_exl3_dense_group", None)
+    if group is None and not hasattr(module, "_exl3_dense_group"):
+        if torch.cuda.is_current_stream_capturing():
+            _dense_group_fallback("capture", "group tables missing during capture")
+            return solo()
+        build_exl3_dense_group(module)
+        group = getattr(module, "_exl3_dense_group", None)
+    if not group:
+        _dense_group_fallback("registration", "dense group tables are unavailable")
+        return solo()
+    if int(x_fp16.shape[1]) != group["k"]:
+        _dense_group_fallback("input", f"group k={group['k']} got {x_fp16.shape[1]}", group["group_id"])
+        return solo()
+    try:
+        outs = ops.gemm_group(x_fp16, group["members"], group["codebook"], out_dtype)
+    except Exception as exc:
+        _dense_group_fallback("error", repr(exc), group["group_id"])
+        return solo()
+    _dense_group_active(1, group["group_id"])
+    return outs
 
 
 # ---------------------------------------------------------------- backend selection

@@ -55,6 +55,25 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
               void* scratch, int64_t scratch_bytes, void* stream);
 
 /*
+ * Same-input fan: c_j[m][n_j] = had_out(had_in(a . suh_j) . Wq_j) . svh_j for
+ * count (1..8) matrices that read one input a (fp16 [m][k], k % 128 == 0): one
+ * launch of split-K partial sums over every member per bit width present, one
+ * finishing launch over all of them.  Replaces exllamav3 `exl3_mgemm` with a
+ * broadcast A (bszm_in == 1), as the plugin's dense groups call it
+ * (recipe-lna/vllm_exl3_exl3.py.lna:546-613); unlike it, members may differ in
+ * bit width and need not be ordered widest first.  trellis/suh/svh/c: host
+ * arrays of count device pointers; n_list: host int64 [count], each a multiple
+ * of 128; bits_list: host int32 [count] in 1..8; every c_j has c_kind.
+ * scratch: >= exl3_gemm_group_scratch_bytes(m, k, count, n_list) bytes (no
+ * zeroing needed); one call at a time per scratch buffer.
+ */
+int64_t exl3_gemm_group_scratch_bytes(int64_t m, int64_t k, int64_t count, const int64_t* n_list);
+int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, const int16_t* const* trellis,
+                    const uint16_t* const* suh, const uint16_t* const* svh, const int64_t* n_list,
+                    const int32_t* bits_list, int codebook, void* const* c, int c_kind, void* scratch,
+                    int64_t scratch_bytes, void* stream);
+
+/*
  * Routed-MoE decode layer: for every row r and top-k slot j with a
  * valid expert e = expert_ids[r][j] (0 <= e < n_experts; others are skipped):
  *   g = had_out(had_in(x[r] . gate_suh[e]) . Wgate[e]) . gate_svh[e]   (fp32)

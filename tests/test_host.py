@@ -116,6 +116,77 @@ def test_gemm_argument_errors_without_device(k, n, cb, kind, msg):
     assert msg in _err()
 
 
+@pytest.mark.parametrize("m,k,ns,msg", [
+    (0, 512, [256], "m must be positive"),
+    (1, 500, [256], "k must be a positive multiple of 128"),
+    (1, 512, [], "1..8"),
+    (1, 512, [256] * 9, "1..8"),
+    (1, 512, [256, 100], "every n must be a positive multiple of 128"),
+])
+def test_gemm_group_argument_errors_without_device(m, k, ns, msg):
+    lib = _lib.load()
+    arr = (ctypes.c_int64 * max(len(ns), 1))(*ns)
+    assert lib.exl3_gemm_group_scratch_bytes(m, k, len(ns), arr) == -1 and msg in _err()
+    p = ctypes.c_void_p(16)
+    ptrs = (ctypes.c_void_p * 9)(*([16] * 9))
+    bits = (ctypes.c_int32 * 9)(*([3] * 9))
+    assert lib.exl3_gemm_group(p, m, k, len(ns), ptrs, ptrs, ptrs, arr, bits, 1, ptrs, 2, p, 1 << 30, None) == -1
+    assert msg in _err()
+
+
+def test_gemm_group_width_and_kind_errors_without_device():
+    lib = _lib.load()
+    arr = (ctypes.c_int64 * 2)(256, 512)
+    p = ctypes.c_void_p(16)
+    ptrs = (ctypes.c_void_p * 2)(16, 16)
+    assert lib.exl3_gemm_group(p, 1, 512, 2, ptrs, ptrs, ptrs, arr, (ctypes.c_int32 * 2)(3, 9), 1, ptrs, 2, p,
+                               1 << 30, None) == -1 and "bits" in _err()
+    assert lib.exl3_gemm_group(p, 1, 512, 2, ptrs, ptrs, ptrs, arr, (ctypes.c_int32 * 2)(3, 4), 1, ptrs, 5, p,
+                               1 << 30, None) == -1 and "c_kind" in _err()
+
+
+@pytest.mark.parametrize("env,want,fallback", [(None, 0, False), ("0", 0, False), ("1", 1, False), ("2", 2, False),
+                                               ("x", 0, True), ("3", 0, True)])
+def test_dense_group_mode(monkeypatch, env, want, fallback):
+    V.reset_dense_group_state()
+    if env is None:
+        monkeypatch.delenv("LNA_EXL3_DENSE_GROUP", raising=False)
+    else:
+        monkeypatch.setenv("LNA_EXL3_DENSE_GROUP", env)
+    assert V.dense_group_mode() == want
+    assert any(k.startswith("config:") for k in V.dense_group_stats()["fallbacks"]) == fallback
+
+
+def test_dense_group_registration_checks(monkeypatch):
+    """Group descriptors: members must share in_features and codebook, carry
+    no bias, and at most eight; a declined module is marked None."""
+    monkeypatch.setenv("LNA_EXL3_DENSE_GROUP", "1")
+    V.reset_dense_group_state()
+
+    def lin(k, n, bits=3, mul1=False):
+        t = torch.zeros((k // 16, n // 16, 16 * bits), dtype=torch.int16)
+        mk = torch.tensor([V.MUL1_MARKER_SIGNED_INT32 if mul1 else V.MCG_MARKER_SIGNED_INT32])
+        return V.make_linear_exl3(t, torch.ones(k, dtype=torch.float16), torch.ones(n, dtype=torch.float16),
+                                  mcg=None if mul1 else mk, mul1=mk if mul1 else None)
+
+    class M:
+        def __init__(self, linears):
+            self._exl3_linears = linears
+            self.prefix = "model.layers.0.attn.fused_wqa_wkv"
+
+    ok = M([lin(512, 256), lin(512, 384, bits=6)])
+    V.build_exl3_dense_group(ok)
+    assert ok._exl3_dense_group["ns"] == [256, 384] and ok._exl3_dense_group["k"] == 512
+    for bad in (M([lin(512, 256), lin(256, 256)]), M([lin(512, 256), lin(512, 256, mul1=True)]),
+                M([lin(512, 256)] * 9)):
+        V.build_exl3_dense_group(bad)
+        assert bad._exl3_dense_group is None
+    single = M([lin(512, 256)])
+    V.build_exl3_dense_group(single)
+    assert single._exl3_dense_group is None
+    assert V.dense_group_stats()["fallbacks"]
+
+
 def test_dequant_argument_errors_without_device():
     lib = _lib.load()
     p = ctypes.c_void_p(16)
