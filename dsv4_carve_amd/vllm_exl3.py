@@ -35,6 +35,7 @@ from __future__ import annotations
 
 import logging
 import os
+import re
 from typing import Any
 
 import torch
@@ -705,6 +706,97 @@ def _suffix_from_mapped_name(weight_name: str) -> str:
     raise ValueError(f"not an EXL3 packed name: {weight_name}")
 
 
+# ---------------------------------------------------------------- quantization config
+
+SUPPORTED_BITS = (2, 3, 4, 5, 6)
+_LAYER_RE = re.compile(r"(?:^|\.)layers\.(\d+)(?:\.|$)")
+
+
+def _prefix_has_suffix(prefix: str, suffix: str) -> bool:
+    return prefix == suffix or prefix.endswith("." + suffix)
+
+
+class Exl3Config:
+    """The pack's ``quantization_config`` for this path
+    (recipe-lna/vllm_exl3_exl3.py.lna:1795-1960): routed experts at ``bits``
+    with an optional per-layer ``layer_bits`` override (a mixed-K pack), and
+    the optional ``non_routed_exl3`` block that names which dense linears are
+    EXL3 and at which K.  Same validation and error text classes."""
+
+    def __init__(self, bits: int = 4, codebook: str = "mcg", scope: str = "glm53_routed_experts_only",
+                 **kwargs: Any) -> None:
+        self.bits = int(bits)
+        self.codebook = str(codebook)
+        self.scope = str(scope)
+        raw = kwargs.pop("layer_bits", None) or {}
+        self.layer_bits: dict[int, int] = {int(k): int(v) for k, v in dict(raw).items()}
+        for idx, k in self.layer_bits.items():
+            if k not in SUPPORTED_BITS:
+                raise ValueError(f"unsupported EXL3 bits={k} for layer {idx}")
+        self.non_routed_exl3: dict[str, Any] = dict(kwargs.pop("non_routed_exl3", None) or {})
+        nr = self.non_routed_exl3
+        if nr.get("bits") is not None and nr["bits"] not in SUPPORTED_BITS:
+            raise ValueError(f"unsupported non_routed_exl3 bits={nr['bits']}")
+        for suffix, k in (nr.get("layer_bits") or {}).items():
+            if k not in SUPPORTED_BITS:
+                raise ValueError(f"unsupported non_routed_exl3 bits={k} for suffix {suffix}")
+        for prefix, cfg in (nr.get("layers") or {}).items():
+            if not isinstance(cfg, dict):
+                raise ValueError(f"non_routed_exl3 layers[{prefix}] must be a dict, got {type(cfg)}")
+            if cfg.get("bits") is not None and cfg["bits"] not in SUPPORTED_BITS:
+                raise ValueError(f"unsupported non_routed_exl3 layers[{prefix}] bits={cfg['bits']}")
+        if nr.get("codebook", "mcg") not in ("mcg", "mul1"):
+            raise ValueError(f"unsupported non_routed_exl3 codebook={nr.get('codebook')!r}; must be 'mcg' or 'mul1'")
+        self.extra = kwargs
+        if self.codebook not in ("mcg", "mul1"):
+            raise ValueError(f"unsupported codebook={self.codebook!r}; must be 'mcg' or 'mul1'")
+        if self.bits not in SUPPORTED_BITS:
+            raise ValueError(f"unsupported EXL3 bits={self.bits}")
+
+    @classmethod
+    def from_config(cls, config: dict[str, Any]) -> "Exl3Config":
+        skip = {"bits", "codebook", "scope", "quant_method", "tensor_storage", "non_routed_exl3",
+                "non_routed_quantization", "mtp_experts", "mtp_experts_start_layer"}
+        return cls(bits=int(config.get("bits", 4)), codebook=str(config.get("codebook", "mcg")),
+                   scope=str(config.get("scope", "glm53_routed_experts_only")),
+                   non_routed_exl3=config.get("non_routed_exl3"),
+                   **{k: v for k, v in config.items() if k not in skip})
+
+    def get_name(self) -> str:
+        return "exl3"
+
+    def bits_for_prefix(self, prefix: str) -> int:
+        """Routed-expert K of the layer named in `prefix`: its layer_bits entry, else bits."""
+        if not self.layer_bits:
+            return self.bits
+        m = _LAYER_RE.search(prefix or "")
+        return self.bits if m is None else self.layer_bits.get(int(m.group(1)), self.bits)
+
+    def _matches_non_routed_exl3(self, prefix: str) -> bool:
+        nr = self.non_routed_exl3
+        if not nr:
+            return False
+        if prefix in (nr.get("layers") or {}):
+            return True
+        return any(_prefix_has_suffix(prefix, m) for m in (nr.get("modules") or []))
+
+    def _bits_for_non_routed(self, prefix: str) -> int:
+        nr = self.non_routed_exl3
+        if not nr:
+            return self.bits
+        layers = nr.get("layers") or {}
+        if prefix in layers:
+            return int(layers[prefix].get("bits", nr.get("bits", self.bits)))
+        matched = next((s for s in (nr.get("modules") or []) if _prefix_has_suffix(prefix, s)), None)
+        if matched is None:
+            return self.bits
+        return int((nr.get("layer_bits") or {}).get(matched, nr.get("bits", self.bits)))
+
+    def _bf16_shards_for(self, prefix: str) -> list[int]:
+        layers = (self.non_routed_exl3 or {}).get("layers") or {}
+        return list(layers[prefix].get("bf16_shards", [])) if prefix in layers else []
+
+
 # ---------------------------------------------------------------- vLLM quant methods
 
 
@@ -798,17 +890,27 @@ class Exl3LinearMethod:
     """EXL3 dense linear with one or more same-input output shards
     (recipe-lna/vllm_exl3_exl3.py.lna:2310-2853, EXL3 shards only)."""
 
-    def __init__(self, quant_config=None, bits: int | None = None):
+    def __init__(self, quant_config=None, bits: int | None = None, tp_rank: int = 0, tp_size: int = 1):
         self.quant_config = quant_config
         self.bits = int(bits) if bits is not None else int(getattr(quant_config, "bits", 0))
+        self.tp_rank, self.tp_size = tp_rank, tp_size
 
     def create_weights(self, layer, input_size_per_partition: int, output_partition_sizes: list[int],
-                       input_size: int = 0, output_size: int = 0, params_dtype=None, **extra_weight_attrs):
+                       input_size: int = 0, output_size: int = 0, params_dtype=None, *,
+                       is_row_parallel: bool = False, **extra_weight_attrs):
+        """Fused parameters over the module's same-input output shards
+        (recipe-lna/vllm_exl3_exl3.py.lna:2323-2493).  vLLM tells row from
+        column parallelism by the layer class; here the caller says which.
+        Every parameter gets a weight_loader bound to its tensor kind."""
         del input_size, output_size, params_dtype, extra_weight_attrs
         k = input_size_per_partition
         for i, n in enumerate(output_partition_sizes):
             if k % 16 or n % 16:
                 raise ValueError(f"EXL3 trellis tiles are 16-wide; shard {i}: in={k} out={n}")
+        bf16 = self.quant_config._bf16_shards_for(getattr(layer, "prefix", "")) \
+            if hasattr(self.quant_config, "_bf16_shards_for") else []
+        if bf16:
+            raise NotImplementedError(f"EXL3 bf16 shards {bf16} are not part of this build's linear path")
         n_shards = len(output_partition_sizes)
         total_tiles = sum(n // 16 for n in output_partition_sizes)
         params = {
@@ -819,11 +921,61 @@ class Exl3LinearMethod:
             "mul1": torch.zeros(n_shards, 1, dtype=torch.int32),
         }
         for name, t in params.items():
-            layer.register_parameter(name, Parameter(t, requires_grad=False))
+            p = Parameter(t, requires_grad=False)
+            p.weight_loader = self._make_weight_loader(name, n_shards, list(output_partition_sizes),
+                                                       is_row_parallel)
+            layer.register_parameter(name, p)
         layer._exl3_linear_n_shards = n_shards
         layer._exl3_linear_output_partition_sizes = list(output_partition_sizes)
         layer._exl3_linear_input_size_per_partition = k
+        layer._exl3_linear_is_row_parallel = bool(is_row_parallel)
         layer._exl3_linear_bf16_shards = []
+        layer._exl3_linear_tp_size = self.tp_size
+        layer._exl3_linear_tp_rank = self.tp_rank
+
+    def _make_weight_loader(self, suffix: str, n_shards: int, sizes: list[int], is_row_parallel: bool):
+        """weight_loader(param, loaded_weight[, shard_id]) for one tensor kind
+        (recipe-lna/vllm_exl3_exl3.py.lna:2495-2633): shard ids "q"/"k"/"v" or
+        an int name the fused output shard; trellis/suh/svh are TP-narrowed
+        (row: trellis dim 0 + suh, column: trellis dim 1 + svh) and copied into
+        the shard's slice; mcg/mul1 store the marker value."""
+        tp_rank, tp_size = self.tp_rank, self.tp_size
+
+        def weight_loader(param: Parameter, loaded_weight: torch.Tensor, loaded_shard_id=None) -> None:
+            shard_idx = 0
+            if isinstance(loaded_shard_id, str):
+                shard_map = {"q": 0, "k": 1, "v": 2}
+                if loaded_shard_id not in shard_map:
+                    raise ValueError(f"unknown shard_id={loaded_shard_id} for EXL3 linear")
+                shard_idx = shard_map[loaded_shard_id]
+            elif isinstance(loaded_shard_id, int):
+                shard_idx = loaded_shard_id
+            if shard_idx >= n_shards:
+                raise ValueError(f"shard_idx={shard_idx} out of range for n_shards={n_shards}")
+            if suffix in ("mcg", "mul1"):
+                dest = param.data[shard_idx]
+                if tuple(dest.shape) != (1,):
+                    raise RuntimeError(f"EXL3 {suffix} marker shape mismatch: expected (1,) got {tuple(dest.shape)}")
+                dest[0] = int(loaded_weight.detach().item()) if loaded_weight.numel() > 0 else 0
+                return
+            loaded = loaded_weight.detach().contiguous()
+            sharded = (shard_exl3_row if is_row_parallel else shard_exl3_col)(loaded, suffix, tp_rank, tp_size)
+            if suffix == "trellis":
+                t0 = sum(s // 16 for s in sizes[:shard_idx])
+                dest = param.data[:, t0:t0 + sizes[shard_idx] // 16, :]
+            elif suffix == "suh":
+                dest = param.data[shard_idx]
+            elif suffix == "svh":
+                o0 = sum(sizes[:shard_idx])
+                dest = param.data[o0:o0 + sizes[shard_idx]]
+            else:
+                raise ValueError(f"unknown EXL3 suffix={suffix}")
+            if tuple(dest.shape) != tuple(sharded.shape):
+                raise RuntimeError(f"EXL3 linear load shape mismatch shard={shard_idx} suffix={suffix}: "
+                                   f"dest {tuple(dest.shape)} != loaded {tuple(sharded.shape)}")
+            dest.copy_(sharded)
+
+        return weight_loader
 
     def process_weights_after_loading(self, layer) -> None:
         sizes = layer._exl3_linear_output_partition_sizes
