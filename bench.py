@@ -111,6 +111,64 @@ def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, 
     return start.elapsed_time(end) * 1000.0 / steps, nbytes
 
 
+def time_glue(layer, dev, rows, topk, steps=40, seed=77):
+    """us per layer from the router's tensors (int64 global ids, bf16 weights)
+    under graph replay, three ways: the kernel alone on ready int32 local ids
+    and fp32 weights; the plugin's host-side glue (map_topk_to_local and the
+    casts, each its own launch) before it; and the glue folded into the
+    kernels (the routed entry point).  With and without an expert map (here
+    the identity map over every expert, so the routed work is the same)."""
+    import torch
+    from dsv4_carve_amd import ops, synth
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    n_exp = len(layer.bits)
+    pool = [synth.routing(rows, n_exp, topk, seed=seed * 1000 + i) for i in range(POOL)]
+    ids64 = torch.tensor(np.stack([p[0] for p in pool]), dtype=torch.int64, device=dev)
+    w16 = torch.tensor(np.stack([p[1] for p in pool]), dtype=torch.float32, device=dev).to(torch.bfloat16)
+    ids32 = ids64.to(torch.int32)
+    w32 = w16.float()
+    emap = torch.arange(n_exp, dtype=torch.int64, device=dev)
+    x = torch.from_numpy(synth.activations(rows, layer.hidden, seed=seed)).to(dev)
+    out = torch.empty((rows, layer.hidden), dtype=torch.float32, device=dev)
+    kw = dict(intermediate=layer.inter, expert_bits=layer.ebits, bits_mask=layer.mask,
+              scratch=ops.moe_scratch(dev, layer.hidden, layer.inter, topk))
+
+    def kernel(i, m):
+        ops.moe_decode(x, out, layer.tables, ids32[i % POOL], w32[i % POOL], **kw)
+
+    def host(i, m):
+        local = V.map_topk_to_local(ids64[i % POOL], n_exp, m).reshape(rows, topk)
+        ops.moe_decode(x, out, layer.tables, local.to(torch.int32).contiguous(),
+                       w16[i % POOL].reshape(local.shape).to(torch.float32).contiguous(), **kw)
+
+    def device(i, m):
+        ops.moe_decode(x, out, layer.tables, ids64[i % POOL], w16[i % POOL], expert_map=m, **kw)
+
+    def timed(fn, m):
+        for i in range(3):
+            fn(i, m)
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                fn(i, m)
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return round(start.elapsed_time(end) * 1000.0 / steps, 2)
+
+    res = {"kernel_only_us": timed(kernel, None)}
+    for name, m in (("no_map", None), ("expert_map", emap)):
+        res[name] = {"host_glue_us": timed(host, m), "device_glue_us": timed(device, m)}
+    return res
+
+
 DENSE_SHAPES = ((4096, 4096), (4096, 1536), (1536, 4096), (4096, 12288))
 DENSE_BITS = (2, 3, 4, 6)
 DENSE_ROWS = (1, 2, 4, 8, 16)
@@ -413,7 +471,7 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
     }
 
 
-EXTRA_LEGS = ("sweep", "tp8", "prefill", "stack", "dense", "fan")
+EXTRA_LEGS = ("sweep", "tp8", "prefill", "stack", "dense", "fan", "glue")
 
 
 def main() -> int:
@@ -518,6 +576,13 @@ def main() -> int:
             fans[name] = time_fan(dev, k, ns, b, DENSE_ROWS)
             print(f"[bench] fan {name}: {fans[name]}", file=sys.stderr, flush=True)
         extra["dense_fan_cold"] = fans
+
+    if "glue" in legs:
+        glue = {}
+        for m in (1, 4, 16):
+            glue[str(m)] = time_glue(layer, dev, m, TOPK)
+            print(f"[bench] routing glue m={m}: {glue[str(m)]}", file=sys.stderr, flush=True)
+        extra["routing_glue_graph_replay"] = glue
 
     cpu = None
     if not a.no_cpu:

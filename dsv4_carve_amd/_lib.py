@@ -23,9 +23,11 @@ EXPORTS = (
     "exl3_moe_scratch_bytes",
     "exl3_moe_max_rows",
     "exl3_moe_decode",
+    "exl3_moe_decode_routed",
     "exl3_moe_info",
     "exl3_moe_prefill_scratch_bytes",
     "exl3_moe_prefill",
+    "exl3_moe_prefill_routed",
 )
 
 _lock = threading.Lock()
@@ -48,11 +50,19 @@ _SIGS = {
     "exl3_moe_decode": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,
                          _P, _P, _P, _P, _P, _P, _P, _P, _P,
                          _P, _P, _P, _I, _I, _I, _F, _P, _L, _P], _I),
+    "exl3_moe_decode_routed": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,
+                                _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                _P, _I, _P, _I, _P, _L,
+                                _P, _I, _I, _I, _F, _P, _L, _P], _I),
     "exl3_moe_info": ([ctypes.POINTER(ctypes.c_int64), _I], _I),
     "exl3_moe_prefill_scratch_bytes": ([_L, _L, _L, _L, _L], _L),
     "exl3_moe_prefill": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,
                           _P, _P, _P, _P, _P, _P, _P, _P, _P,
                           _P, _P, _P, _I, _I, _I, _F, _P, _L, _P], _I),
+    "exl3_moe_prefill_routed": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,
+                                 _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                 _P, _I, _P, _I, _P, _L,
+                                 _P, _I, _I, _I, _F, _P, _L, _P], _I),
 }
 
 

@@ -40,6 +40,7 @@
 #pragma once
 
 #include "exl3_gemv.hpp"
+#include "exl3_route.hpp"
 #include "exl3_capi_util.hpp"
 
 namespace exl3 {
@@ -130,7 +131,7 @@ struct Params {
     const int64_t* gt; const int64_t* gsu; const int64_t* gsv;
     const int64_t* ut; const int64_t* usu; const int64_t* usv;
     const int64_t* dt; const int64_t* dsu; const int64_t* dsv;
-    const int32_t* ids; const float* w;
+    Route rt;            // top-k ids / weights / expert map
     const int8_t* ebits; int bits;
     float limit;
     char* scratch;
@@ -206,8 +207,8 @@ __device__ inline void build_plan(const Params& P, Plan& pl, char* tmp) {
     __syncthreads();
     const int slots = P.m * P.topk;
     for (int s = lane; s < slots; s += WAVE) {
-        const int id = P.ids[s];
-        if (id >= 0 && id < P.E) atomicOr(&rowmask[id], 1u << (s / P.topk));
+        const int id = P.rt.local(s, P.E);
+        if (id >= 0) atomicOr(&rowmask[id], 1u << (s / P.topk));
     }
     __syncthreads();
     const int chunk = (P.E + WAVE - 1) / WAVE;
@@ -240,9 +241,9 @@ __device__ inline void build_plan(const Params& P, Plan& pl, char* tmp) {
     if (lane == WAVE - 1) pl.U = sg;
     __syncthreads();
     for (int s = lane; s < slots; s += WAVE) {
-        const int id = P.ids[s];
+        const int id = P.rt.local(s, P.E);
         int16_t pr = -1;
-        if (id >= 0 && id < P.E) {
+        if (id >= 0) {
             const int row = s / P.topk;
             pr = (int16_t)(epair[id] + __popc(rowmask[id] & ((1u << row) - 1u)));
         }
@@ -586,7 +587,7 @@ __device__ void item_g(const Params& P, const Plan& pl, int t, int epoch, Tracer
 #pragma unroll
     for (int j = 0; j < MAX_TOPK; ++j) {       // every slot's load issued first
         pr[j] = j < P.topk ? pl.slotpair[row * P.topk + j] : -1;
-        wt[j] = pr[j] >= 0 ? P.w[row * P.topk + j] : 0.f;
+        wt[j] = pr[j] >= 0 ? P.rt.weight(row * P.topk + j) : 0.f;
         if (pr[j] >= 0) d[j] = ld_dev4_buf(dc, (uint32_t)col * 4u, (uint32_t)pr[j] * (uint32_t)P.H * 4u);
     }
     float s4[4] = {0.f, 0.f, 0.f, 0.f};
@@ -808,7 +809,7 @@ __global__ __launch_bounds__(MAX_TOPK * WAVE) void moe_phase_finish(Params P) {
     const int pair = pl->slotpair[row * P.topk + j];
     if (pair >= 0) {
         uint16_t dsv[4];
-        load_half4(dsv, P.dsv[P.ids[row * P.topk + j]], col);
+        load_half4(dsv, P.dsv[P.rt.local(row * P.topk + j, P.E)], col);
         slot_val[j][lane] = down_value<CPOL_PLAIN>(P, pair, dsv, col);
     }
     __syncthreads();
@@ -816,7 +817,7 @@ __global__ __launch_bounds__(MAX_TOPK * WAVE) void moe_phase_finish(Params P) {
     float s4[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < P.topk; ++k) {      // fp32 sum in top-k slot order
         if (pl->slotpair[row * P.topk + k] < 0) continue;
-        const float w = P.w[row * P.topk + k];
+        const float w = P.rt.weight(row * P.topk + k);
         const float4_t o = slot_val[k][lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) s4[i] = s4[i] + w * o[i];

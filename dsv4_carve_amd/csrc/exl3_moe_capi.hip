@@ -98,16 +98,17 @@ int exl3_moe_info(int64_t* out, int n) {
     return k;
 }
 
-int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
-                    int64_t intermediate, int64_t n_experts, int64_t topk,
-                    const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
-                    const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
-                    const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
-                    const int32_t* expert_ids, const float* routing_weights,
-                    const int8_t* expert_bits, int bits, int bits_mask, int codebook,
-                    float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
-    clear_error();
-    if (!x || !out || !expert_ids || !routing_weights || !scratch) return fail("null pointer");
+}  // extern "C"
+
+// The decode layer for one routing descriptor; both entry points below.
+static int moe_decode_impl(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                           int64_t intermediate, int64_t n_experts, int64_t topk,
+                           const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                           const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                           const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                           const Route& rt, const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                           float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    if (!x || !out || !rt.ids || !rt.w || !scratch) return fail("null pointer");
     if (!gate_trellis || !gate_suh || !gate_svh || !up_trellis || !up_suh || !up_svh || !down_trellis ||
         !down_suh || !down_svh)
         return fail("null pointer table");
@@ -155,7 +156,7 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
     P.gt = gate_trellis; P.gsu = gate_suh; P.gsv = gate_svh;
     P.ut = up_trellis; P.usu = up_suh; P.usv = up_svh;
     P.dt = down_trellis; P.dsu = down_suh; P.dsv = down_svh;
-    P.ids = expert_ids; P.w = routing_weights;
+    P.rt = rt;
     P.ebits = expert_bits; P.bits = bits;
     P.limit = swiglu_limit;
     P.scratch = reinterpret_cast<char*>(scratch);
@@ -174,6 +175,40 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
     const int nxcd = (cus >= 64 && cus % 32 == 0) ? cus / 32 : 1;
     P.nclass = nxcd <= MAX_CLASSES ? nxcd : MAX_CLASSES;
     return kInstances[idx].launch(P, waves, lds_kb, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" {
+
+int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                    int64_t intermediate, int64_t n_experts, int64_t topk,
+                    const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                    const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                    const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                    const int32_t* expert_ids, const float* routing_weights,
+                    const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                    float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    clear_error();
+    const Route rt{expert_ids, routing_weights, nullptr, IDS_I32, OUT_F32, 0};
+    return moe_decode_impl(x, x_kind, out, out_kind, m, hidden, intermediate, n_experts, topk, gate_trellis,
+                           gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh, rt,
+                           expert_bits, bits, bits_mask, codebook, swiglu_limit, scratch, scratch_bytes, stream);
+}
+
+int exl3_moe_decode_routed(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                           int64_t intermediate, int64_t n_experts, int64_t topk,
+                           const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                           const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                           const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                           const void* topk_ids, int ids_kind, const void* topk_weights, int weights_kind,
+                           const int64_t* expert_map, int64_t n_global,
+                           const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                           float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    clear_error();
+    Route rt;
+    if (int rc = make_route(topk_ids, ids_kind, topk_weights, weights_kind, expert_map, n_global, rt)) return rc;
+    return moe_decode_impl(x, x_kind, out, out_kind, m, hidden, intermediate, n_experts, topk, gate_trellis,
+                           gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh, rt,
+                           expert_bits, bits, bits_mask, codebook, swiglu_limit, scratch, scratch_bytes, stream);
 }
 
 }  // extern "C"

@@ -23,6 +23,7 @@
 #pragma once
 
 #include "exl3_gemv.hpp"
+#include "exl3_route.hpp"
 #include "exl3_capi_util.hpp"
 
 namespace exl3 {
@@ -81,7 +82,7 @@ struct PfParams {
     const int64_t* gt; const int64_t* gsu; const int64_t* gsv;
     const int64_t* ut; const int64_t* usu; const int64_t* usv;
     const int64_t* dt; const int64_t* dsu; const int64_t* dsv;
-    const int32_t* ids; const float* w;
+    Route rt;                            // top-k ids / weights / expert map
     const int8_t* ebits; int bits;
     float limit;
     char* scratch;

@@ -42,8 +42,8 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     for (int e = tid; e < P.E; e += nt) cnt[e] = 0;
     __syncthreads();
     for (int s = tid; s < P.P; s += nt) {
-        const int e = P.ids[s];
-        if (e >= 0 && e < P.E) atomicAdd(&cnt[e], 1);
+        const int e = P.rt.local(s, P.E);
+        if (e >= 0) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
     for (int e = tid; e < P.E; e += nt) {
@@ -83,9 +83,9 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     int* pair_slot = pat<int>(P.scratch, L.pair_slot);
     int* pos = pat<int>(P.scratch, L.pos);
     for (int s = tid; s < P.P; s += nt) {
-        const int e = P.ids[s];
+        const int e = P.rt.local(s, P.E);
         int p = -1;
-        if (e >= 0 && e < P.E) {
+        if (e >= 0) {
             p = atomicAdd(&cnt[e], 1);
             pair_slot[p] = s;
         }
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     if (p >= pat<int>(P.scratch, L.meta)[0]) return;
     const int lane = threadIdx.x;
     const int s = pat<int>(P.scratch, L.pair_slot)[p];
-    const int tok = s / P.topk, e = P.ids[s];
+    const int tok = s / P.topk, e = P.rt.local(s, P.E);
     const uint16_t* suh = reinterpret_cast<const uint16_t*>((proj ? P.usu : P.gsu)[e]);
     const uint32_t* xr = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (size_t)tok * P.H);
     uint32_t* dst = reinterpret_cast<uint32_t*>(pat<uint16_t>(P.scratch, L.Xh) + ((size_t)proj * P.P + p) * P.H);
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(64) void pf_act_kernel(PfParams P) {
     const int p = blockIdx.x;
     if (p >= pat<int>(P.scratch, L.meta)[0]) return;
     const int lane = threadIdx.x;
-    const int e = P.ids[pat<int>(P.scratch, L.pair_slot)[p]];
+    const int e = P.rt.local(pat<int>(P.scratch, L.pair_slot)[p], P.E);
     const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I;
     const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I;
     const size_t kstride = (size_t)2 * P.P * P.I;     // between k-parts
@@ -172,7 +172,7 @@ __global__ __launch_bounds__(64) void pf_gather_kernel(PfParams P) {
     for (int j = 0; j < P.topk; ++j) {
         const int p = pos[tok * P.topk + j];
         if (p < 0) continue;
-        const float wt = P.w[tok * P.topk + j];
+        const float wt = P.rt.weight(tok * P.topk + j);
         float4_t d = *reinterpret_cast<const float4_t*>(D + (size_t)p * P.H + col);
         for (int ks = 1; ks < L.ks_down; ++ks)      // k-parts added in order
             d += *reinterpret_cast<const float4_t*>(D + ((size_t)ks * P.P + p) * P.H + col);
@@ -225,16 +225,17 @@ int64_t exl3_moe_prefill_scratch_bytes(int64_t tokens, int64_t hidden, int64_t i
     return pf_layout(tokens * topk, hidden, intermediate, n_experts).total;
 }
 
-int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t tokens, int64_t hidden,
-                     int64_t intermediate, int64_t n_experts, int64_t topk,
-                     const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
-                     const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
-                     const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
-                     const int32_t* expert_ids, const float* routing_weights,
-                     const int8_t* expert_bits, int bits, int bits_mask, int codebook,
-                     float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
-    clear_error();
-    if (!x || !out || !expert_ids || !routing_weights || !scratch) return fail("null pointer");
+}  // extern "C"
+
+// The prefill layer for one routing descriptor; both entry points below.
+static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, int64_t tokens, int64_t hidden,
+                            int64_t intermediate, int64_t n_experts, int64_t topk,
+                            const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                            const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                            const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                            const Route& rt, const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                            float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    if (!x || !out || !rt.ids || !rt.w || !scratch) return fail("null pointer");
     if (!gate_trellis || !gate_suh || !gate_svh || !up_trellis || !up_suh || !up_svh || !down_trellis ||
         !down_suh || !down_svh)
         return fail("null pointer table");
@@ -261,7 +262,7 @@ int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t
     P.gt = gate_trellis; P.gsu = gate_suh; P.gsv = gate_svh;
     P.ut = up_trellis; P.usu = up_suh; P.usv = up_svh;
     P.dt = down_trellis; P.dsu = down_suh; P.dsv = down_svh;
-    P.ids = expert_ids; P.w = routing_weights;
+    P.rt = rt;
     P.ebits = expert_bits; P.bits = bits;
     P.limit = swiglu_limit;
     P.scratch = reinterpret_cast<char*>(scratch);
@@ -280,6 +281,40 @@ int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t
     if ((rc = launch_widths(P, mask, codebook, true, (int)(tiles * (hidden / COLS) * P.L.ks_down), s))) return rc;
     hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)(tokens * (hidden / COLS))), dim3(WAVE), 0, s, P);
     return check_launch();
+}
+
+extern "C" {
+
+int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t tokens, int64_t hidden,
+                     int64_t intermediate, int64_t n_experts, int64_t topk,
+                     const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                     const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                     const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                     const int32_t* expert_ids, const float* routing_weights,
+                     const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                     float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    clear_error();
+    const Route rt{expert_ids, routing_weights, nullptr, IDS_I32, OUT_F32, 0};
+    return moe_prefill_impl(x, x_kind, out, out_kind, tokens, hidden, intermediate, n_experts, topk, gate_trellis,
+                            gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh, rt,
+                            expert_bits, bits, bits_mask, codebook, swiglu_limit, scratch, scratch_bytes, stream);
+}
+
+int exl3_moe_prefill_routed(const void* x, int x_kind, void* out, int out_kind, int64_t tokens, int64_t hidden,
+                            int64_t intermediate, int64_t n_experts, int64_t topk,
+                            const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                            const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                            const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                            const void* topk_ids, int ids_kind, const void* topk_weights, int weights_kind,
+                            const int64_t* expert_map, int64_t n_global,
+                            const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                            float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream) {
+    clear_error();
+    Route rt;
+    if (int rc = make_route(topk_ids, ids_kind, topk_weights, weights_kind, expert_map, n_global, rt)) return rc;
+    return moe_prefill_impl(x, x_kind, out, out_kind, tokens, hidden, intermediate, n_experts, topk, gate_trellis,
+                            gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh, rt,
+                            expert_bits, bits, bits_mask, codebook, swiglu_limit, scratch, scratch_bytes, stream);
 }
 
 }  // extern "C"

@@ -26,6 +26,7 @@ from . import _lib
 CB_3INST, CB_MCG, CB_MUL1 = 0, 1, 2
 OUT_KIND = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
 X_KIND = {torch.float16: 0, torch.bfloat16: 1}
+IDS_KIND = {torch.int32: 0, torch.int64: 1}
 
 
 def codebook_id(mcg: bool, mul1: bool) -> int:
@@ -90,9 +91,9 @@ _LIB.define("gemm(Tensor a, Tensor b, Tensor(a!) c, Tensor suh, Tensor svh, int 
             "Tensor(b!) scratch) -> ()")
 _LIB.define("moe_decode(Tensor x, Tensor(a!) out, Tensor gate_trellis, Tensor gate_suh, Tensor gate_svh, "
             "Tensor up_trellis, Tensor up_suh, Tensor up_svh, Tensor down_trellis, Tensor down_suh, "
-            "Tensor down_svh, Tensor expert_ids, Tensor routing_weights, Tensor? expert_bits, int bits, "
-            "int bits_mask, int codebook, float swiglu_limit, int hidden, int intermediate, "
-            "Tensor(b!) scratch) -> ()")
+            "Tensor down_svh, Tensor expert_ids, Tensor routing_weights, Tensor? expert_map, "
+            "Tensor? expert_bits, int bits, int bits_mask, int codebook, float swiglu_limit, int hidden, "
+            "int intermediate, Tensor(b!) scratch) -> ()")
 
 
 def _dequant_impl(trellis, suh, svh, bits, codebook, out):
@@ -112,33 +113,38 @@ def _gemm_impl(a, b, c, suh, svh, codebook, scratch):
                            _ptr(c), OUT_KIND[c.dtype], _ptr(scratch), scratch.numel(), _stream(a.device)))
 
 
-def _moe_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, expert_bits, bits, bits_mask,
+def _route_args(ids, w, emap):
+    return (_ptr(ids), IDS_KIND[ids.dtype], _ptr(w), OUT_KIND[w.dtype], _ptr(emap),
+            0 if emap is None else emap.numel())
+
+
+def _moe_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, emap, expert_bits, bits, bits_mask,
               codebook, limit, hidden, intermediate, scratch):
     L = _lib.load()
     m = x.shape[0]
-    _lib.check(L.exl3_moe_decode(
+    _lib.check(L.exl3_moe_decode_routed(
         _ptr(x), X_KIND[x.dtype], _ptr(out), OUT_KIND[out.dtype], m, int(hidden), int(intermediate),
         gt.numel(), ids.shape[1],
         _ptr(gt), _ptr(gsu), _ptr(gsv), _ptr(ut), _ptr(usu), _ptr(usv), _ptr(dt), _ptr(dsu), _ptr(dsv),
-        _ptr(ids), _ptr(w), _ptr(expert_bits), int(bits), int(bits_mask), int(codebook), float(limit),
+        *_route_args(ids, w, emap), _ptr(expert_bits), int(bits), int(bits_mask), int(codebook), float(limit),
         _ptr(scratch), scratch.numel(), _stream(x.device)))
 
 
 _LIB.define("moe_prefill(Tensor x, Tensor(a!) out, Tensor gate_trellis, Tensor gate_suh, Tensor gate_svh, "
             "Tensor up_trellis, Tensor up_suh, Tensor up_svh, Tensor down_trellis, Tensor down_suh, "
-            "Tensor down_svh, Tensor expert_ids, Tensor routing_weights, Tensor? expert_bits, int bits, "
-            "int bits_mask, int codebook, float swiglu_limit, int hidden, int intermediate, "
-            "Tensor(b!) scratch) -> ()")
+            "Tensor down_svh, Tensor expert_ids, Tensor routing_weights, Tensor? expert_map, "
+            "Tensor? expert_bits, int bits, int bits_mask, int codebook, float swiglu_limit, int hidden, "
+            "int intermediate, Tensor(b!) scratch) -> ()")
 
 
-def _prefill_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, expert_bits, bits, bits_mask,
+def _prefill_impl(x, out, gt, gsu, gsv, ut, usu, usv, dt, dsu, dsv, ids, w, emap, expert_bits, bits, bits_mask,
                   codebook, limit, hidden, intermediate, scratch):
     L = _lib.load()
-    _lib.check(L.exl3_moe_prefill(
+    _lib.check(L.exl3_moe_prefill_routed(
         _ptr(x), X_KIND[x.dtype], _ptr(out), OUT_KIND[out.dtype], x.shape[0], int(hidden), int(intermediate),
         gt.numel(), ids.shape[1],
         _ptr(gt), _ptr(gsu), _ptr(gsv), _ptr(ut), _ptr(usu), _ptr(usv), _ptr(dt), _ptr(dsu), _ptr(dsv),
-        _ptr(ids), _ptr(w), _ptr(expert_bits), int(bits), int(bits_mask), int(codebook), float(limit),
+        *_route_args(ids, w, emap), _ptr(expert_bits), int(bits), int(bits_mask), int(codebook), float(limit),
         _ptr(scratch), scratch.numel(), _stream(x.device)))
 
 
@@ -362,16 +368,33 @@ def bits_mask_of(bits) -> int:
     return sum(1 << int(b) for b in set(int(b) for b in bits))
 
 
+def _check_route(expert_ids, routing_weights, rows: int, device, expert_map, what: str) -> None:
+    _check(expert_ids.is_cuda and expert_ids.device == device and expert_ids.dtype in IDS_KIND and
+           expert_ids.is_contiguous() and expert_ids.dim() == 2 and expert_ids.shape[0] == rows,
+           f"expert_ids must be contiguous int32/int64 [{what}, topk] on the input device")
+    _check(routing_weights.is_cuda and routing_weights.device == device and routing_weights.dtype in OUT_KIND and
+           routing_weights.is_contiguous() and routing_weights.shape == expert_ids.shape,
+           f"routing_weights must be contiguous fp16/bf16/fp32 [{what}, topk] on the input device")
+    if expert_map is not None:
+        _check(expert_map.is_cuda and expert_map.device == device and expert_map.dtype == torch.int64 and
+               expert_map.dim() == 1 and expert_map.is_contiguous() and expert_map.numel() >= 1,
+               "expert_map must be a contiguous int64 [global experts] tensor on the input device")
+
+
 def moe_decode(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Tensor,
                routing_weights: torch.Tensor, *, intermediate: int, bits: int | None = None,
                expert_bits: torch.Tensor | None = None, bits_mask: int | None = None,
                codebook: int = CB_MCG, swiglu_limit: float = 10.0,
-               scratch: torch.Tensor | None = None) -> torch.Tensor:
-    """One-launch routed-expert decode of x [m, hidden] into out [m, hidden].
+               scratch: torch.Tensor | None = None, expert_map: torch.Tensor | None = None) -> torch.Tensor:
+    """Routed-expert decode of x [m, hidden] into out [m, hidden].
 
     tables: the nine int64 device pointer tables (dict keyed by MOE_TABLE_KEYS,
     or a sequence in that order).  Either `bits` (every expert) or
-    `expert_bits` (int8 [E] device tensor) with `bits_mask` (set of widths)."""
+    `expert_bits` (int8 [E] device tensor) with `bits_mask` (set of widths).
+    expert_ids int32/int64 and routing_weights fp16/bf16/fp32, [m, topk], as
+    the router produced them; with `expert_map` (int64 [global experts],
+    negative for other ranks' experts) the ids are global and are mapped to
+    local ones inside the kernels, as map_topk_to_local does on the host."""
     if isinstance(tables, dict):
         tabs = [tables[k] for k in MOE_TABLE_KEYS]
     else:
@@ -384,11 +407,7 @@ def moe_decode(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Ten
     _check(out.is_cuda and out.device == x.device and tuple(out.shape) == tuple(x.shape) and out.is_contiguous(),
            "output must match x shape/device and be contiguous")
     _check(out.dtype in OUT_KIND, "output must be fp16/bf16/fp32")
-    _check(expert_ids.is_cuda and expert_ids.dtype == torch.int32 and expert_ids.is_contiguous() and
-           expert_ids.dim() == 2 and expert_ids.shape[0] == m, "expert_ids must be contiguous int32 [m, topk]")
-    _check(routing_weights.is_cuda and routing_weights.dtype == torch.float32 and
-           routing_weights.is_contiguous() and routing_weights.shape == expert_ids.shape,
-           "routing_weights must be contiguous fp32 [m, topk]")
+    _check_route(expert_ids, routing_weights, m, x.device, expert_map, "m")
     n_experts = tabs[0].numel()
     for t in tabs:
         _check(t.is_cuda and t.device == x.device and t.dtype == torch.int64 and t.is_contiguous() and
@@ -403,7 +422,7 @@ def moe_decode(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Ten
         b, mask = int(bits), 0
     if scratch is None:
         scratch = moe_scratch(x.device, hidden, intermediate, expert_ids.shape[1])
-    torch.ops.exl3_amd.moe_decode(x, out, *tabs, expert_ids, routing_weights, expert_bits, b, mask,
+    torch.ops.exl3_amd.moe_decode(x, out, *tabs, expert_ids, routing_weights, expert_map, expert_bits, b, mask,
                                   int(codebook), float(swiglu_limit), int(hidden), int(intermediate), scratch)
     return out
 
@@ -476,7 +495,7 @@ def moe_prefill(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Te
                 routing_weights: torch.Tensor, *, intermediate: int, bits: int | None = None,
                 expert_bits: torch.Tensor | None = None, bits_mask: int | None = None,
                 codebook: int = CB_MCG, swiglu_limit: float = 10.0,
-                scratch: torch.Tensor | None = None) -> torch.Tensor:
+                scratch: torch.Tensor | None = None, expert_map: torch.Tensor | None = None) -> torch.Tensor:
     """Routed-expert layer over many tokens (grouped GEMMs): x [tokens, hidden]
     -> out [tokens, hidden]; arguments as moe_decode, any number of tokens with
     tokens * topk <= 65536."""
@@ -487,11 +506,7 @@ def moe_prefill(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Te
     T, hidden = x.shape
     _check(out.is_cuda and out.device == x.device and tuple(out.shape) == (T, hidden) and out.is_contiguous()
            and out.dtype in OUT_KIND, "output must be contiguous fp16/bf16/fp32 [tokens, hidden] on x's device")
-    _check(expert_ids.is_cuda and expert_ids.dtype == torch.int32 and expert_ids.is_contiguous() and
-           expert_ids.dim() == 2 and expert_ids.shape[0] == T, "expert_ids must be contiguous int32 [tokens, topk]")
-    _check(routing_weights.is_cuda and routing_weights.dtype == torch.float32 and
-           routing_weights.is_contiguous() and routing_weights.shape == expert_ids.shape,
-           "routing_weights must be contiguous fp32 [tokens, topk]")
+    _check_route(expert_ids, routing_weights, T, x.device, expert_map, "tokens")
     n_experts = tabs[0].numel()
     for t in tabs:
         _check(t.is_cuda and t.device == x.device and t.dtype == torch.int64 and t.is_contiguous() and
@@ -506,6 +521,6 @@ def moe_prefill(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Te
         b, mask = int(bits), 0
     if scratch is None:
         scratch = moe_prefill_scratch(x.device, T, hidden, intermediate, expert_ids.shape[1], n_experts)
-    torch.ops.exl3_amd.moe_prefill(x, out, *tabs, expert_ids, routing_weights, expert_bits, b, mask,
+    torch.ops.exl3_amd.moe_prefill(x, out, *tabs, expert_ids, routing_weights, expert_map, expert_bits, b, mask,
                                    int(codebook), float(swiglu_limit), int(hidden), int(intermediate), scratch)
     return out

@@ -613,20 +613,26 @@ def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
     if _ptrs_stale(layer, inners):
         _lna2_log_reject("ptr tables are stale (weights re-bound after build_exl3_fused_state)", not_ready=True)
         return None
-    local = map_topk_to_local(ids, len(inners), expert_map).reshape(ids.shape)
-    safe_ids = local.to(torch.int32).contiguous()
-    route_w = weights.reshape(local.shape).to(torch.float32).contiguous()
+    # The router's ids (int32/int64), weights (fp16/bf16/fp32) and the pinned
+    # expert_map go to the kernels as they are: the global -> local mapping
+    # (map_topk_to_local's rule), the widening and the weight cast happen in
+    # the kernels' route planning, so no launches run before the layer.
+    route_ids = ids if ids.dtype in ops.IDS_KIND and ids.is_contiguous() else ids.to(torch.long).contiguous()
+    route_w = weights if weights.dtype in ops.OUT_KIND and weights.is_contiguous() else \
+        weights.to(torch.float32).contiguous()
     x_in = x2d if x2d.is_contiguous() else x2d.contiguous()
     out = torch.empty_like(x_in)
+    if expert_map is not None and expert_map.numel() == 0:
+        return out.zero_()                  # an empty map routes nothing here
     kw = dict(intermediate=inter, expert_bits=layer._exl3_bits_table, bits_mask=layer._exl3_bits_mask,
-              codebook=layer._exl3_codebook, swiglu_limit=float(limit))
+              codebook=layer._exl3_codebook, swiglu_limit=float(limit), expert_map=expert_map)
     if rows <= lna2_max_rows():
-        ops.moe_decode(x_in, out, ptrs, safe_ids, route_w, scratch=_lna2_scratch_for(layer, x2d.device), **kw)
+        ops.moe_decode(x_in, out, ptrs, route_ids, route_w, scratch=_lna2_scratch_for(layer, x2d.device), **kw)
         _MOE_CALLS["lna2"] += 1
     else:
         # many rows: the grouped-GEMM prefill path (the reference falls back to
         # exllamav3's fused exl3_moe here, vllm_exl3_exl3.py.lna:1597-1704)
-        ops.moe_prefill(x_in, out, ptrs, safe_ids, route_w, **kw)
+        ops.moe_prefill(x_in, out, ptrs, route_ids, route_w, **kw)
         _MOE_CALLS["prefill"] += 1
     return out
 
@@ -642,7 +648,9 @@ def apply_exl3_experts(x, topk_ids, topk_weights, layer, *, limit: float = SWIGL
         raise RuntimeError("EXL3 experts were not built after weight load")
     tokens, hidden = x.shape[-2], x.shape[-1]
     x2d = x.reshape(tokens, hidden)
-    ids = topk_ids.reshape(tokens, -1).to(torch.long)
+    ids = topk_ids.reshape(tokens, -1)
+    if ids.dtype not in (torch.int32, torch.int64):
+        ids = ids.to(torch.long)
     weights = topk_weights.reshape(tokens, -1)
     expert_map = pin_exl3_expert_map(layer, x2d.device)
     have_ptrs = bool(getattr(layer, "_exl3_ptrs", None))

@@ -116,6 +116,32 @@ int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t 
                     float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
 
 /*
+ * exl3_moe_decode over the top-k tensors as the serving layer holds them: the
+ * global-to-local expert mapping, id widening and weight cast that the plugin
+ * runs as separate launches before the kernel (map_topk_to_local,
+ * recipe-lna/vllm_exl3_exl3.py.lna:963-985, and the .to(int32)/.to(float32)
+ * copies of _apply_lna2_moe, :1234-1236) are done inside the kernels' route
+ * planning instead.  Results are bitwise those of exl3_moe_decode on the
+ * mapped int32 ids and fp32 weights.
+ *   topk_ids: [m][topk], ids_kind 0 = int32, 1 = int64.
+ *   topk_weights: [m][topk], weights_kind 0 = fp16, 1 = bf16, 2 = fp32.
+ *   expert_map: device int64 [n_global] (global id -> local id, negative for
+ *     experts of other ranks), or NULL when the ids are already local.  A slot
+ *     whose id is outside the map, or whose mapped id is outside
+ *     [0, n_experts), contributes nothing.
+ * Other arguments as exl3_moe_decode.
+ */
+int exl3_moe_decode_routed(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                           int64_t intermediate, int64_t n_experts, int64_t topk,
+                           const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                           const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                           const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                           const void* topk_ids, int ids_kind, const void* topk_weights, int weights_kind,
+                           const int64_t* expert_map, int64_t n_global,
+                           const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                           float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
+
+/*
  * Routed-MoE layer for many tokens (prefill), same mathematics as
  * exl3_moe_decode: tokens are routed by expert on the device and each expert's
  * weights are decoded once per 32 routed rows, feeding fp16 MFMA with fp32
@@ -138,6 +164,22 @@ int exl3_moe_prefill(const void* x, int x_kind, void* out, int out_kind, int64_t
                      const int32_t* expert_ids, const float* routing_weights,
                      const int8_t* expert_bits, int bits, int bits_mask, int codebook,
                      float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
+
+/*
+ * exl3_moe_prefill over the serving layer's top-k tensors and expert map, as
+ * exl3_moe_decode_routed is to exl3_moe_decode (replaces the plugin's
+ * map_topk_to_local and casts before the fused MoE,
+ * recipe-lna/vllm_exl3_exl3.py.lna:1616-1620).
+ */
+int exl3_moe_prefill_routed(const void* x, int x_kind, void* out, int out_kind, int64_t tokens, int64_t hidden,
+                            int64_t intermediate, int64_t n_experts, int64_t topk,
+                            const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                            const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                            const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                            const void* topk_ids, int ids_kind, const void* topk_weights, int weights_kind,
+                            const int64_t* expert_map, int64_t n_global,
+                            const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                            float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
 
 /*
  * Launch geometry for diagnostics (replaces lna2_moe_info,

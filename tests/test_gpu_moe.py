@@ -265,8 +265,8 @@ def test_argument_errors(small, dev):
                        torch.empty((17, 512), device=dev), small.tables,
                        torch.zeros((17, 6), dtype=torch.int32, device=dev),
                        torch.zeros((17, 6), device=dev), **kw)
-    with pytest.raises(RuntimeError):      # int64 ids
-        ops.moe_decode(x, out, small.tables, ids.long(), w, **kw)
+    with pytest.raises(RuntimeError):      # int16 ids (int32 and int64 are accepted)
+        ops.moe_decode(x, out, small.tables, ids.to(torch.int16), w, **kw)
     with pytest.raises(RuntimeError):      # non-finite limit
         ops.moe_decode(x, out, small.tables, ids, w, swiglu_limit=float("inf"), **kw)
     with pytest.raises(RuntimeError):      # a 0-bit width is not a width

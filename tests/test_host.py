@@ -103,6 +103,35 @@ def test_moe_argument_errors_without_device(kw, msg):
     assert msg in _err()
 
 
+def _routed_call(entry, **kw):
+    lib = _lib.load()
+    one = ctypes.c_void_p(16)
+    a = dict(x=one, x_kind=0, out=one, out_kind=2, m=1, hidden=512, intermediate=256, n_experts=4, topk=2,
+             tabs=[one] * 9, ids=one, ids_kind=1, w=one, w_kind=1, emap=None, n_global=0, ebits=None, bits=3,
+             mask=0, cb=1, limit=10.0, scratch=one, scratch_bytes=1 << 30, stream=None)
+    a.update(kw)
+    return getattr(lib, entry)(a["x"], a["x_kind"], a["out"], a["out_kind"], a["m"], a["hidden"], a["intermediate"],
+                               a["n_experts"], a["topk"], *a["tabs"], a["ids"], a["ids_kind"], a["w"], a["w_kind"],
+                               a["emap"], a["n_global"], a["ebits"], a["bits"], a["mask"], a["cb"], a["limit"],
+                               a["scratch"], a["scratch_bytes"], a["stream"])
+
+
+@pytest.mark.parametrize("entry", ["exl3_moe_decode_routed", "exl3_moe_prefill_routed"])
+@pytest.mark.parametrize("kw,msg", [
+    ({"ids_kind": 2}, "int32 or int64"),
+    ({"w_kind": 3}, "fp16, bf16 or fp32"),
+    ({"emap": ctypes.c_void_p(16), "n_global": 0}, "expert map length"),
+    ({"emap": ctypes.c_void_p(16), "n_global": (1 << 20) + 1}, "expert map length"),
+    ({"ids": None}, "null pointer"),
+    ({"w": None}, "null pointer"),
+    ({"hidden": 500}, "multiples of 256"),
+    ({"limit": 0.0}, "SwiGLU limit"),
+])
+def test_moe_routed_argument_errors_without_device(entry, kw, msg):
+    assert _routed_call(entry, **kw) == -1
+    assert msg in _err()
+
+
 @pytest.mark.parametrize("k,n,cb,kind,msg", [
     (100, 256, 1, 2, "k must be a positive multiple of 128"),
     (256, 100, 1, 2, "n must be a positive multiple of 128"),
