@@ -391,11 +391,12 @@ __device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int 
 // with device-scope stores (another wave reduces them).  The MFMA result
 // layout (lane = n-tile + 16 * row group, register = column in the tile) is
 // transposed through LDS (`tbuf`, >= R KB, free at this point) so every store
-// instruction writes one contiguous 1 KB row.  DEV: device-scope stores (the
+// instruction writes one contiguous 1 KB row.  rowmap (LDS, optional): row r
+// goes to dst + rowmap[r] * ld instead of dst + r * ld.  DEV: device-scope stores (the
 // reader runs in the same launch); otherwise plain stores (a later launch).
 template <bool DEV = true>
 __device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float* dst, size_t ld, int R,
-                                               int cols_valid, float* tbuf) {
+                                               int cols_valid, float* tbuf, const int16_t* rowmap = nullptr) {
     const int lane = threadIdx.x & (WAVE - 1);
     const int c = lane & 15, rg = lane >> 4;
     __syncthreads();
@@ -413,8 +414,9 @@ __device__ __forceinline__ void store_partials(const float4_t (&acc)[16], float*
     if (4 * lane < cols_valid)
         for (int row = 0; row < R; ++row) {
             const float4_t v = reinterpret_cast<const float4_t*>(tbuf + row * COLS)[lane];
-            if constexpr (DEV) st_dev4(dst + (size_t)row * ld + 4 * lane, v);
-            else *reinterpret_cast<float4_t*>(dst + (size_t)row * ld + 4 * lane) = v;
+            float* d = dst + (size_t)(rowmap ? rowmap[row] : row) * ld + 4 * lane;
+            if constexpr (DEV) st_dev4(d, v);
+            else *reinterpret_cast<float4_t*>(d) = v;
         }
 }
 

@@ -35,6 +35,8 @@
 //     block of `out` in top-k slot order (fp32) and casts once.
 //   * Counters are reset by whoever consumes them; flags compare against an
 //     epoch the last retiring wave advances, so the control block is zeroed once.
+// Short layers run the same items as three plain launches instead (the
+// phased launches below, keyed by top-k slot), with bitwise the same result.
 // Reference counterpart: lna2_kernel<K> (lna_moe_ticket.cu:240-429), whose expert
 // teams need co-resident CTAs and a team barrier (lna_moe_ticket.cu:459-466).
 #pragma once
@@ -72,9 +74,9 @@ __host__ __device__ inline int item_steps(int k, int64_t units, int64_t waves) {
 
 struct Layout {
     int nI, nH, SA, SB, stepsA, stepsB;
-    int64_t ctrl, cls, cntA, doneA, cntB, cntG, doneB, plan, PA, DI, PB, DC, total;
+    int64_t ctrl, cls, cntA, doneA, cntB, cntG, doneB, PA, DI, PB, DC, total;
 };
-constexpr int64_t PLAN_BYTES = 4096;          // the route plan, saved for the phased launches
+constexpr int64_t PLAN_BYTES = 4096;          // bound on the route plan (LDS)
 
 __host__ __device__ inline int64_t al(int64_t v) { return (v + 255) / 256 * 256; }
 
@@ -101,7 +103,6 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     L.cntB = o;  o += (int64_t)MAX_SLOTS * MAX_BLOCKS * WORD_STRIDE;
     L.cntG = o;  o += (int64_t)MAX_BLOCKS * WORD_STRIDE;
     L.doneB = o; o += (int64_t)MAX_BLOCKS * WORD_STRIDE;
-    L.plan = o;  o += PLAN_BYTES;
     o = al(o);
     L.PA = o;    o = al(o + P * 2 * L.SA * I * 4);
     L.DI = o;    o = al(o + P * I * 2);
@@ -167,8 +168,11 @@ struct Tracer {
 #if EXL3_TRACE
     uint2* buf = nullptr;
     int n = 0;
-    __device__ void init(char* base) {
-        if (blockIdx.x < TRACE_WAVES) buf = reinterpret_cast<uint2*>(base) + (size_t)blockIdx.x * TRACE_EVENTS;
+    // records of workgroup b go to wave slot slot0 + b (phased launches use
+    // disjoint slot ranges so one call's launches do not overwrite each other)
+    __device__ void init(char* base, int slot0 = 0) {
+        const int slot = slot0 + (int)blockIdx.x;
+        if (slot < TRACE_WAVES) buf = reinterpret_cast<uint2*>(base) + (size_t)slot * TRACE_EVENTS;
     }
     __device__ void operator()(uint32_t ev, uint32_t arg = 0) {
         if (buf && n < TRACE_EVENTS - 1 && threadIdx.x == 0) {
@@ -179,7 +183,7 @@ struct Tracer {
         ++n;
     }
 #else
-    __device__ void init(char*) {}
+    __device__ void init(char*, int = 0) {}
     __device__ void operator()(uint32_t, uint32_t = 0) {}
 #endif
 };
@@ -194,7 +198,7 @@ struct Plan {
     int8_t gbits[MAX_SLOTS];
     int16_t slotpair[MAX_SLOTS]; // pair of slot (row*topk + j), -1 if invalid
 };
-static_assert(sizeof(Plan) <= PLAN_BYTES && sizeof(Plan) % 4 == 0, "plan fits its scratch slot");
+static_assert(sizeof(Plan) <= PLAN_BYTES && sizeof(Plan) % 4 == 0, "plan size bound");
 
 // Expert-major row bitmask, then a wave-wide exclusive scan over experts
 // (lna_moe_ticket.cu:167-214 computes the same plan with block scans).
@@ -384,10 +388,11 @@ __device__ __forceinline__ void load_half4(uint16_t (&v)[4], int64_t addr, int c
 // uniform branch per wave).
 
 // gate/up partial sums of (expert e, pairs pb.., rows `mask`, projection p,
-// 256-column block cb, k-chunk kc).
+// 256-column block cb, k-chunk kc).  rowmap (LDS, optional): the pair of the
+// r-th row is rowmap[r] instead of pb + r.
 template <int B, int CB, bool DEV>
 __device__ __forceinline__ void gateup_partials(const Params& P, int e, int pb, uint32_t mask, uint16_t* xa, int p,
-                                                int cb, int kc, Tracer& tr) {
+                                                int cb, int kc, Tracer& tr, const int16_t* rowmap = nullptr) {
     const Layout& L = P.L;
     const int R = __popc(mask);
     const int kchunk = L.stepsA * STEP_K;
@@ -412,13 +417,46 @@ __device__ __forceinline__ void gateup_partials(const Params& P, int e, int pb, 
     tr(EV_A_MMA);
 
     float* PA = at<float>(P.scratch, L.PA);
-    store_partials<DEV>(acc, PA + ((size_t)(pb * 2 + p) * L.SA + kc) * P.I + cb * COLS, (size_t)2 * L.SA * P.I, R,
-                        COLS, reinterpret_cast<float*>(xa));
+    store_partials<DEV>(acc, PA + ((size_t)((rowmap ? 0 : pb) * 2 + p) * L.SA + kc) * P.I + cb * COLS,
+                        (size_t)2 * L.SA * P.I, R, COLS, reinterpret_cast<float*>(xa), rowmap);
 }
 
-// gate/up finish of (expert e, pairs pb..pb+R-1, column block cb): the split-K
-// sums in chunk order, output Hadamard + svh, clamped SwiGLU, fp16, the down
-// projection's suh and input Hadamard; stores the fp16 down input DI.
+// Four fp16 down-input values of one pair at columns col..col+3 of the
+// intermediate (col % 4 == 0; each half-wave holds one 128-block): the gate/up
+// split-K sums in chunk order, output Hadamard + svh, clamped SwiGLU, fp16, the
+// down projection's suh and input Hadamard.  gsv/usv/dsu: the expert's scales
+// at those columns.
+template <int CPOL>
+__device__ __forceinline__ uint2 down_input4(const Params& P, int pair, int col, const uint16_t (&gsv)[4],
+                                             const uint16_t (&usv)[4], const uint16_t (&dsu)[4]) {
+    const Layout& L = P.L;
+    const float* PA = at<float>(P.scratch, L.PA);
+    float4_t ga, ua;
+    // uniform buffer bases, the pair in the per-lane offset: `pair` may differ
+    // between the half-waves (< 1 GB of partials, inside the 32-bit offset)
+    sum_partials2<CPOL>(PA, PA + (size_t)L.SA * P.I, ((uint32_t)pair * 2u * (uint32_t)(L.SA * P.I) + (uint32_t)col) * 4u,
+                        P.I, L.SA, ga, ua);
+    float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
+    fwht128_x4(gv);
+    fwht128_x4(uv);
+    float dv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float gg = gv[i] * HAD_NORM * f16_bits_to_f32(gsv[i]);
+        const float uu = uv[i] * HAD_NORM * f16_bits_to_f32(usv[i]);
+        const uint16_t act = f32_to_f16_bits(silu_clamped(gg, uu, P.limit));
+        // down input rotation: half(act * down_suh), fp32 butterflies
+        dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[i])));
+    }
+    fwht128_x4(dv);
+    uint2 packed;
+    packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
+    packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
+    return packed;
+}
+
+// gate/up finish of (expert e, pairs pb..pb+R-1, column block cb): stores the
+// fp16 down input DI of every pair.
 template <bool DEV>
 __device__ __forceinline__ void gateup_finish(const Params& P, int e, int pb, int R, int cb) {
     const Layout& L = P.L;
@@ -429,30 +467,10 @@ __device__ __forceinline__ void gateup_finish(const Params& P, int e, int pb, in
     load_half4(gsv, P.gsv[e], col);
     load_half4(usv, P.usv[e], col);
     load_half4(dsu, P.dsu[e], col);
-    const float* PA = at<float>(P.scratch, L.PA);
     uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
     for (int r = 0; r < R; ++r) {
         const int pair = pb + r;
-        float4_t ga, ua;
-        sum_partials2<DEV ? CPOL_SC1 : CPOL_PLAIN>(PA + (size_t)(pair * 2 + 0) * L.SA * P.I,
-                                                  PA + (size_t)(pair * 2 + 1) * L.SA * P.I, (uint32_t)col * 4u, P.I,
-                                                  L.SA, ga, ua);
-        float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
-        fwht128_x4(gv);
-        fwht128_x4(uv);
-        float dv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const float gg = gv[i] * HAD_NORM * f16_bits_to_f32(gsv[i]);
-            const float uu = uv[i] * HAD_NORM * f16_bits_to_f32(usv[i]);
-            const uint16_t act = f32_to_f16_bits(silu_clamped(gg, uu, P.limit));
-            // down input rotation: half(act * down_suh), fp32 butterflies
-            dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[i])));
-        }
-        fwht128_x4(dv);
-        uint2 packed;
-        packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
-        packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
+        const uint2 packed = down_input4<DEV ? CPOL_SC1 : CPOL_PLAIN>(P, pair, col, gsv, usv, dsu);
         uint32_t* dst = reinterpret_cast<uint32_t*>(DI + (size_t)pair * P.I + col);
         if constexpr (DEV) st_dev2(dst, packed);
         else *reinterpret_cast<uint2*>(dst) = packed;
@@ -722,102 +740,182 @@ __global__ __launch_bounds__(64, 2) void moe_kernel(Params P) {   // 2 waves per
     }
 }
 
-// ---------------------------------------------------------------- phased launches
+// ---------------------------------------------------------------- phased launches (short layers)
 //
-// Small batches: four launches instead of one, each a plain grid with one
-// item per workgroup -- gate/up partials; the gate/up finish of every
-// (group, column block); down partials; down finish + gather per (H block,
-// row).  The launch boundaries order the data (plain stores and loads).  With
-// little work to overlap them, a boundary (about 2 us in a graph) is cheaper
-// than the ticket kernel's chains of device-scope stores, counters, flag polls
-// and loads.  Same items, same sums in the same order: the results are
-// bitwise those of the ticket kernel.
+// Three plain launches on one stream, keyed by top-k slot instead of the
+// expert-sorted route plan: an item's slot o names its expert e, the item runs
+// only when o is e's first slot, and it finds the rows routed to e itself (one
+// ballot over the call's slot ids: no plan, no barrier before the first weight
+// load).  The pair (row r, expert e) is indexed by the first slot of row r
+// that holds e, so partial sums and down outputs are found by slot and the
+// last launch sums a row's slots directly.  Item sizes, the sums and their
+// order are the ticket kernel's, so both schedules give bitwise the same out.
 
-__device__ __forceinline__ void save_plan(const Plan& pl, Plan* dst) {
-    const int* s = reinterpret_cast<const int*>(&pl);
-    int* d = reinterpret_cast<int*>(dst);
-    for (int i = threadIdx.x; i < (int)(sizeof(Plan) / 4); i += WAVE) d[i] = s[i];
+struct SlotGroup {
+    int e, R, bits;
+    uint32_t mask;     // rows routed to e
+};
+
+// Expert of slot o, its rows and each row's pair slot (pslot[r], LDS, for the
+// r-th row in ascending order).  False when slot o holds no valid expert or is
+// not the first slot holding it.
+__device__ __forceinline__ bool slot_group(const Params& P, int o, SlotGroup& g, int16_t* pslot) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int S = P.m * P.topk;                 // <= MAX_SLOTS = 3 * WAVE: three slots per lane
+    static_assert(MAX_SLOTS <= 3 * WAVE, "slot ids fit three per lane");
+    const int sl[3] = {lane, lane + WAVE, lane + 2 * WAVE};
+    int v[3];
+    P.rt.local_n(sl, S, P.E, v);
+    const int oi = o / WAVE;
+    const int e = __builtin_amdgcn_readlane(oi == 0 ? v[0] : oi == 1 ? v[1] : v[2], o & (WAVE - 1));
+    if (e < 0) return false;
+    uint64_t mk[3];
+#pragma unroll
+    for (int i = 0; i < 3; ++i) mk[i] = __ballot(v[i] == e);
+    const int first = mk[0] ? __builtin_ctzll(mk[0])
+                    : mk[1] ? WAVE + __builtin_ctzll(mk[1]) : 2 * WAVE + __builtin_ctzll(mk[2]);
+    if (first != o) return false;
+    uint32_t mask = 0u;
+    int R = 0;
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        uint64_t bits = mk[i];
+        while (bits) {
+            const int s = WAVE * i + __builtin_ctzll(bits);
+            bits &= bits - 1u;
+            const int row = s / P.topk;
+            if (!((mask >> row) & 1u)) {
+                mask |= 1u << row;
+                if (lane == 0) pslot[R] = (int16_t)s;
+                ++R;
+            }
+        }
+    }
+    g.e = e;
+    g.R = R;
+    g.mask = mask;
+    g.bits = P.ebits ? P.ebits[e] : P.bits;
+    __syncthreads();
+    return true;
 }
 
-// Launch 1: item = (group, projection, column block of I, k-chunk); every
-// workgroup builds the route plan, the first one saves it for launches 2-4.
+// Down input of the rows pslot[0..R) at intermediate columns [k0, k0 + kchunk)
+// (kchunk a multiple of 128), written into the LDS A tile: each half-wave
+// computes one (row, 128-block) unit per pass (its butterflies never leave the
+// half-wave, so a half-wave without a unit skips the pass).
+__device__ __forceinline__ void down_input_chunk(const Params& P, int e, int R, const int16_t* pslot, uint16_t* xa,
+                                                 int k0, int kchunk) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int nblk = kchunk / 128;
+    const int units = R * nblk;
+    for (int u0 = 0; u0 < units; u0 += 2) {
+        const int u = u0 + (lane >> 5);
+        if (u < units) {
+            const int r = u / nblk, b = u - r * nblk;
+            const int kk = 128 * b + 4 * (lane & 31);      // column within the chunk
+            const int col = k0 + kk;
+            uint16_t gsv[4], usv[4], dsu[4];
+            load_half4(gsv, P.gsv[e], col);
+            load_half4(usv, P.usv[e], col);
+            load_half4(dsu, P.dsu[e], col);
+            const uint2 pk = down_input4<CPOL_PLAIN>(P, pslot[r], col, gsv, usv, dsu);
+            const uint16_t h[4] = {(uint16_t)(pk.x & 0xffffu), (uint16_t)(pk.x >> 16), (uint16_t)(pk.y & 0xffffu),
+                                   (uint16_t)(pk.y >> 16)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xa[xa_index(r, (kk + i) >> 6, NSTEP_CAP, (kk + i) & 63)] = h[i];
+        }
+    }
+}
+
+// Launch 1: item = (slot, projection, column block of I, k-chunk).
 template <uint32_t MASK, int CB>
-__global__ __launch_bounds__(64, 2) void moe_phase_gateup(Params P) {
+__global__ __launch_bounds__(64, 2) void moe_slot_gateup(Params P) {
     extern __shared__ __align__(16) uint16_t xa[];   // moe_lds_kb(m, E) KB
-    __shared__ Plan pl;
+    __shared__ int16_t pslot[MAX_M];
     const Layout& L = P.L;
-    build_plan(P, pl, reinterpret_cast<char*>(xa));
-    if (blockIdx.x == 0) save_plan(pl, at<Plan>(P.scratch, L.plan));
-    const int per_g = 2 * L.nI * L.SA;
-    const int g = blockIdx.x / per_g;
-    if (g >= pl.U) return;
-    int rem = blockIdx.x - g * per_g;
+    Tracer tr;
+    tr.init(P.scratch + P.trace_off);
+    tr(EV_START);
+    const int per_o = 2 * L.nI * L.SA;
+    const int o = blockIdx.x / per_o;
+    SlotGroup g;
+    if (!slot_group(P, o, g, pslot)) return;
+    tr(EV_PLAN);
+    int rem = blockIdx.x - o * per_o;
     const int p = rem / (L.nI * L.SA);
     rem -= p * L.nI * L.SA;
     const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
-    Tracer tr;
-    dispatch_bits<MASK>(pl.gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
-        gateup_partials<decltype(BI)::value, CB, false>(P, pl.gexp[g], pl.gpair[g], pl.gmask[g], xa, p, cb, kc, tr);
+    dispatch_bits<MASK>(g.bits, &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
+        gateup_partials<decltype(BI)::value, CB, false>(P, g.e, 0, g.mask, xa, p, cb, kc, tr, pslot);
     });
+    tr(EV_A_END);
 }
 
-// Launch 2: item = (group, column block of I).
-template <int DUMMY = 0>
-__global__ __launch_bounds__(64) void moe_phase_act(Params P) {
-    const Layout& L = P.L;
-    const Plan* pl = at<Plan>(P.scratch, L.plan);
-    const int g = blockIdx.x / L.nI, cb = blockIdx.x - (blockIdx.x / L.nI) * L.nI;
-    if (g >= pl->U) return;
-    gateup_finish<false>(P, pl->gexp[g], pl->gpair[g], __popc(pl->gmask[g]), cb);
-}
-
-// Launch 3: item = (group, column block of H, k-chunk of I).
+// Launch 2: item = (slot, column block of H, k-chunk of I).  The item first
+// computes its chunk of the down input (the activation of the gate/up sums)
+// into LDS, while its first weight tile is in flight.
 template <uint32_t MASK, int CB>
-__global__ __launch_bounds__(64, 2) void moe_phase_down(Params P) {
+__global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
     extern __shared__ __align__(16) uint16_t xa[];   // moe_lds_kb(m, E) KB
+    __shared__ int16_t pslot[MAX_M];
     const Layout& L = P.L;
-    const Plan* pl = at<Plan>(P.scratch, L.plan);
-    const int per_g = L.nH * L.SB;
-    const int g = blockIdx.x / per_g;
-    if (g >= pl->U) return;
-    const int rem = blockIdx.x - g * per_g;
-    const int cb = rem / L.SB, kc = rem - (rem / L.SB) * L.SB;
-    const int e = pl->gexp[g], pb = pl->gpair[g], R = __popc(pl->gmask[g]);
     Tracer tr;
-    dispatch_bits<MASK>(pl->gbits[g], &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
+    tr.init(P.scratch + P.trace_off, TRACE_WAVES / 2);
+    tr(EV_B_BEGIN);
+    const int per_o = L.nH * L.SB;
+    const int o = blockIdx.x / per_o;
+    SlotGroup g;
+    if (!slot_group(P, o, g, pslot)) return;
+    tr(EV_PLAN);
+    const int rem = blockIdx.x - o * per_o;
+    const int cb = rem / L.SB, kc = rem - (rem / L.SB) * L.SB;
+    dispatch_bits<MASK>(g.bits, &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
         constexpr int B = decltype(BI)::value;
-        const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[e]), P.H / 16,
-                                        kc * L.stepsB * STEP_K / 16, cb * 16);
+        const int kchunk = L.stepsB * STEP_K;
+        const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[g.e]), P.H / 16, kc * kchunk / 16,
+                                        cb * 16);
         TileRegs<B> first;
         load_tile<B>(first, tp);
-        down_partials<B, CB, false>(P, pb, R, xa, cb, kc, first, tp, tr);
+        down_input_chunk(P, g.e, g.R, pslot, xa, kc * kchunk, kchunk);
+        __syncthreads();
+        tr(EV_B_WAITED);
+        float4_t acc[16];
+        mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, g.R, acc);
+        tr(EV_B_MMA);
+        store_partials<false>(acc, at<float>(P.scratch, L.PB) + (size_t)kc * P.H + cb * COLS, (size_t)L.SB * P.H,
+                              g.R, COLS, reinterpret_cast<float*>(xa), pslot);
     });
+    tr(EV_B_END);
 }
 
-// Launch 4: item = (column block of H, row), one wave per top-k slot: each
+// Launch 3: item = (column block of H, row), one wave per top-k slot: each
 // wave finishes its slot's down output (the split-K sum, output Hadamard,
 // svh), so every slot's loads are in flight at once; wave 0 then adds them in
 // top-k slot order (fp32) and casts once.
 template <int DUMMY = 0>
-__global__ __launch_bounds__(MAX_TOPK * WAVE) void moe_phase_finish(Params P) {
+__global__ __launch_bounds__(MAX_TOPK * WAVE) void moe_slot_finish(Params P) {
     __shared__ float4_t slot_val[MAX_TOPK][WAVE];
-    const Layout& L = P.L;
-    const Plan* pl = at<Plan>(P.scratch, L.plan);
     const int cb = blockIdx.x / P.m, row = blockIdx.x - (blockIdx.x / P.m) * P.m;
     const int j = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    const int pair = pl->slotpair[row * P.topk + j];
-    if (pair >= 0) {
+    const int s0 = row * P.topk;
+    const int sl[1] = {s0 + (lane < P.topk ? lane : P.topk)};         // lanes past top-k read nothing
+    int vv[1];
+    P.rt.local_n(sl, s0 + P.topk, P.E, vv);
+    const int v = vv[0];                                              // the row's experts, one per lane
+    const int e = __builtin_amdgcn_readlane(v, j);
+    if (e >= 0) {
+        const int pair = s0 + __builtin_ctzll(__ballot(v == e));       // the row's first slot with e
         uint16_t dsv[4];
-        load_half4(dsv, P.dsv[P.rt.local(row * P.topk + j, P.E)], col);
+        load_half4(dsv, P.dsv[e], col);
         slot_val[j][lane] = down_value<CPOL_PLAIN>(P, pair, dsv, col);
     }
     __syncthreads();
     if (j != 0) return;
     float s4[4] = {0.f, 0.f, 0.f, 0.f};
     for (int k = 0; k < P.topk; ++k) {      // fp32 sum in top-k slot order
-        if (pl->slotpair[row * P.topk + k] < 0) continue;
-        const float w = P.rt.weight(row * P.topk + k);
+        if (__builtin_amdgcn_readlane(v, k) < 0) continue;
+        const float w = P.rt.weight(s0 + k);
         const float4_t o = slot_val[k][lane];
 #pragma unroll
         for (int i = 0; i < 4; ++i) s4[i] = s4[i] + w * o[i];
@@ -830,9 +928,9 @@ __global__ __launch_bounds__(MAX_TOPK * WAVE) void moe_phase_finish(Params P) {
 template <uint32_t MASK, int CB>
 int launch_moe(const Params& P, int waves, int lds_kb, hipStream_t stream);
 
-// The four phased launches (grids from the group bound `groups`).
+// The three phased launches.
 template <uint32_t MASK, int CB>
-int launch_phased(const Params& P, int groups, int lds_kb, hipStream_t stream);
+int launch_phased(const Params& P, int lds_kb, hipStream_t stream);
 
 template <uint32_t MASK, int CB>
 int moe_waves_per_cu(int lds_kb);

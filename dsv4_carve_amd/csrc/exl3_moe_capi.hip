@@ -21,7 +21,7 @@ namespace moe {
 
 #define EXL3_DECL(M, C)                                                          \
     template <> int launch_moe<M, C>(const Params&, int, int, hipStream_t);     \
-    template <> int launch_phased<M, C>(const Params&, int, int, hipStream_t);  \
+    template <> int launch_phased<M, C>(const Params&, int, hipStream_t);       \
     template <> int moe_waves_per_cu<M, C>(int);
 EXL3_MOE_INSTANCES(EXL3_DECL)
 #undef EXL3_DECL
@@ -30,7 +30,7 @@ struct Instance {
     uint32_t mask;
     int cb;
     int (*launch)(const Params&, int, int, hipStream_t);
-    int (*phased)(const Params&, int, int, hipStream_t);
+    int (*phased)(const Params&, int, hipStream_t);
     int (*waves)(int);
 };
 
@@ -165,7 +165,7 @@ static int moe_decode_impl(const void* x, int x_kind, void* out, int out_kind, i
 
     const int64_t steps = groups * (2LL * L.nI * (hidden / STEP_K) + (int64_t)L.nH * (intermediate / STEP_K));
     if (use_phased(m, steps, resident))
-        return kInstances[idx].phased(P, (int)groups, lds_kb, reinterpret_cast<hipStream_t>(stream));
+        return kInstances[idx].phased(P, lds_kb, reinterpret_cast<hipStream_t>(stream));
 
     const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB) + (int64_t)L.nH * m;
     const int waves = (int)(items < resident ? items : resident);

@@ -21,19 +21,18 @@ int launch_moe<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int waves, int lds_k
 }
 
 template <>
-int launch_phased<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int groups, int lds_kb, hipStream_t stream) {
+int launch_phased<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int lds_kb, hipStream_t stream) {
     const Layout& L = P.L;
     const size_t lds = (size_t)lds_kb * 1024;
-    hipLaunchKernelGGL((moe_phase_gateup<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(groups * 2 * L.nI * L.SA), dim3(WAVE),
+    const int slots = P.m * P.topk;
+    hipLaunchKernelGGL((moe_slot_gateup<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(slots * 2 * L.nI * L.SA), dim3(WAVE),
                        lds, stream, P);
     int rc = check_launch();
     if (rc) return rc;
-    hipLaunchKernelGGL((moe_phase_act<0>), dim3(groups * L.nI), dim3(WAVE), 0, stream, P);
-    if ((rc = check_launch())) return rc;
-    hipLaunchKernelGGL((moe_phase_down<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(groups * L.nH * L.SB), dim3(WAVE), lds,
+    hipLaunchKernelGGL((moe_slot_down<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(slots * L.nH * L.SB), dim3(WAVE), lds,
                        stream, P);
     if ((rc = check_launch())) return rc;
-    hipLaunchKernelGGL((moe_phase_finish<0>), dim3(L.nH * P.m), dim3(P.topk * WAVE), 0, stream, P);
+    hipLaunchKernelGGL((moe_slot_finish<0>), dim3(L.nH * P.m), dim3(P.topk * WAVE), 0, stream, P);
     return check_launch();
 }
 

@@ -25,15 +25,46 @@ struct Route {
     const int64_t* emap;    // [n_global] or null
     int ids_kind, w_kind, n_global;
 
-    // Local expert of slot s, or -1.
-    __device__ __forceinline__ int local(int s, int E) const {
-        int64_t g = ids_kind == IDS_I64 ? static_cast<const int64_t*>(ids)[s]
-                                        : (int64_t) static_cast<const int32_t*>(ids)[s];
+    // Global id of slot s as stored.
+    __device__ __forceinline__ int64_t raw(int s) const {
+        return ids_kind == IDS_I64 ? static_cast<const int64_t*>(ids)[s] : (int64_t) static_cast<const int32_t*>(ids)[s];
+    }
+
+    // Local expert of global id g, or -1.
+    __device__ __forceinline__ int map(int64_t g, int E) const {
         if (emap) {
             if (g < 0 || g >= n_global) return -1;
             g = emap[g];
         }
         return (g >= 0 && g < E) ? (int)g : -1;
+    }
+
+    // Local expert of slot s, or -1.
+    __device__ __forceinline__ int local(int s, int E) const { return map(raw(s), E); }
+
+    // local() for N slots per lane (slots >= S give -1), branch-free so all N
+    // id loads, then all N map loads, are in flight together.
+    template <int N>
+    __device__ __forceinline__ void local_n(const int (&s)[N], int S, int E, int (&out)[N]) const {
+        int64_t g[N];
+        if (ids_kind == IDS_I64) {
+            const int64_t* p = static_cast<const int64_t*>(ids);
+#pragma unroll
+            for (int i = 0; i < N; ++i) g[i] = p[s[i] < S ? s[i] : S - 1];
+        } else {
+            const int32_t* p = static_cast<const int32_t*>(ids);
+#pragma unroll
+            for (int i = 0; i < N; ++i) g[i] = p[s[i] < S ? s[i] : S - 1];
+        }
+        if (emap) {
+            int64_t mg[N];
+#pragma unroll
+            for (int i = 0; i < N; ++i) mg[i] = emap[g[i] < 0 ? 0 : g[i] >= n_global ? n_global - 1 : g[i]];
+#pragma unroll
+            for (int i = 0; i < N; ++i) g[i] = (g[i] < 0 || g[i] >= n_global) ? -1 : mg[i];
+        }
+#pragma unroll
+        for (int i = 0; i < N; ++i) out[i] = (s[i] < S && g[i] >= 0 && g[i] < E) ? (int)g[i] : -1;
     }
 
     __device__ __forceinline__ float weight(int s) const {
