@@ -54,11 +54,14 @@ static int cached_waves(int idx, int lds_kb) {
 // Schedule choice.  The phased launches win while the layer is short: below
 // about PHASED_STEPS_PER_WAVE decode steps (64 x 256 weights) per resident
 // wave the ticket kernel has too little work to hide its device-scope
-// hand-offs behind (measured on the 256-expert layer: phased faster up to 4
-// rows, even at 8, slower at 16; one GPU's TP8 share: phased faster at every
-// row count).  EXL3_MOE_PHASED_MAX_ROWS, when set, replaces the rule by a row
-// count (0: always the ticket kernel; 16: always the phased launches).
-constexpr int64_t PHASED_STEPS_PER_WAVE = 40;
+// hand-offs behind.  Measured on the 256-expert layer (hidden 4096,
+// intermediate 2048, top-8): phased 50 / 78 / 135 / 235 us at 1 / 2 / 4 / 8
+// rows against 82 / 100 / 159 / 243 for the ticket kernel, and level at 16
+// rows (382 / 387, within run-to-run spread; about 96 steps per wave), where
+// the ticket kernel stays.  One GPU's TP8 share is phased at every row count.
+// EXL3_MOE_PHASED_MAX_ROWS, when set, replaces the rule by a row count (0:
+// always the ticket kernel; 16: always the phased launches).
+constexpr int64_t PHASED_STEPS_PER_WAVE = 64;
 static bool use_phased(int64_t m, int64_t steps, int64_t resident) {
     const char* v = getenv("EXL3_MOE_PHASED_MAX_ROWS");
     if (v && *v) return m <= atoi(v);

@@ -98,7 +98,7 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
  *     serve layers of different shapes (its control words have fixed
  *     offsets).  One call at a time per scratch buffer.
  * Schedule: one persistent ticket-kernel launch for long layers, three plain
- * launches for short ones (below ~40 decode steps per resident wave); both
+ * launches for short ones (below ~64 decode steps per resident wave); both
  * give bitwise the same result.  The environment variable
  * EXL3_MOE_PHASED_MAX_ROWS, when set, picks by row count instead (0: always
  * the single launch).  Every launch is on `stream`; nothing is allocated or
