@@ -438,9 +438,13 @@ def time_stack(dev, rows, steps, warmup):
     return us, nbytes
 
 
+CPU_SAMPLE = 10          # experts per bit width timed on the CPU
+
+
 def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> dict:
-    """CPU restatement timed on four 3-bit and four 2-bit experts of the layer,
-    scaled to the mean set of distinct experts per step at this row count."""
+    """CPU restatement timed on ten 3-bit and ten 2-bit experts of the layer
+    (about 10 s of CPU work), scaled to the mean set of distinct experts per
+    step at this row count."""
     import torch
     from dsv4_carve_amd import synth
     from oracle import cpu_baseline as CB
@@ -450,8 +454,8 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
         print(f"[bench] cpu baseline: expert {e} ({b}-bit) {t * 1e3:.0f} ms", file=sys.stderr, flush=True)
         return t
 
-    t3 = float(np.mean([timed(e, 3) for e in range(4)]))
-    t2 = float(np.mean([timed(e, 2) for e in range(128, 132)]))
+    t3 = float(np.mean([timed(e, 3) for e in range(CPU_SAMPLE)]))
+    t2 = float(np.mean([timed(e, 2) for e in range(128, 128 + CPU_SAMPLE)]))
     n3 = n2 = 0.0
     for ids in us_ids:
         act = {int(e) for e in ids.reshape(-1)}
@@ -464,7 +468,7 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
         "unit": "us/layer",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"experts 0-3 (3-bit) and 128-131 (2-bit) of the layer, {rows} rows each: gate+up+down with "
+        "sample": (f"experts 0-{CPU_SAMPLE - 1} (3-bit) and 128-{127 + CPU_SAMPLE} (2-bit) of the layer, {rows} rows each: gate+up+down with "
                    f"per-call dequant + fp32 matmul (the reference CPU path), median of 3 after 1 warm-up per "
                    f"expert; mean {t3 * 1e3:.0f} ms (3-bit) and {t2 * 1e3:.0f} ms (2-bit) per expert, scaled by "
                    f"the mean distinct experts per step ({n3:.1f} 3-bit + {n2:.1f} 2-bit)"),
