@@ -11,7 +11,8 @@ seeded pool, so consecutive steps read different experts (no reuse through the
 
 Prints ONE JSON line; `value` is microseconds per layer at --rows (lower is
 better), `roofline` the achieved HBM bandwidth on the algorithmic bytes of the
-experts actually read, `cpu_baseline` the CPU restatement of the reference's
+experts actually read (over the whole layer: its gate/up, activation, down and
+finishing launches), `cpu_baseline` the CPU restatement of the reference's
 CPU path timed on a bounded sample on this host.
 """
 
@@ -607,7 +608,7 @@ def main() -> int:
     prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_c2_m16_traffic.json")
     if os.path.isfile(prof):
         with open(prof) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            traffic = json.load(f).get("hbm_bytes_per_layer")
 
     line = {
         "metric": "routed-MoE decode us/layer + achieved HBM GB/s (% of 8 TB/s), rows 1-16",
@@ -627,7 +628,7 @@ def main() -> int:
                    "rows": a.rows, "experts": EXPERTS, "topk": TOPK, "hidden": HIDDEN, "intermediate": INTER},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "bytes_per_launch": int(nbytes)},
+                     "bytes_per_layer": int(nbytes)},
         "cpu_baseline": cpu,
     }
     line.update(extra)

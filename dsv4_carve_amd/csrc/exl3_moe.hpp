@@ -35,8 +35,9 @@
 //     block of `out` in top-k slot order (fp32) and casts once.
 //   * Counters are reset by whoever consumes them; flags compare against an
 //     epoch the last retiring wave advances, so the control block is zeroed once.
-// Short layers run the same items as three plain launches instead (the
-// phased launches below, keyed by top-k slot), with bitwise the same result.
+// Short layers run the same items as three or four plain launches instead
+// (the phased launches below, keyed by top-k slot), with bitwise the same
+// result.
 // Reference counterpart: lna2_kernel<K> (lna_moe_ticket.cu:240-429), whose expert
 // teams need co-resident CTAs and a team barrier (lna_moe_ticket.cu:459-466).
 #pragma once
@@ -139,6 +140,7 @@ struct Params {
     Layout L;
     int64_t trace_off;   // start of the phase-trace region (EXL3_TRACE builds)
     int nclass;          // ticket classes: the XCD count, or 1 for small grids
+    int fuse_act;        // phased launches: down items compute their own input
 };
 
 template <typename T>
@@ -742,7 +744,8 @@ __global__ __launch_bounds__(64, 2) void moe_kernel(Params P) {   // 2 waves per
 
 // ---------------------------------------------------------------- phased launches (short layers)
 //
-// Three plain launches on one stream, keyed by top-k slot instead of the
+// Plain launches on one stream (gate/up, the activation for larger batches,
+// down, finish), keyed by top-k slot instead of the
 // expert-sorted route plan: an item's slot o names its expert e, the item runs
 // only when o is e's first slot, and it finds the rows routed to e itself (one
 // ballot over the call's slot ids: no plan, no barrier before the first weight
@@ -851,9 +854,32 @@ __global__ __launch_bounds__(64, 2) void moe_slot_gateup(Params P) {
     tr(EV_A_END);
 }
 
-// Launch 2: item = (slot, column block of H, k-chunk of I).  The item first
-// computes its chunk of the down input (the activation of the gate/up sums)
-// into LDS, while its first weight tile is in flight.
+// Launch 2 (large batches only): item = (slot, column block of I); stores the
+// fp16 down input DI of every row of the slot's expert.
+template <int DUMMY = 0>
+__global__ __launch_bounds__(64) void moe_slot_act(Params P) {
+    __shared__ int16_t pslot[MAX_M];
+    const Layout& L = P.L;
+    const int o = blockIdx.x / L.nI, cb = blockIdx.x - (blockIdx.x / L.nI) * L.nI;
+    SlotGroup g;
+    if (!slot_group(P, o, g, pslot)) return;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
+    uint16_t gsv[4], usv[4], dsu[4];
+    load_half4(gsv, P.gsv[g.e], col);
+    load_half4(usv, P.usv[g.e], col);
+    load_half4(dsu, P.dsu[g.e], col);
+    uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
+    for (int r = 0; r < g.R; ++r) {
+        const int pair = pslot[r];
+        *reinterpret_cast<uint2*>(DI + (size_t)pair * P.I + col) = down_input4<CPOL_PLAIN>(P, pair, col, gsv, usv, dsu);
+    }
+}
+
+// Launch 3: item = (slot, column block of H, k-chunk of I).  For small
+// batches (fuse_act) the item first computes its chunk of the down input (the
+// activation of the gate/up sums) into LDS while its first weight tile is in
+// flight; otherwise it copies that chunk from the activation launch's DI.
 template <uint32_t MASK, int CB>
 __global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
     extern __shared__ __align__(16) uint16_t xa[];   // moe_lds_kb(m, E) KB
@@ -876,7 +902,13 @@ __global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
                                         cb * 16);
         TileRegs<B> first;
         load_tile<B>(first, tp);
-        down_input_chunk(P, g.e, g.R, pslot, xa, kc * kchunk, kchunk);
+        if (P.fuse_act) {
+            down_input_chunk(P, g.e, g.R, pslot, xa, kc * kchunk, kchunk);
+        } else {
+            const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
+            for (int r = 0; r < g.R; ++r)
+                copy_row<false>(DI + (size_t)pslot[r] * P.I + kc * kchunk, xa, r, kchunk / 128, NSTEP_CAP);
+        }
         __syncthreads();
         tr(EV_B_WAITED);
         float4_t acc[16];
@@ -888,7 +920,7 @@ __global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
     tr(EV_B_END);
 }
 
-// Launch 3: item = (column block of H, row), one wave per top-k slot: each
+// Launch 4: item = (column block of H, row), one wave per top-k slot: each
 // wave finishes its slot's down output (the split-K sum, output Hadamard,
 // svh), so every slot's loads are in flight at once; wave 0 then adds them in
 // top-k slot order (fp32) and casts once.
@@ -928,7 +960,7 @@ __global__ __launch_bounds__(MAX_TOPK * WAVE) void moe_slot_finish(Params P) {
 template <uint32_t MASK, int CB>
 int launch_moe(const Params& P, int waves, int lds_kb, hipStream_t stream);
 
-// The three phased launches.
+// The phased launches (three, or four with a separate activation launch).
 template <uint32_t MASK, int CB>
 int launch_phased(const Params& P, int lds_kb, hipStream_t stream);
 

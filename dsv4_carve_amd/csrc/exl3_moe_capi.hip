@@ -51,21 +51,31 @@ static int cached_waves(int idx, int lds_kb) {
     return cache[dev][idx][lds_kb];
 }
 
-// Schedule choice.  The phased launches win while the layer is short: below
-// about PHASED_STEPS_PER_WAVE decode steps (64 x 256 weights) per resident
-// wave the ticket kernel has too little work to hide its device-scope
-// hand-offs behind.  Measured on the 256-expert layer (hidden 4096,
-// intermediate 2048, top-8): phased 50 / 78 / 135 / 235 us at 1 / 2 / 4 / 8
-// rows against 82 / 100 / 159 / 243 for the ticket kernel, and level at 16
-// rows (382 / 387, within run-to-run spread; about 96 steps per wave), where
-// the ticket kernel stays.  One GPU's TP8 share is phased at every row count.
-// EXL3_MOE_PHASED_MAX_ROWS, when set, replaces the rule by a row count (0:
-// always the ticket kernel; 16: always the phased launches).
-constexpr int64_t PHASED_STEPS_PER_WAVE = 64;
-static bool use_phased(int64_t m, int64_t steps, int64_t resident) {
+// Phased launches: down items assemble their own input (no activation launch)
+// while the layer's activation is small, m * topk * intermediate <=
+// FUSE_ACT_MAX_ELEMS; beyond, the redundant assembly (every H block repeats
+// it) costs more than the extra launch.  Measured, us, assembled / separate:
+// 256-expert layer (intermediate 2048, top-8), 1 row 52 / 52, 2 rows 81 / 80,
+// 4 rows 139 / 133, 16 rows 387 / 375; one GPU's TP8 share (intermediate 256,
+// top-6), 1 row 27 / 30, 16 rows 76 / 80.  EXL3_MOE_FUSE_ACT_MAX_ROWS, when
+// set, replaces the rule by a row count.
+constexpr int64_t FUSE_ACT_MAX_ELEMS = 32768;
+static bool fuse_act(int64_t m, int64_t topk, int64_t intermediate) {
+    const char* v = getenv("EXL3_MOE_FUSE_ACT_MAX_ROWS");
+    if (v && *v) return m <= atoi(v);
+    return m * topk * intermediate <= FUSE_ACT_MAX_ELEMS;
+}
+
+// Schedule choice.  The phased launches are the default: on the 256-expert
+// layer they beat the ticket kernel at every row count (1 / 2 / 4 / 8 / 16
+// rows: 50 / 78 / 134 / 225 / 360 us against 82 / 100 / 159 / 248 / 379), and
+// one GPU's TP8 share likewise.  The ticket kernel (one persistent launch,
+// device-scope hand-offs) stays available: EXL3_MOE_PHASED_MAX_ROWS, when
+// set, selects by row count (0: always the ticket kernel).
+static bool use_phased(int64_t m) {
     const char* v = getenv("EXL3_MOE_PHASED_MAX_ROWS");
     if (v && *v) return m <= atoi(v);
-    return steps < PHASED_STEPS_PER_WAVE * resident;
+    return true;
 }
 
 }  // namespace moe
@@ -165,9 +175,9 @@ static int moe_decode_impl(const void* x, int x_kind, void* out, int out_kind, i
     P.scratch = reinterpret_cast<char*>(scratch);
     P.L = L;
     P.trace_off = trace_off;
+    P.fuse_act = fuse_act(m, topk, intermediate) ? 1 : 0;
 
-    const int64_t steps = groups * (2LL * L.nI * (hidden / STEP_K) + (int64_t)L.nH * (intermediate / STEP_K));
-    if (use_phased(m, steps, resident))
+    if (use_phased(m))
         return kInstances[idx].phased(P, lds_kb, reinterpret_cast<hipStream_t>(stream));
 
     const int64_t items = groups * (2LL * L.nI * L.SA + (int64_t)L.nH * L.SB) + (int64_t)L.nH * m;

@@ -29,6 +29,10 @@ int launch_phased<EXL3_MOE_MASK, EXL3_MOE_CB>(const Params& P, int lds_kb, hipSt
                        lds, stream, P);
     int rc = check_launch();
     if (rc) return rc;
+    if (!P.fuse_act) {
+        hipLaunchKernelGGL((moe_slot_act<0>), dim3(slots * L.nI), dim3(WAVE), 0, stream, P);
+        if ((rc = check_launch())) return rc;
+    }
     hipLaunchKernelGGL((moe_slot_down<EXL3_MOE_MASK, EXL3_MOE_CB>), dim3(slots * L.nH * L.SB), dim3(WAVE), lds,
                        stream, P);
     if ((rc = check_launch())) return rc;

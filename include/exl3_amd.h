@@ -97,11 +97,12 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
  *     once before first use; self-resetting afterwards, and one buffer may
  *     serve layers of different shapes (its control words have fixed
  *     offsets).  One call at a time per scratch buffer.
- * Schedule: one persistent ticket-kernel launch for long layers, three plain
- * launches for short ones (below ~64 decode steps per resident wave); both
- * give bitwise the same result.  The environment variable
+ * Schedule: plain launches keyed by top-k slot (gate/up, an activation launch
+ * when m * topk * intermediate > 32768, down, finish), or one persistent
+ * ticket-kernel launch; both give bitwise the same result.  The launches are
+ * the default at every batch size.  The environment variable
  * EXL3_MOE_PHASED_MAX_ROWS, when set, picks by row count instead (0: always
- * the single launch).  Every launch is on `stream`; nothing is allocated or
+ * the ticket kernel).  Every launch is on `stream`; nothing is allocated or
  * synchronised, so a call can be captured in a graph.
  */
 int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk);

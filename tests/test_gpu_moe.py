@@ -179,6 +179,42 @@ def test_phased_equals_ticket_bitwise(small, profile):
         assert torch.equal(a, b), f"{profile} m={m}: phased and ticket outputs differ"
 
 
+@contextlib.contextmanager
+def fuse_act(max_rows):
+    """Phased launches: down items assemble their own input up to `max_rows`
+    rows, beyond it a separate activation launch does."""
+    key = "EXL3_MOE_FUSE_ACT_MAX_ROWS"
+    old = os.environ.get(key)
+    os.environ[key] = str(max_rows)
+    try:
+        yield
+    finally:
+        if old is None:
+            os.environ.pop(key, None)
+        else:
+            os.environ[key] = old
+
+
+@pytest.mark.parametrize("profile", ["random", "within-row-dup", "invalid"])
+def test_fused_activation_equals_separate_launch(small, profile):
+    """Down items that assemble their input and the separate activation launch
+    run the same arithmetic: bitwise the same output."""
+    import torch
+
+    for m in (1, 3, 9, 16):
+        print(f"fused vs separate activation {profile} m={m}", flush=True)
+        ids = route_ids(m, profile)
+        w = route_weights(m, "normal")
+        x = inputs(m, "real")
+        with moe_path("phased"):
+            with fuse_act(16):
+                a = small.run(x, ids, w)
+            with fuse_act(0):
+                b = small.run(x, ids, w)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"{profile} m={m}: fused and separate activation differ"
+
+
 def test_cancel_and_zero_weights(small):
     """Fully cancelling slots (each expert twice with +w and -w) leave a
     degenerate row, judged on absolute error as in parity_native.py:54-58;
