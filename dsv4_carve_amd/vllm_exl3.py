@@ -56,6 +56,7 @@ AUTO_RECONSTRUCT_THRESHOLD = 144
 MAX_RECONSTRUCT_SLICE_N = 32768
 MOE_TABLE_KEYS = ops.MOE_TABLE_KEYS
 PREFILL_MAX_PAIRS = 65536
+_FAT_CHUNK_LOGGED = False
 
 
 # ---------------------------------------------------------------- linear
@@ -600,7 +601,7 @@ def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
     inter = int(getattr(layer, "_exl3_intermediate_local", -1))
     topk = int(ids.shape[-1])
     rows = int(x2d.shape[0]) if x2d.dim() == 2 else -1
-    if (not x2d.is_cuda or x2d.dim() != 2 or rows < 1 or rows * topk > PREFILL_MAX_PAIRS
+    if (not x2d.is_cuda or x2d.dim() != 2 or rows < 1
             or int(x2d.shape[1]) != hidden or hidden % 256 or inter % 256 or hidden > 16384 or inter > 16384
             or not 1 <= topk <= 9 or x2d.dtype not in (torch.float16, torch.bfloat16) or not float(limit) > 0.0):
         _lna2_log_reject("geometry x=%s dtype=%s hidden=%s inter=%s topk=%s limit=%s" % (
@@ -631,8 +632,19 @@ def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
         _MOE_CALLS["lna2"] += 1
     else:
         # many rows: the grouped-GEMM prefill path (the reference falls back to
-        # exllamav3's fused exl3_moe here, vllm_exl3_exl3.py.lna:1597-1704)
-        ops.moe_prefill(x_in, out, ptrs, route_ids, route_w, **kw)
+        # exllamav3's fused exl3_moe here, vllm_exl3_exl3.py.lna:1597-1704).
+        # One call takes up to PREFILL_MAX_PAIRS (token, slot) pairs and any
+        # number of rows per expert; longer batches run in token slices, as the
+        # reference's fat-chunk slicing does (:1627-1643).
+        chunk = max(1, PREFILL_MAX_PAIRS // topk)
+        if rows > chunk:
+            global _FAT_CHUNK_LOGGED
+            if not _FAT_CHUNK_LOGGED:
+                logger.info("EXL3 prefill token slicing ACTIVE (tokens=%d, slice=%d)", rows, chunk)
+                _FAT_CHUNK_LOGGED = True
+        for s0 in range(0, rows, chunk):
+            s1 = min(rows, s0 + chunk)
+            ops.moe_prefill(x_in[s0:s1], out[s0:s1], ptrs, route_ids[s0:s1], route_w[s0:s1], **kw)
         _MOE_CALLS["prefill"] += 1
     return out
 

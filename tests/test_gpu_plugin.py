@@ -188,6 +188,27 @@ def test_apply_experts_large_batches_use_prefill(dev, experts, monkeypatch):
     assert_close(y2.float().cpu().numpy(), experts.ref(x, ids, w), max_abs=2e-2 + 8e-3)
 
 
+def test_apply_experts_long_batches_run_in_token_slices(dev, experts, monkeypatch):
+    """Batches past the prefill kernel's pair limit run in token slices (the
+    reference's fat-chunk slicing); a row's result does not depend on which
+    slice it is in, so the output is bitwise the one-call output."""
+    import torch
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", "lna2")
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "2")
+    ids, w = synth.routing(40, 12, 6, seed=94)
+    x = to_dev(synth.activations(40, 512, seed=95), dev)
+    args = (x, to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
+    whole = V.apply_exl3_experts(*args)
+    monkeypatch.setattr(V, "PREFILL_MAX_PAIRS", 60)            # 10-token slices
+    sliced = V.apply_exl3_experts(*args)
+    torch.cuda.synchronize()
+    assert experts.layer._exl3_last_apply == "prefill"
+    assert torch.equal(whole, sliced), "token slices changed the result"
+    assert_close(sliced.float().cpu().numpy(), experts.ref(x.cpu().numpy(), ids, w), max_abs=2e-2 + 8e-3)
+
+
 def test_apply_experts_declines_bad_geometry(dev, experts, monkeypatch):
     from dsv4_carve_amd import vllm_exl3 as V
 
