@@ -155,9 +155,8 @@ __device__ __forceinline__ void gemv_partials(const uint16_t* __restrict__ x, co
     // weights for step 0 are in flight while the input rotation runs
     const u32x4_t* tp = tile_ptr<BITS>(trellis, N / 16, k0 / 16, cb * 16);
     TileRegs<BITS> first;
-    load_tile<BITS>(first, tp);
-    for (int m = 0; m < R; ++m)
-        had_in_row(x, (size_t)m * K + k0, 0, suh + k0, xa, m, nsteps * STEP_K / 128, GEMV_NSTEP_CAP);
+    rotate_rows_and_load<BITS>(x, K, k0, 0, suh + k0, R >= 32 ? ~0u : (1u << R) - 1u, xa, nsteps * STEP_K / 128,
+                               GEMV_NSTEP_CAP, first, tp);
     __syncthreads();
 
     float4_t acc[16];

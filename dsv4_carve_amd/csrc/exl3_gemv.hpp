@@ -338,28 +338,38 @@ __device__ __forceinline__ void fwht128_x4(float (&v)[4]) {
 // x_kind: 0 = fp16, 1 = bf16 (converted to fp16 with RNE first).
 constexpr int HAD_MAX_BLOCKS = 4;
 
-__device__ __forceinline__ void had_in_row(const void* x, size_t x_off, int x_kind, const uint16_t* suh,
-                                           uint16_t* xa, int m, int nblocks, int nsteps_cap) {
+// The global loads of had_in_row, apart from its arithmetic: a caller issues
+// them before a weight-tile prefetch, so that waiting for them (loads complete
+// in issue order) does not also wait for the tile.
+struct RowIn {
+    uint32_t x[HAD_MAX_BLOCKS], s[HAD_MAX_BLOCKS];
+};
+
+__device__ __forceinline__ void had_in_load(const void* x, size_t x_off, const uint16_t* suh, int nblocks, RowIn& in) {
     const int lane = threadIdx.x & (WAVE - 1);
-    uint32_t xx[HAD_MAX_BLOCKS], ss[HAD_MAX_BLOCKS];
     gptr_t<uint32_t> xp = as_global(reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(x) + x_off) + lane);
     gptr_t<uint32_t> sp = as_global(reinterpret_cast<const uint32_t*>(suh) + lane);
 #pragma unroll
     for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
         if (b < nblocks) {
-            xx[b] = xp[64 * b];
-            ss[b] = sp[64 * b];
+            in.x[b] = xp[64 * b];
+            in.s[b] = sp[64 * b];
         }
+}
+
+__device__ __forceinline__ void had_in_store(const RowIn& in, int x_kind, uint16_t* xa, int m, int nblocks,
+                                             int nsteps_cap) {
+    const int lane = threadIdx.x & (WAVE - 1);
 #pragma unroll
     for (int b = 0; b < HAD_MAX_BLOCKS; ++b) {
         if (b >= nblocks) break;
-        uint32_t v2 = xx[b];
+        uint32_t v2 = in.x[b];
         if (x_kind != 0)
             v2 = (uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 & 0xffffu))) |
                  ((uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 >> 16))) << 16);
         // half(x*suh): the fp32 product of two halves is exact, so one RNE cast = half mul
-        float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 & 0xffffu) * f16_bits_to_f32(ss[b] & 0xffffu)));
-        float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 >> 16) * f16_bits_to_f32(ss[b] >> 16)));
+        float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 & 0xffffu) * f16_bits_to_f32(in.s[b] & 0xffffu)));
+        float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 >> 16) * f16_bits_to_f32(in.s[b] >> 16)));
         fwht128_x2(v0, v1);
         const int k0 = 128 * b + 2 * lane;
         xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = f32_to_f16_bits(v0 * HAD_NORM);
@@ -367,16 +377,57 @@ __device__ __forceinline__ void had_in_row(const void* x, size_t x_off, int x_ki
     }
 }
 
+__device__ __forceinline__ void had_in_row(const void* x, size_t x_off, int x_kind, const uint16_t* suh,
+                                           uint16_t* xa, int m, int nblocks, int nsteps_cap) {
+    RowIn in;
+    had_in_load(x, x_off, suh, nblocks, in);
+    had_in_store(in, x_kind, xa, m, nblocks, nsteps_cap);
+}
+
+// Input rotation of the rows in `mask` (row r of the tile = the r-th set bit)
+// with the step-0 weight tile loaded in between: the first IN_AHEAD rows'
+// inputs are requested before the tile, the rest after it.
+constexpr int IN_AHEAD = 2;
+
+template <int BITS>
+__device__ __forceinline__ void rotate_rows_and_load(const void* x, size_t row_stride, size_t k0, int x_kind,
+                                                     const uint16_t* suh, uint32_t mask, uint16_t* xa, int nblocks,
+                                                     int nsteps_cap, TileRegs<BITS>& first, const u32x4_t* tp) {
+    const int R = __popc(mask);
+    RowIn in[IN_AHEAD];
+    uint32_t rest = mask;
+#pragma unroll
+    for (int i = 0; i < IN_AHEAD; ++i)
+        if (i < R) {
+            const int row = __ffs((int)rest) - 1;
+            rest &= rest - 1u;
+            had_in_load(x, (size_t)row * row_stride + k0, suh, nblocks, in[i]);
+        }
+    load_tile<BITS>(first, tp);
+#pragma unroll
+    for (int i = 0; i < IN_AHEAD; ++i)
+        if (i < R) had_in_store(in[i], x_kind, xa, i, nblocks, nsteps_cap);
+    for (int r = IN_AHEAD; r < R; ++r) {
+        const int row = __ffs((int)rest) - 1;
+        rest &= rest - 1u;
+        had_in_row(x, (size_t)row * row_stride + k0, x_kind, suh, xa, r, nblocks, nsteps_cap);
+    }
+}
+
 // Copies `nblocks` (<= 4) already-rotated fp16 blocks of one row, written by
 // other waves, into the LDS A tile.
 template <bool DEV = true>
-__device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int m, int nblocks, int nsteps_cap) {
+__device__ __forceinline__ void copy_row_load(const uint16_t* src, int nblocks, uint32_t (&v)[HAD_MAX_BLOCKS]) {
     const int lane = threadIdx.x & (WAVE - 1);
-    uint32_t v[HAD_MAX_BLOCKS];
     const uint32_t* sp = reinterpret_cast<const uint32_t*>(src) + lane;
 #pragma unroll
     for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
         if (b < nblocks) v[b] = DEV ? ld_dev(sp + 64 * b) : sp[64 * b];
+}
+
+__device__ __forceinline__ void copy_row_store(const uint32_t (&v)[HAD_MAX_BLOCKS], uint16_t* xa, int m, int nblocks,
+                                               int nsteps_cap) {
+    const int lane = threadIdx.x & (WAVE - 1);
 #pragma unroll
     for (int b = 0; b < HAD_MAX_BLOCKS; ++b) {
         if (b >= nblocks) break;
@@ -384,6 +435,13 @@ __device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int 
         xa[xa_index(m, k0 >> 6, nsteps_cap, k0 & 63)] = (uint16_t)(v[b] & 0xffffu);
         xa[xa_index(m, (k0 + 1) >> 6, nsteps_cap, (k0 + 1) & 63)] = (uint16_t)(v[b] >> 16);
     }
+}
+
+template <bool DEV = true>
+__device__ __forceinline__ void copy_row(const uint16_t* src, uint16_t* xa, int m, int nblocks, int nsteps_cap) {
+    uint32_t v[HAD_MAX_BLOCKS];
+    copy_row_load<DEV>(src, nblocks, v);
+    copy_row_store(v, xa, m, nblocks, nsteps_cap);
 }
 
 // Writes the 16 accumulators of one item (rows < R) as fp32 partials

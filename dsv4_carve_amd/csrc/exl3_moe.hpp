@@ -403,16 +403,11 @@ __device__ __forceinline__ void gateup_partials(const Params& P, int e, int pb, 
     // step-0 weights are in flight while the input rotation runs
     const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]), P.I / 16, k0 / 16,
                                     cb * 16);
-    TileRegs<B> first;
-    load_tile<B>(first, tp);
     const uint16_t* suh = reinterpret_cast<const uint16_t*>((p ? P.usu : P.gsu)[e]);
-    uint32_t rest = mask;
-    for (int r = 0; r < R; ++r) {
-        const int row = __ffs((int)rest) - 1;
-        rest &= rest - 1u;
-        had_in_row(P.x, (size_t)row * P.H + k0, P.x_kind, suh + k0, xa, r, kchunk / 128, NSTEP_CAP);
-    }
+    TileRegs<B> first;
+    rotate_rows_and_load<B>(P.x, P.H, k0, P.x_kind, suh + k0, mask, xa, kchunk / 128, NSTEP_CAP, first, tp);
     __syncthreads();
+    tr(EV_STORED);                  // input rotated (trace builds)
 
     float4_t acc[16];
     mma_steps<B, CB, true>(first, tp, P.I / 16, L.stepsA, xa, NSTEP_CAP, R, acc);
@@ -901,13 +896,23 @@ __global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
         const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[g.e]), P.H / 16, kc * kchunk / 16,
                                         cb * 16);
         TileRegs<B> first;
-        load_tile<B>(first, tp);
         if (P.fuse_act) {
+            load_tile<B>(first, tp);
             down_input_chunk(P, g.e, g.R, pslot, xa, kc * kchunk, kchunk);
         } else {
-            const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
-            for (int r = 0; r < g.R; ++r)
-                copy_row<false>(DI + (size_t)pslot[r] * P.I + kc * kchunk, xa, r, kchunk / 128, NSTEP_CAP);
+            // the first rows' input is requested before the step-0 tile, so
+            // waiting for it (loads complete in issue order) skips the tile
+            const uint16_t* DI = at<uint16_t>(P.scratch, L.DI) + (size_t)kc * kchunk;
+            uint32_t v[IN_AHEAD][HAD_MAX_BLOCKS];
+#pragma unroll
+            for (int i = 0; i < IN_AHEAD; ++i)
+                if (i < g.R) copy_row_load<false>(DI + (size_t)pslot[i] * P.I, kchunk / 128, v[i]);
+            load_tile<B>(first, tp);
+#pragma unroll
+            for (int i = 0; i < IN_AHEAD; ++i)
+                if (i < g.R) copy_row_store(v[i], xa, i, kchunk / 128, NSTEP_CAP);
+            for (int r = IN_AHEAD; r < g.R; ++r)
+                copy_row<false>(DI + (size_t)pslot[r] * P.I, xa, r, kchunk / 128, NSTEP_CAP);
         }
         __syncthreads();
         tr(EV_B_WAITED);
