@@ -849,26 +849,29 @@ __global__ __launch_bounds__(64, 2) void moe_slot_gateup(Params P) {
     tr(EV_A_END);
 }
 
-// Launch 2 (large batches only): item = (slot, column block of I); stores the
-// fp16 down input DI of every row of the slot's expert.
+// Launch 2 (large batches only): item = (slot, column block of I).  A slot
+// that is the pair slot of its (row, expert), i.e. the first slot of its row
+// holding that expert, stores that pair's fp16 down input DI; one row per item,
+// so all rows run at once.
 template <int DUMMY = 0>
 __global__ __launch_bounds__(64) void moe_slot_act(Params P) {
-    __shared__ int16_t pslot[MAX_M];
     const Layout& L = P.L;
-    const int o = blockIdx.x / L.nI, cb = blockIdx.x - (blockIdx.x / L.nI) * L.nI;
-    SlotGroup g;
-    if (!slot_group(P, o, g, pslot)) return;
+    const int s = blockIdx.x / L.nI, cb = blockIdx.x - (blockIdx.x / L.nI) * L.nI;
     const int lane = threadIdx.x & (WAVE - 1);
+    const int s0 = (s / P.topk) * P.topk;
+    const int sl[1] = {s0 + (lane < P.topk ? lane : P.topk)};          // lanes past top-k read nothing
+    int vv[1];
+    P.rt.local_n(sl, s0 + P.topk, P.E, vv);
+    const int v = vv[0];                                               // the row's experts, one per lane
+    const int e = __builtin_amdgcn_readlane(v, s - s0);
+    if (e < 0 || s0 + __builtin_ctzll(__ballot(v == e)) != s) return;
     const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
     uint16_t gsv[4], usv[4], dsu[4];
-    load_half4(gsv, P.gsv[g.e], col);
-    load_half4(usv, P.usv[g.e], col);
-    load_half4(dsu, P.dsu[g.e], col);
+    load_half4(gsv, P.gsv[e], col);
+    load_half4(usv, P.usv[e], col);
+    load_half4(dsu, P.dsu[e], col);
     uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
-    for (int r = 0; r < g.R; ++r) {
-        const int pair = pslot[r];
-        *reinterpret_cast<uint2*>(DI + (size_t)pair * P.I + col) = down_input4<CPOL_PLAIN>(P, pair, col, gsv, usv, dsu);
-    }
+    *reinterpret_cast<uint2*>(DI + (size_t)s * P.I + col) = down_input4<CPOL_PLAIN>(P, s, col, gsv, usv, dsu);
 }
 
 // Launch 3: item = (slot, column block of H, k-chunk of I).  For small
