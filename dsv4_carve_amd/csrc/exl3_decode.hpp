@@ -106,6 +106,17 @@ struct CbConst;
 template <> struct CbConst<CB_MCG>   { static constexpr uint32_t MULT = 0xCBAC1FEDu, ADD = 0u; };
 template <> struct CbConst<CB_3INST> { static constexpr uint32_t MULT = 89226354u, ADD = 64248484u; };
 
+// The same x for an isolated window w (w < 2^16), as one full 32-bit multiply:
+// x = w * MULT + ADD (mod 2^32), then the masked xor.  On gfx950 v_mul_lo_u32
+// issues at the rate of the 16-bit multiplies it replaces, and the masks and
+// shifts that isolate a window issue at twice that rate, so a decoded weight
+// costs fewer VALU cycles than through mcg_bits.
+template <int CB>
+__device__ __forceinline__ uint32_t codebook_word(uint32_t w) {
+    const uint32_t x = w * CbConst<CB>::MULT + CbConst<CB>::ADD;
+    return (x & 0x8fff8fffu) ^ 0x3b603b60u;
+}
+
 // Codebook output as a packed pair of fp16 ADDENDS (lo, hi) whose sum is the
 // weight, for MCG/3INST; for MUL1 the pair is (weight, 0).  GEMV kernels feed
 // both addends to the MFMA against a duplicated activation, so the codebook's

@@ -58,9 +58,21 @@ __device__ __forceinline__ uint32_t win_src(const uint32_t* W) {
     else return win_lo<BITS, S::SRC_T>(W);
 }
 
+// The window of element T alone (bits above it cleared), for the codebooks
+// that multiply it as a 32-bit integer: one field extract when the window lies
+// inside a word (a mask or a shift when it is a word's low or high half), one
+// funnel shift plus a mask when it straddles two.
+template <int BITS, int T>
+__device__ __forceinline__ uint32_t win16(const uint32_t* W) {
+    using S = WinSel<BITS, T>;
+    if constexpr (S::O >= 16) return (W[S::I1] >> (32 - S::O)) & 0xffffu;
+    else return win_lo<BITS, T>(W) & 0xffffu;
+}
+
 template <int BITS, int CB, int T>
 __device__ __forceinline__ uint32_t decode_pair(const uint32_t* W) {
-    return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
+    if constexpr (CB == CB_MUL1) return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
+    else return codebook_word<CB>(win16<BITS, T>(W));
 }
 template <int BITS, int CB, int T>
 __device__ __forceinline__ uint16_t decode_half(const uint32_t* W) {
