@@ -108,9 +108,8 @@ template <> struct CbConst<CB_3INST> { static constexpr uint32_t MULT = 89226354
 
 // The same x for an isolated window w (w < 2^16), as one full 32-bit multiply:
 // x = w * MULT + ADD (mod 2^32), then the masked xor.  On gfx950 v_mul_lo_u32
-// issues at the rate of the 16-bit multiplies it replaces, and the masks and
-// shifts that isolate a window issue at twice that rate, so a decoded weight
-// costs fewer VALU cycles than through mcg_bits.
+// issues at the rate of each 16-bit multiply it replaces, and the masks and
+// shifts that isolate a window issue at twice that rate.
 template <int CB>
 __device__ __forceinline__ uint32_t codebook_word(uint32_t w) {
     const uint32_t x = w * CbConst<CB>::MULT + CbConst<CB>::ADD;

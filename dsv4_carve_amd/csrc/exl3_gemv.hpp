@@ -61,7 +61,12 @@ __device__ __forceinline__ uint32_t win_src(const uint32_t* W) {
 // The window of element T alone (bits above it cleared), for the codebooks
 // that multiply it as a 32-bit integer: one field extract when the window lies
 // inside a word (a mask or a shift when it is a word's low or high half), one
-// funnel shift plus a mask when it straddles two.
+// funnel shift plus a mask when it straddles two.  Used for the widths that do
+// not divide 16: there every straddling window needed its own funnel shift
+// anyway, and the single 32-bit multiply saves an instruction per weight.
+// Widths dividing 16 keep the paired funnels and the 16-bit multiplies that
+// read a window straight from a register half (no isolation, fewer
+// instructions), which latency-bound launches favour.
 template <int BITS, int T>
 __device__ __forceinline__ uint32_t win16(const uint32_t* W) {
     using S = WinSel<BITS, T>;
@@ -71,7 +76,7 @@ __device__ __forceinline__ uint32_t win16(const uint32_t* W) {
 
 template <int BITS, int CB, int T>
 __device__ __forceinline__ uint32_t decode_pair(const uint32_t* W) {
-    if constexpr (CB == CB_MUL1) return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
+    if constexpr (CB == CB_MUL1 || 16 % BITS == 0) return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
     else return codebook_word<CB>(win16<BITS, T>(W));
 }
 template <int BITS, int CB, int T>
