@@ -125,6 +125,18 @@ def test_gemm_other_codebooks(ops, dev, cb):
     assert_close(got, ref, what=f"cb={cb}")
 
 
+@pytest.mark.parametrize("bits,cb", [(1, O.CB_MCG), (5, O.CB_MCG), (7, O.CB_MCG), (8, O.CB_MCG),
+                                     (5, O.CB_3INST), (6, O.CB_3INST), (2, O.CB_3INST)])
+def test_gemm_other_widths(ops, dev, bits, cb):
+    """Widths and codebooks outside the sweep: the one-multiply decode where
+    the width does not divide 16 (5, 6, 7 bits) and the paired-funnel decode
+    where it does (1, 2, 8 bits), for MCG and 3INST."""
+    import torch
+
+    got, ref = _gemm_case(ops, dev, 512, 512, bits, 3, torch.float32, cb=cb)
+    assert_close(got, ref, what=f"K{bits} cb={cb}")
+
+
 def test_reference_call_surfaces(ops, dev):
     """exllamav3-style exl3_gemm and vllm_exl3_c-style exl3_gemv entry points."""
     import torch
