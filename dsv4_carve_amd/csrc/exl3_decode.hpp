@@ -84,8 +84,9 @@ __device__ __forceinline__ uint32_t win_lo(const uint32_t* W) {
 
 // x = (w * MULT + ADD) mod 2^32 for the 16-bit window w held in the low (HI=false)
 // or high (HI=true) half of `src`, then (x & 0x8fff8fff) ^ 0x3b603b60.
-// Two full-rate ops for the multiply (v_mad_u32_u16 + v_pk_mad_u16 with operand
-// selection, no masking of `src` needed) plus the masked xor (v_bitop3_b32).
+// Two ops for the multiply (a 16x16-bit multiply and v_pk_mad_u16, both reading
+// the window from its register half, so `src` needs no masking) plus the
+// masked xor (v_bitop3_b32).
 template <bool HI, uint32_t MULT, uint32_t ADD>
 __device__ __forceinline__ uint32_t mcg_bits(uint32_t src) {
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
