@@ -112,13 +112,15 @@ __device__ __forceinline__ half8_t a_from_words(const u32x4_t& lo, const u32x4_t
 // Software-pipelined by one operand: row block 1's MFMA on the previous B is
 // issued halfway through decoding the next B, so no two MFMAs are adjacent
 // (back to back, the second waits for the matrix pipe).
-template <int BITS, int CB>
+// TWO false: row block 0 only (a tile of at most 16 rows), the same MFMA
+// sequence on acc[0] without block 1's.
+template <int BITS, int CB, bool TWO = true>
 __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[2][2], float4_t (&acc)[2][16]) {
     half8_t A0[4], A1[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         A0[r] = a_from_words(a[0][0], a[0][1], r);
-        A1[r] = a_from_words(a[1][0], a[1][1], r);
+        if constexpr (TWO) A1[r] = a_from_words(a[1][0], a[1][1], r);
     }
     half8_t Bprev;
     static_for<64>([&](auto II) {
@@ -128,7 +130,7 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
         u32x4_t b;
         b[0] = decode_pair<BITS, CB, T0 + 0>(W);
         b[1] = decode_pair<BITS, CB, T0 + 1>(W);
-        if constexpr (i > 0) {
+        if constexpr (TWO && i > 0) {
             constexpr int np = (i - 1) / 4, rp = (i - 1) % 4;
             acc[1][np] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[rp], Bprev, acc[1][np], 0, 0, 0);
         }
@@ -138,7 +140,7 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
         acc[0][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A0[r], B, acc[0][n], 0, 0, 0);
         Bprev = B;
     });
-    acc[1][15] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[3], Bprev, acc[1][15], 0, 0, 0);
+    if constexpr (TWO) acc[1][15] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[3], Bprev, acc[1][15], 0, 0, 0);
 }
 
 // One (tile, 256-column block) of C[rows, N] = A[rows, K] . Wq[K, N], rows of A
@@ -171,22 +173,31 @@ __device__ __forceinline__ void pf_tile(bool valid, int wave, const uint16_t* A,
     // nsteps (64 k-rows each, from k0) is even
     TileRegs<BITS> t0, t1;
     u32x4_t ac[2][2];
-    auto load_a = [&](int s) {
-        ac[0][0] = a0[s * astep]; ac[0][1] = a0[s * astep + 1];
-        ac[1][0] = a1[s * astep]; ac[1][1] = a1[s * astep + 1];
-    };
     // Each step's A loads are issued before the next step's tile loads: the
     // wait for A (needed at once) then leaves the tile prefetch in flight
     // (loads complete in issue order, so A issued after it would wait for it).
-    if (valid) load_tile<BITS>(t0, tp);
-    for (int s = 0; s < (valid ? nsteps : 0); s += 2) {
-        load_a(s);
-        load_tile<BITS>(t1, tp + (s + 1) * tstep);
-        mma_tile2<BITS, CB>(t0.words(), ac, acc);
-        load_a(s + 1);
-        // the last iteration reloads its own step (a valid address, unused)
-        load_tile<BITS>(t0, tp + min(s + 2, nsteps - 1) * tstep);
-        mma_tile2<BITS, CB>(t1.words(), ac, acc);
+    // A tile of at most 16 rows (most tiles under skewed routing) runs a loop
+    // without row block 1's A loads and MFMAs; its rows are the same.
+    auto steps = [&](auto two) {
+        constexpr bool TWO = decltype(two)::value;
+        auto load_a = [&](int s) {
+            ac[0][0] = a0[s * astep]; ac[0][1] = a0[s * astep + 1];
+            if constexpr (TWO) { ac[1][0] = a1[s * astep]; ac[1][1] = a1[s * astep + 1]; }
+        };
+        load_tile<BITS>(t0, tp);
+        for (int s = 0; s < nsteps; s += 2) {
+            load_a(s);
+            load_tile<BITS>(t1, tp + (s + 1) * tstep);
+            mma_tile2<BITS, CB, TWO>(t0.words(), ac, acc);
+            load_a(s + 1);
+            // the last iteration reloads its own step (a valid address, unused)
+            load_tile<BITS>(t0, tp + min(s + 2, nsteps - 1) * tstep);
+            mma_tile2<BITS, CB, TWO>(t1.words(), ac, acc);
+        }
+    };
+    if (valid) {
+        if (nrows > 16) steps(std::true_type{});
+        else steps(std::false_type{});
     }
 
     // epilogue, one wave of the block after the other: both row blocks
@@ -233,7 +244,10 @@ __device__ __forceinline__ void pf_tile(bool valid, int wave, const uint16_t* A,
 // two waves per SIMD); items past the planned tile count or of another width
 // are skipped, and a block with none returns at once.
 template <int BITS, int CB, bool DOWN>
-__global__ __launch_bounds__(2 * WAVE) void pf_gemm_kernel(PfParams P) {
+// Up to 3 bits the kernel fits two waves per SIMD (at most 256 registers);
+// the request keeps the compiler there with both step loops of pf_tile.
+__global__ __launch_bounds__(2 * WAVE) __attribute__((amdgpu_waves_per_eu(BITS <= 3 ? 2 : 1, BITS <= 3 ? 2 : 8)))
+void pf_gemm_kernel(PfParams P) {
     __shared__ float tbuf[PF_RB * COLS];
     const PfLayout& L = P.L;
     const int ncb = (DOWN ? P.H : P.I) / COLS;
