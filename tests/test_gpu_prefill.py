@@ -53,6 +53,19 @@ def test_prefill_against_oracle(small, tokens, routing):
     assert_close(got, small.ref(x, ids, w), what=f"prefill {routing} T={tokens}")
 
 
+@pytest.mark.parametrize("tokens", [9, 70])
+def test_prefill_other_widths(dev, tokens):
+    """Experts at 1, 5, 6, 7 and 8 bits: one GEMM launch per width, the
+    one-multiply decode at 5, 6 and 7 bits, tiles with and without a second
+    16-row block (70 tokens over 8 experts gives tiles past 16 rows)."""
+    print(f"prefill other widths tokens={tokens}", flush=True)
+    layer = Layer(dev, 8, 512, 256, [5, 6, 7, 1, 8, 5, 7, 6], seed=31)
+    ids, w = synth.zipf_routing(tokens, 8, 6, seed=830 + tokens)
+    x = synth.activations(tokens, 512, seed=831 + tokens)
+    got = run_prefill(layer, x, ids, w).cpu().numpy()
+    assert_close(got, layer.ref(x, ids, w), what=f"prefill widths 1/5/6/7/8 T={tokens}")
+
+
 def test_prefill_hot_expert_many_tiles(small):
     """Every token routes to expert 3 (4 tiles of 32 rows + a partial one) and
     to one other expert; duplicate ids within a row count twice."""
