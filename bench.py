@@ -439,6 +439,48 @@ def time_stack(dev, rows, steps, warmup):
     return us, nbytes
 
 
+def time_read_ceiling(dev, gib: int = 2, reps: int = 10) -> dict:
+    """Achievable cold HBM read rate: the probe kernel (csrc/exl3_probe.hip)
+    streams a `gib` GiB buffer once per run, after a 1 GiB read of another
+    buffer has flushed the 256 MB MALL; p50/max over `reps` runs for a few
+    grid sizes.  This is the ceiling the decode kernels' weight streams are
+    compared with, beside the nominal 8 TB/s."""
+    import ctypes
+
+    import torch
+    from dsv4_carve_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_LIB)
+    lib.exl3_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.exl3_probe_read.restype = ctypes.c_int
+    threads = int(lib.exl3_probe_threads())
+    nbytes = gib << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=dev)
+    flush = torch.ones((1 << 30) // 4, dtype=torch.int32, device=dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    stream = int(torch.cuda.current_stream(dev).cuda_stream)
+    res = {}
+    for per_cu in (4, 8, 16):
+        blocks = cus * per_cu
+        sink = torch.empty(blocks * threads, dtype=torch.int32, device=dev)
+        times = []
+        for _ in range(reps + 1):
+            assert lib.exl3_probe_read(flush.data_ptr(), flush.numel() * 4, sink.data_ptr(), blocks, stream) == 0
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            assert lib.exl3_probe_read(buf.data_ptr(), nbytes, sink.data_ptr(), blocks, stream) == 0
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) * 1e-3)
+        rates = sorted(nbytes / t / 1e9 for t in times[1:])
+        res[f"{per_cu}_blocks_per_cu"] = {"p50_GBps": round(rates[len(rates) // 2], 1), "max_GBps": round(rates[-1], 1)}
+    best = max(v["p50_GBps"] for v in res.values())
+    del buf, flush
+    torch.cuda.empty_cache()
+    return {"buffer_GiB": gib, "runs": reps, "best_p50_GBps": best, "frac_of_8TBps": round(best / HBM_PEAK_GBS, 4),
+            **res}
+
+
 CPU_SAMPLE = 10          # experts per bit width timed on the CPU
 
 
@@ -476,7 +518,7 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
     }
 
 
-EXTRA_LEGS = ("sweep", "tp8", "prefill", "stack", "dense", "fan", "glue")
+EXTRA_LEGS = ("ceiling", "sweep", "tp8", "prefill", "stack", "dense", "fan", "glue")
 
 
 def main() -> int:
@@ -518,6 +560,9 @@ def main() -> int:
     print(f"[bench] rows={a.rows}: {us:.1f} us/layer, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
 
     extra = {}
+    if "ceiling" in legs:
+        extra["hbm_read_ceiling"] = time_read_ceiling(dev)
+        print(f"[bench] read ceiling: {extra['hbm_read_ceiling']}", file=sys.stderr, flush=True)
     if "sweep" in legs:
         sweep = {}
         for m in (1, 2, 4, 8, 16):

@@ -22,6 +22,7 @@ EXPORTS = (
     "exl3_gemm_group",
     "exl3_moe_scratch_bytes",
     "exl3_moe_max_rows",
+    "exl3_moe_error_offset",
     "exl3_moe_decode",
     "exl3_moe_decode_routed",
     "exl3_moe_info",
@@ -47,6 +48,7 @@ _SIGS = {
     "exl3_gemm_group": ([_P, _L, _L, _L, _P, _P, _P, _P, _P, _I, _P, _I, _P, _L, _P], _I),
     "exl3_moe_scratch_bytes": ([_L, _L, _L], _L),
     "exl3_moe_max_rows": ([], _I),
+    "exl3_moe_error_offset": ([], _L),
     "exl3_moe_decode": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,
                          _P, _P, _P, _P, _P, _P, _P, _P, _P,
                          _P, _P, _P, _I, _I, _I, _F, _P, _L, _P], _I),

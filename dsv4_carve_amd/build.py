@@ -13,6 +13,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libexl3_amd.so")
+# The HBM read-ceiling probe the benchmark times beside the decode kernels
+# (not part of the decode path's ABI, so a library of its own).
+PROBE_LIB = os.path.join(HERE, "libexl3_probe.so")
 ARCH = os.environ.get("EXL3_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -62,8 +65,14 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
     os.replace(tmp, LIB)
+    tmp = PROBE_LIB + ".tmp"
+    cmd = [HIPCC, *COMMON, "-shared", "-o", tmp, os.path.join(CSRC, "exl3_probe.hip")]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("probe build failed:\n" + r.stderr)
+    os.replace(tmp, PROBE_LIB)
     if verbose:
-        print(f"built {LIB} from {len(objs)} objects", file=sys.stderr)
+        print(f"built {LIB} from {len(objs)} objects, and {PROBE_LIB}", file=sys.stderr)
     return LIB
 
 

@@ -91,7 +91,7 @@ __device__ __forceinline__ uint16_t decode_half(const uint32_t* W) {
 // first 2*BITS vectors are loaded and decoded.
 template <int CAP>
 struct TileBuf {
-    u32x4_t v[CAP];
+    u32x4_t v[CAP > 0 ? CAP : 1];       // CAP 0: the buffer of a skipped item, never loaded
     __device__ __forceinline__ const uint32_t* words() const {
         return reinterpret_cast<const uint32_t*>(v);
     }
@@ -126,6 +126,11 @@ __device__ __forceinline__ half8_t a_operand(const uint16_t* xa, int m, int s, i
     d[2] = __builtin_amdgcn_perm(v.y, v.y, 0x01000100u);
     d[3] = __builtin_amdgcn_perm(v.y, v.y, 0x03020302u);
     return __builtin_bit_cast(half8_t, d);
+}
+
+__device__ __forceinline__ void zero_acc(float4_t (&acc)[16]) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 }
 
 // Decodes all 256 weights of the lane's tile and accumulates 64 MFMAs into acc.

@@ -113,11 +113,16 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     return L;
 }
 
+// Bits of the error word (Ctrl::error).  The kernels only set bits; the word is
+// zero in a freshly zeroed scratch and the host reads and clears it.
+constexpr int ERR_WIDTH = 1;     // an expert width outside the kernel's instance
+constexpr int ERR_WAIT = 2;      // a bounded wait gave up (ticket kernel)
+
 // Control words at the head of the scratch buffer.  The two counters every
 // wave updates sit 4 KB apart and away from the words that are only read.
 struct Ctrl {
     int epoch;
-    int error;                     // nonzero: a wait gave up (see wait_flag)
+    int error;                     // ERR_* bits (see dispatch_bits and wait_flag)
     int pad0[1022];
     int later;                     // down and gather items, in order (see draw_ticket)
     int pad1[1023];
@@ -278,7 +283,7 @@ __device__ __forceinline__ void wait_flag(int* flag, int target, int* err) {
     if (threadIdx.x == 0) {
         for (uint32_t n = 0; __hip_atomic_load(flag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != target; ++n) {
             if (n == (1u << 24)) {
-                __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_or(err, ERR_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
             __builtin_amdgcn_s_sleep(EXL3_POLL_SLEEP);
@@ -400,18 +405,21 @@ __device__ __forceinline__ void gateup_partials(const Params& P, int e, int pb, 
     const int kchunk = L.stepsA * STEP_K;
     const int k0 = kc * kchunk;
 
-    // step-0 weights are in flight while the input rotation runs
-    const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]), P.I / 16, k0 / 16,
-                                    cb * 16);
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>((p ? P.usu : P.gsu)[e]);
-    TileRegs<B> first;
-    rotate_rows_and_load<B>(P.x, P.H, k0, P.x_kind, suh + k0, mask, xa, kchunk / 128, NSTEP_CAP, first, tp);
-    __syncthreads();
-    tr(EV_STORED);                  // input rotated (trace builds)
-
     float4_t acc[16];
-    mma_steps<B, CB, true>(first, tp, P.I / 16, L.stepsA, xa, NSTEP_CAP, R, acc);
-    tr(EV_A_MMA);
+    if constexpr (B == 0) {
+        zero_acc(acc);              // a width outside the instance (see dispatch_bits)
+    } else {
+        // step-0 weights are in flight while the input rotation runs
+        const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>((p ? P.ut : P.gt)[e]), P.I / 16, k0 / 16,
+                                        cb * 16);
+        const uint16_t* suh = reinterpret_cast<const uint16_t*>((p ? P.usu : P.gsu)[e]);
+        TileRegs<B> first;
+        rotate_rows_and_load<B>(P.x, P.H, k0, P.x_kind, suh + k0, mask, xa, kchunk / 128, NSTEP_CAP, first, tp);
+        __syncthreads();
+        tr(EV_STORED);                  // input rotated (trace builds)
+        mma_steps<B, CB, true>(first, tp, P.I / 16, L.stepsA, xa, NSTEP_CAP, R, acc);
+        tr(EV_A_MMA);
+    }
 
     float* PA = at<float>(P.scratch, L.PA);
     store_partials<DEV>(acc, PA + ((size_t)((rowmap ? 0 : pb) * 2 + p) * L.SA + kc) * P.I + cb * COLS,
@@ -482,13 +490,16 @@ __device__ __forceinline__ void down_partials(const Params& P, int pb, int R, ui
     const Layout& L = P.L;
     const int kchunk = L.stepsB * STEP_K;
     const int k0 = kc * kchunk;
-    const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
-    for (int r = 0; r < R; ++r) copy_row<DEV>(DI + (size_t)(pb + r) * P.I + k0, xa, r, kchunk / 128, NSTEP_CAP);
-    __syncthreads();
-
     float4_t acc[16];
-    mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
-    tr(EV_B_MMA);
+    if constexpr (B == 0) {
+        zero_acc(acc);
+    } else {
+        const uint16_t* DI = at<uint16_t>(P.scratch, L.DI);
+        for (int r = 0; r < R; ++r) copy_row<DEV>(DI + (size_t)(pb + r) * P.I + k0, xa, r, kchunk / 128, NSTEP_CAP);
+        __syncthreads();
+        mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
+        tr(EV_B_MMA);
+    }
 
     float* PB = at<float>(P.scratch, L.PB);
     store_partials<DEV>(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS,
@@ -549,7 +560,7 @@ __device__ void item_b_body(const Params& P, const Plan& pl, uint16_t* xa, int g
 
     const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[e]), P.H / 16, k0 / 16, cb * 16);
     TileRegs<B> first;
-    load_tile<B>(first, tp);
+    if constexpr (B != 0) load_tile<B>(first, tp);
 
     // wait for the gate/up column blocks this chunk reads
     for (int c = k0 / COLS; c <= (k0 + kchunk - 1) / COLS; ++c)
@@ -617,8 +628,11 @@ __device__ void item_g(const Params& P, const Plan& pl, int t, int epoch, Tracer
     tr(EV_GATHER_END);
 }
 
-// Width dispatch: runs body<B> for the instantiated width B == bits; a width
-// outside MASK (the host checks against it) sets the error word and skips.
+// Width dispatch: runs body<B> for the instantiated width B == bits.  A width
+// outside MASK (the host rejects such tables before launch) sets bit 0 of the
+// error word and runs body<0>: the item writes zero partials and still takes
+// part in every counter and flag, so the layer completes with that expert's
+// contribution zero and the scratch's control words stay consistent.
 template <uint32_t MASK, typename F>
 __device__ __forceinline__ void dispatch_bits(int bits, int* err, F&& body) {
     bool done = false;
@@ -631,7 +645,10 @@ __device__ __forceinline__ void dispatch_bits(int bits, int* err, F&& body) {
             }
         }
     });
-    if (!done && threadIdx.x == 0) atomicOr(err, 1);
+    if (!done) {
+        if (threadIdx.x == 0) atomicOr(err, ERR_WIDTH);
+        body(std::integral_constant<int, 0>{});
+    }
 }
 
 template <uint32_t MASK, int CB>
@@ -896,32 +913,36 @@ __global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
     dispatch_bits<MASK>(g.bits, &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
         constexpr int B = decltype(BI)::value;
         const int kchunk = L.stepsB * STEP_K;
-        const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[g.e]), P.H / 16, kc * kchunk / 16,
-                                        cb * 16);
-        TileRegs<B> first;
-        if (P.fuse_act) {
-            load_tile<B>(first, tp);
-            down_input_chunk(P, g.e, g.R, pslot, xa, kc * kchunk, kchunk);
-        } else {
-            // the first rows' input is requested before the step-0 tile, so
-            // waiting for it (loads complete in issue order) skips the tile
-            const uint16_t* DI = at<uint16_t>(P.scratch, L.DI) + (size_t)kc * kchunk;
-            uint32_t v[IN_AHEAD][HAD_MAX_BLOCKS];
-#pragma unroll
-            for (int i = 0; i < IN_AHEAD; ++i)
-                if (i < g.R) copy_row_load<false>(DI + (size_t)pslot[i] * P.I, kchunk / 128, v[i]);
-            load_tile<B>(first, tp);
-#pragma unroll
-            for (int i = 0; i < IN_AHEAD; ++i)
-                if (i < g.R) copy_row_store(v[i], xa, i, kchunk / 128, NSTEP_CAP);
-            for (int r = IN_AHEAD; r < g.R; ++r)
-                copy_row<false>(DI + (size_t)pslot[r] * P.I, xa, r, kchunk / 128, NSTEP_CAP);
-        }
-        __syncthreads();
-        tr(EV_B_WAITED);
         float4_t acc[16];
-        mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, g.R, acc);
-        tr(EV_B_MMA);
+        if constexpr (B == 0) {
+            zero_acc(acc);
+        } else {
+            const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[g.e]), P.H / 16, kc * kchunk / 16,
+                                            cb * 16);
+            TileRegs<B> first;
+            if (P.fuse_act) {
+                load_tile<B>(first, tp);
+                down_input_chunk(P, g.e, g.R, pslot, xa, kc * kchunk, kchunk);
+            } else {
+                // the first rows' input is requested before the step-0 tile, so
+                // waiting for it (loads complete in issue order) skips the tile
+                const uint16_t* DI = at<uint16_t>(P.scratch, L.DI) + (size_t)kc * kchunk;
+                uint32_t v[IN_AHEAD][HAD_MAX_BLOCKS];
+#pragma unroll
+                for (int i = 0; i < IN_AHEAD; ++i)
+                    if (i < g.R) copy_row_load<false>(DI + (size_t)pslot[i] * P.I, kchunk / 128, v[i]);
+                load_tile<B>(first, tp);
+#pragma unroll
+                for (int i = 0; i < IN_AHEAD; ++i)
+                    if (i < g.R) copy_row_store(v[i], xa, i, kchunk / 128, NSTEP_CAP);
+                for (int r = IN_AHEAD; r < g.R; ++r)
+                    copy_row<false>(DI + (size_t)pslot[r] * P.I, xa, r, kchunk / 128, NSTEP_CAP);
+            }
+            __syncthreads();
+            tr(EV_B_WAITED);
+            mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, g.R, acc);
+            tr(EV_B_MMA);
+        }
         store_partials<false>(acc, at<float>(P.scratch, L.PB) + (size_t)kc * P.H + cb * COLS, (size_t)L.SB * P.H,
                               g.R, COLS, reinterpret_cast<float*>(xa), pslot);
     });

@@ -4,6 +4,7 @@
 //   exl3_moe_max_rows       <- lna2_moe_max_rows       :484
 //   exl3_moe_info           <- lna2_moe_info           :494-505
 #include <math.h>
+#include <stddef.h>
 #include <stdlib.h>
 
 #include "exl3_moe.hpp"
@@ -97,6 +98,11 @@ int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t top
 }
 
 int exl3_moe_max_rows(void) { return MAX_M; }
+
+int64_t exl3_moe_error_offset(void) {
+    static_assert(offsetof(Ctrl, error) == 4, "error word at byte 4 of the control block");
+    return layout(COLS, COLS, 1).ctrl + (int64_t)offsetof(Ctrl, error);
+}
 
 int exl3_moe_info(int64_t* out, int n) {
     clear_error();

@@ -34,6 +34,11 @@ constexpr int PF_MAX_EXPERTS = 2048;
 constexpr int PF_MAX_TOPK = 9;
 constexpr int PF_MAX_PAIRS = 65536;
 
+// Words of the meta block at the head of the scratch.  The error word sits at
+// byte 4, as in the decode scratch; the plan launch rewrites it every call.
+constexpr int PF_META_PAIRS = 0, PF_META_ERROR = 1, PF_META_TILES = 2;
+constexpr int PF_ERR_WIDTH = 1;          // an expert width outside bits_mask was routed (it contributed nothing)
+
 struct PfLayout {
     int64_t meta, eoff, toff, tile_e, tile_r0, tile_n, pair_slot, pos, Xh, GU, AD, D, total;
     int64_t max_tiles;
@@ -84,6 +89,7 @@ struct PfParams {
     const int64_t* dt; const int64_t* dsu; const int64_t* dsv;
     Route rt;                            // top-k ids / weights / expert map
     const int8_t* ebits; int bits;
+    uint32_t mask;                       // widths with a GEMM launch (bit b = b-bit experts)
     float limit;
     char* scratch;
     PfLayout L;
@@ -257,7 +263,7 @@ void pf_gemm_kernel(PfParams P) {
     const int item = 2 * blockIdx.x + wave;
     const int t = item / per_tile;
     int rem = item - t * per_tile;
-    bool valid = t < pat<int>(P.scratch, L.meta)[1];
+    bool valid = t < pat<int>(P.scratch, L.meta)[PF_META_TILES];
     const int e = valid ? pat<int>(P.scratch, L.tile_e)[t] : 0;
     valid = valid && (P.ebits ? (int)P.ebits[e] : P.bits) == BITS;
     if (!__syncthreads_or(valid)) return;

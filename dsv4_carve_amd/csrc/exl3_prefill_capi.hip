@@ -32,17 +32,31 @@ __device__ __forceinline__ void wave0_scan(int* v, int n, int* total) {
     if (lane == 0) *total = carry;
 }
 
+// Local expert of slot s, or -1.  An expert whose width is outside the
+// call's bits_mask (no GEMM launch covers it) is routed nowhere, so it
+// contributes nothing, and sets `bad`.
+__device__ __forceinline__ int pf_local(const PfParams& P, int s, int* bad) {
+    const int e = P.rt.local(s, P.E);
+    if (e >= 0 && P.ebits && !((P.mask >> (P.ebits[e] & 31)) & 1u)) {
+        *bad = 1;
+        return -1;
+    }
+    return e;
+}
+
 __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     __shared__ int cnt[PF_MAX_EXPERTS + 1];
     __shared__ int off[PF_MAX_EXPERTS + 1];
     __shared__ int tof[PF_MAX_EXPERTS + 1];
     __shared__ int totals[2];
+    __shared__ int bad;
     const PfLayout& L = P.L;
     const int tid = threadIdx.x, nt = blockDim.x;
     for (int e = tid; e < P.E; e += nt) cnt[e] = 0;
+    if (tid == 0) bad = 0;
     __syncthreads();
     for (int s = tid; s < P.P; s += nt) {
-        const int e = P.rt.local(s, P.E);
+        const int e = pf_local(P, s, &bad);
         if (e >= 0) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
@@ -72,8 +86,9 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     if (tid == 0) {
         eoff[P.E] = totals[0];
         toff[P.E] = totals[1];
-        pat<int>(P.scratch, L.meta)[0] = totals[0];
-        pat<int>(P.scratch, L.meta)[1] = totals[1];
+        pat<int>(P.scratch, L.meta)[PF_META_PAIRS] = totals[0];
+        pat<int>(P.scratch, L.meta)[PF_META_ERROR] = bad ? PF_ERR_WIDTH : 0;
+        pat<int>(P.scratch, L.meta)[PF_META_TILES] = totals[1];
     }
     __syncthreads();
     // place the pairs: any order within an expert (a row's result does not
@@ -83,7 +98,7 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     int* pair_slot = pat<int>(P.scratch, L.pair_slot);
     int* pos = pat<int>(P.scratch, L.pos);
     for (int s = tid; s < P.P; s += nt) {
-        const int e = P.rt.local(s, P.E);
+        const int e = pf_local(P, s, &bad);
         int p = -1;
         if (e >= 0) {
             p = atomicAdd(&cnt[e], 1);
@@ -98,7 +113,7 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
 __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     const PfLayout& L = P.L;
     const int p = blockIdx.x >> 1, proj = blockIdx.x & 1;
-    if (p >= pat<int>(P.scratch, L.meta)[0]) return;
+    if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
     const int lane = threadIdx.x;
     const int s = pat<int>(P.scratch, L.pair_slot)[p];
     const int tok = s / P.topk, e = P.rt.local(s, P.E);
@@ -124,7 +139,7 @@ __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
 __global__ __launch_bounds__(64) void pf_act_kernel(PfParams P) {
     const PfLayout& L = P.L;
     const int p = blockIdx.x;
-    if (p >= pat<int>(P.scratch, L.meta)[0]) return;
+    if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
     const int lane = threadIdx.x;
     const int e = P.rt.local(pat<int>(P.scratch, L.pair_slot)[p], P.E);
     const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I;
@@ -212,6 +227,8 @@ static int launch_widths(const PfParams& P, uint32_t mask, int codebook, bool do
 using namespace exl3;
 using namespace exl3::prefill;
 
+static_assert(PF_META_ERROR * 4 == 4, "prefill error word at byte 4, as in the decode scratch");
+
 extern "C" {
 
 int64_t exl3_moe_prefill_scratch_bytes(int64_t tokens, int64_t hidden, int64_t intermediate, int64_t topk,
@@ -263,7 +280,7 @@ static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, 
     P.ut = up_trellis; P.usu = up_suh; P.usv = up_svh;
     P.dt = down_trellis; P.dsu = down_suh; P.dsv = down_svh;
     P.rt = rt;
-    P.ebits = expert_bits; P.bits = bits;
+    P.ebits = expert_bits; P.bits = bits; P.mask = mask;
     P.limit = swiglu_limit;
     P.scratch = reinterpret_cast<char*>(scratch);
     P.L = pf_layout(P.P, hidden, intermediate, n_experts);

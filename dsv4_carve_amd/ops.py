@@ -56,10 +56,13 @@ class _ScratchPool:
 
     The kernels' counters must be zero before the first launch and are left
     zero by every launch (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296 is the
-    same contract), so a buffer is zeroed exactly once, when it is created."""
+    same contract), so a buffer is zeroed exactly once, when it is created.
+    A buffer that a larger one replaces is kept alive until the process ends:
+    a graph captured while it was current keeps launching on its address."""
 
     def __init__(self):
         self._bufs: dict[tuple[int, str], torch.Tensor] = {}
+        self._retired: list[torch.Tensor] = []
         self._lock = threading.Lock()
 
     def get(self, device: torch.device, purpose: str, nbytes: int) -> torch.Tensor:
@@ -72,13 +75,18 @@ class _ScratchPool:
                     raise RuntimeError(
                         f"exl3 {purpose} scratch was not prewarmed for device {idx} "
                         f"(need {nbytes} bytes during graph capture)")
-                torch.cuda.synchronize(device)     # the old buffer may still be in use
+                if buf is not None:
+                    self._retired.append(buf)
                 buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 
+    def current(self, device: torch.device, purpose: str) -> torch.Tensor | None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return self._bufs.get((int(idx), purpose))
+
     def resident_bytes(self) -> int:
-        return sum(int(b.numel()) for b in self._bufs.values())
+        return sum(int(b.numel()) for b in self._bufs.values()) + sum(int(b.numel()) for b in self._retired)
 
 
 SCRATCH = _ScratchPool()
@@ -345,6 +353,55 @@ def moe_max_rows() -> int:
     return int(_lib.load().exl3_moe_max_rows())
 
 
+ERR_WIDTH = 1      # an expert width outside bits_mask was routed (its contribution was zero)
+ERR_WAIT = 2       # a bounded wait of the ticket schedule gave up
+
+
+def moe_error(scratch: torch.Tensor, clear: bool = True) -> int:
+    """The error word of a decode or prefill scratch (ERR_* bits; 0 = none).
+    Synchronises with the device; call it outside captured regions.  A decode
+    scratch keeps bits until cleared; a prefill scratch reports its last call."""
+    off = int(_lib.load().exl3_moe_error_offset())
+    word = scratch[off:off + 4]
+    value = int(word.view(torch.int32).item())
+    if clear and value:
+        word.zero_()
+    return value
+
+
+def moe_scratch_errors(device: torch.device, clear: bool = True) -> dict[str, int]:
+    """Error words of this device's shared decode and prefill scratch buffers."""
+    out = {}
+    for purpose in ("moe", "moe_prefill"):
+        buf = SCRATCH.current(device, purpose)
+        if buf is not None:
+            out[purpose] = moe_error(buf, clear)
+    return out
+
+
+_WIDTHS_CHECKED: dict[tuple, bool] = {}
+
+
+def check_expert_bits(expert_bits: torch.Tensor, bits_mask: int) -> None:
+    """Every width in the per-expert table must be in bits_mask, the set the
+    kernel instance is chosen for (the role of the reference's TORCH_CHECKs on
+    K, lna_moe_ticket.cu:516-553).  Read from the device once per table
+    version; inside a graph capture an unchecked table is left to the
+    kernels' error word."""
+    key = (expert_bits.device.index, int(expert_bits.data_ptr()), int(expert_bits.numel()),
+           int(expert_bits._version), int(bits_mask))
+    if key in _WIDTHS_CHECKED:
+        return
+    if torch.cuda.is_current_stream_capturing():
+        return
+    widths = {int(b) for b in expert_bits.cpu().tolist()}
+    bad = sorted(b for b in widths if not (1 <= b <= 8 and (int(bits_mask) >> b) & 1))
+    _check(not bad, f"expert_bits holds widths {bad} outside bits_mask 0x{int(bits_mask):x}")
+    if len(_WIDTHS_CHECKED) > 4096:
+        _WIDTHS_CHECKED.clear()
+    _WIDTHS_CHECKED[key] = True
+
+
 def moe_scratch_bytes(hidden: int, intermediate: int, topk: int) -> int:
     return int(_lib.check(_lib.load().exl3_moe_scratch_bytes(hidden, intermediate, topk)))
 
@@ -416,6 +473,7 @@ def moe_decode(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Ten
         _check(expert_bits.is_cuda and expert_bits.dtype == torch.int8 and expert_bits.numel() == n_experts,
                "expert_bits must be int8 [experts] on the device")
         _check(bits_mask is not None and bits_mask > 0, "bits_mask is required with expert_bits")
+        check_expert_bits(expert_bits, bits_mask)
         b, mask = 0, int(bits_mask)
     else:
         _check(bits is not None and 1 <= int(bits) <= 8, "bits must be in 1..8")
@@ -515,6 +573,7 @@ def moe_prefill(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Te
         _check(expert_bits.is_cuda and expert_bits.dtype == torch.int8 and expert_bits.numel() == n_experts,
                "expert_bits must be int8 [experts] on the device")
         _check(bits_mask is not None and bits_mask > 0, "bits_mask is required with expert_bits")
+        check_expert_bits(expert_bits, bits_mask)
         b, mask = 0, int(bits_mask)
     else:
         _check(bits is not None and 1 <= int(bits) <= 8, "bits must be in 1..8")

@@ -192,17 +192,31 @@ def execute_exl3_linear(x, trellis, suh, svh, mcg=None, mul1=None, *, out_dtype=
 #
 # LNA_EXL3_DENSE_GROUP (recipe-lna/vllm_exl3_exl3.py.lna:121-135): 0 = off
 # (every shard its own call), 1 = T0 (the EXL3 shards of one module, which read
-# the same input, in one fused call), 2 = T1 (the reference's cross-module fans
-# with cached outputs; not built here: a module in a fan falls back to its own
-# T0 group with the reference's "T1 fan is not complete" decline).
+# the same input, in one fused call), 2 = T1 (cross-module fans: the modules of
+# one attention layer that read the same tensor run as one fused call, issued
+# by the first of them to be called; the later ones take their outputs from
+# that call, recipe-lna/vllm_exl3_exl3.py.lna:183-545, 616-802).
+#
+# The two T1 fans of a DSV4 attention layer:
+#   h-fan: fused_wqa_wkv (role qkv), compressor.fused_wkv_wgate (compressor),
+#          indexer.compressor.fused_wkv_wgate (indexer_compressor) -- all read
+#          the layer's hidden state; complete once qkv and one more are loaded;
+#   q-fan: wq_b (qb) and indexer.wq_b (indexer_qb) -- both read the q latent.
 
 DENSE_GROUP_MAX_MATRICES = 8
-_DENSE_GROUP_STATS: dict[str, int] = {"t0_active": 0, "t1_active": 0, "fallback_total": 0, "prewarm_groups": 0}
+DENSE_GROUP_MAX_ROWS = 16
+_DENSE_GROUP_STATS: dict[str, int] = {"t0_active": 0, "t1_active": 0, "t1_cached": 0, "fallback_total": 0,
+                                      "prewarm_groups": 0}
 _DENSE_GROUP_FALLBACK_COUNTS: dict[str, int] = {}
 _DENSE_GROUP_CALL_COUNTS: dict[int, int] = {1: 0, 2: 0}
 _DENSE_GROUP_ACTIVE_LOGGED: set[str] = set()
-_DENSE_FAN_SUFFIXES = (".fused_wqa_wkv", ".indexer.compressor.fused_wkv_wgate", ".compressor.fused_wkv_wgate",
-                       ".indexer.wq_b", ".wq_b")
+_DENSE_FAN_ROLES = ((".indexer.compressor.fused_wkv_wgate", "h", "indexer_compressor"),
+                    (".compressor.fused_wkv_wgate", "h", "compressor"),
+                    (".fused_wqa_wkv", "h", "qkv"),
+                    (".indexer.wq_b", "q", "indexer_qb"),
+                    (".wq_b", "q", "qb"))
+_DENSE_FAN_ORDER = {"h": ("qkv", "compressor", "indexer_compressor"), "q": ("qb", "indexer_qb")}
+_DENSE_FAN_REGISTRY: dict[str, dict[str, Any]] = {}     # group id -> role -> weakref(module)
 
 
 def dense_group_mode() -> int:
@@ -243,14 +257,23 @@ def _dense_group_active(mode: int, group_id: str) -> None:
 
 def dense_group_stats() -> dict[str, Any]:
     return {**_DENSE_GROUP_STATS, "fallbacks": dict(_DENSE_GROUP_FALLBACK_COUNTS),
-            "active_groups": sorted(_DENSE_GROUP_ACTIVE_LOGGED)}
+            "active_groups": sorted(_DENSE_GROUP_ACTIVE_LOGGED), "call_counts": dense_group_call_counts()}
 
 
 def dense_group_call_counts() -> dict[int, int]:
+    """Fused calls issued: T0 groups (1) and T1 fans (2)."""
     return dict(_DENSE_GROUP_CALL_COUNTS)
 
 
 def reset_dense_group_state() -> None:
+    """Clears the counters, the T1 registry and every fan's cached generation
+    (tests; modules keep their T0 groups)."""
+    for entries in _DENSE_FAN_REGISTRY.values():
+        for ref in entries.values():
+            module = ref()
+            if module is not None and hasattr(module, "_exl3_dense_fan"):
+                module._exl3_dense_fan = None
+    _DENSE_FAN_REGISTRY.clear()
     for key in _DENSE_GROUP_STATS:
         _DENSE_GROUP_STATS[key] = 0
     _DENSE_GROUP_FALLBACK_COUNTS.clear()
@@ -278,64 +301,267 @@ def _dense_group_members(linears: list, group_id: str) -> dict:
         raise ValueError(f"a fused group needs k and every n to be multiples of 128, k={k}, ns={ns}")
     if len(ns) > DENSE_GROUP_MAX_MATRICES:
         raise ValueError("dense group exceeds the matrix capacity")
+    if len({lin.trellis.device for lin in linears}) != 1:
+        raise ValueError("members live on different devices")
     return {"group_id": group_id, "members": [(lin.trellis, lin.suh, lin.svh) for lin in linears],
-            "codebook": linears[0].codebook, "k": k, "ns": ns}
+            "codebook": linears[0].codebook, "k": k, "ns": ns, "device": linears[0].trellis.device}
+
+
+def _dense_prewarm_rows() -> tuple[int, ...]:
+    """LNA_EXL3_PREWARM_ROWS (default 1,2,4,8,16): row counts whose scratch is
+    reserved before graph capture (recipe-lna/vllm_exl3_exl3.py.lna:352-369)."""
+    rows = []
+    for value in os.environ.get("LNA_EXL3_PREWARM_ROWS", "1,2,4,8,16").split(","):
+        if not value.strip():
+            continue
+        try:
+            row = int(value)
+        except ValueError:
+            _dense_group_fallback("prewarm", f"invalid row bucket {value!r}")
+            continue
+        if 1 <= row <= DENSE_GROUP_MAX_ROWS:
+            rows.append(row)
+        else:
+            _dense_group_fallback("prewarm", f"row bucket {row} outside 1..{DENSE_GROUP_MAX_ROWS}")
+    return tuple(dict.fromkeys(rows))
+
+
+def _prewarm_group(group: dict, outs_for=None) -> bool:
+    """Runs the fused call once per prewarm row count (and at the largest row
+    count the group runs, so every later row count fits) so the shared scratch
+    exists before any capture.  False (logged) on failure."""
+    device = group["device"]
+    if device.type != "cuda":
+        return False
+    try:
+        for rows in sorted(set(_dense_prewarm_rows()) | {DENSE_GROUP_MAX_ROWS}):
+            x = torch.zeros((rows, group["k"]), dtype=torch.float16, device=device)
+            ops.gemm_group(x, group["members"], group["codebook"], torch.float32,
+                           outs=None if outs_for is None else outs_for(rows))
+        _DENSE_GROUP_STATS["prewarm_groups"] += 1
+        return True
+    except Exception as exc:
+        _dense_group_fallback("prewarm", repr(exc), group["group_id"])
+        return False
 
 
 def build_exl3_dense_group(module) -> None:
     """Build the module's group descriptor once after load (and before graph
     capture).  Sentinels on ``_exl3_dense_group`` as in the reference
     (recipe-lna/vllm_exl3_exl3.py.lna:508-545): missing = not yet checked,
-    None = checked and declined, dict = ready."""
+    None = checked and declined, dict = ready.  In T1 mode the module also
+    joins its layer's fan, if its name makes it a fan member."""
     if not dense_group_enabled() or hasattr(module, "_exl3_dense_group"):
         return
     linears = [lin for lin in getattr(module, "_exl3_linears", None) or [] if lin is not None]
-    if getattr(module, "_exl3_linear_bf16_shards", []) or len(linears) < 2:
-        module._exl3_dense_group = None
+    if getattr(module, "_exl3_linear_bf16_shards", []):
+        module._exl3_dense_group = None            # never fused: mixed bf16 shards
         return
-    group_id = f"local:{getattr(module, 'prefix', '?')}:{id(module)}"
-    try:
-        module._exl3_dense_group = _dense_group_members(linears, group_id)
-    except ValueError as exc:
-        module._exl3_dense_group = None
-        _dense_group_fallback("registration", str(exc), group_id)
+    if len(linears) < 2:
+        module._exl3_dense_group = None            # a one-shard module may still join a fan
+    else:
+        group_id = f"local:{getattr(module, 'prefix', '?')}:{id(module)}"
+        try:
+            module._exl3_dense_group = _dense_group_members(linears, group_id)
+        except ValueError as exc:
+            module._exl3_dense_group = None
+            _dense_group_fallback("registration", str(exc), group_id)
+    if dense_group_mode() == 2:
+        _register_dense_fan(module)
+
+
+def prewarm_exl3_dense_group(module) -> None:
+    """Reserve the fused call's scratch for the prewarm row counts."""
+    group = getattr(module, "_exl3_dense_group", None)
+    if group:
+        _prewarm_group(group)
+
+
+# ---------------------------------------------------------------- T1 fans
+
+
+def _fan_spec(prefix: str | None):
+    """(kind, base prefix, role) of a fan member's module name, or None."""
+    for suffix, kind, role in _DENSE_FAN_ROLES:
+        if prefix and prefix.endswith(suffix):
+            return kind, prefix[: -len(suffix)], role
+    return None
 
 
 def _in_dense_fan(module) -> bool:
-    prefix = getattr(module, "prefix", None) or ""
-    return any(prefix.endswith(sfx) for sfx in _DENSE_FAN_SUFFIXES)
+    return _fan_spec(getattr(module, "prefix", None)) is not None
+
+
+def _fan_outputs(fan: dict, rows: int) -> list[torch.Tensor]:
+    """Row-count views of the fan's outputs in its own fp32 buffer (16 rows x
+    the members' total columns, reserved when the fan is built: under 3 MB for
+    the largest DSV4 fan, so every fan keeps its own and no fan waits for
+    another's generation to be read), one per member."""
+    buf = fan["outbuf"]
+    outs, off = [], 0
+    for n in fan["ns"]:
+        outs.append(buf[off:off + rows * n].view(rows, n))
+        off += rows * n
+    return outs
+
+
+def _register_dense_fan(module) -> None:
+    spec = _fan_spec(getattr(module, "prefix", None))
+    if spec is None:
+        return
+    kind, base, role = spec
+    group_id = f"{base}:{kind}fan"
+    import weakref
+
+    _DENSE_FAN_REGISTRY.setdefault(group_id, {})[role] = weakref.ref(module)
+    _publish_dense_fan(group_id, kind)
+
+
+def _publish_dense_fan(group_id: str, kind: str) -> None:
+    """Builds the fan once enough members are loaded: the h-fan needs qkv and
+    at least one compressor, the q-fan both of its modules
+    (recipe-lna/vllm_exl3_exl3.py.lna:423-505).  Members are the modules'
+    EXL3 linears in role order; the output buffer and the scratch are reserved
+    and every prewarm row count is run once."""
+    live = {role: ref() for role, ref in _DENSE_FAN_REGISTRY.get(group_id, {}).items() if ref() is not None}
+    roles = [r for r in _DENSE_FAN_ORDER[kind] if r in live]
+    complete = ("qkv" in live and len(roles) >= 2) if kind == "h" else len(roles) == len(_DENSE_FAN_ORDER["q"])
+    if not complete:
+        return
+    modules = [live[r] for r in roles]
+    flat, positions = [], {}
+    for module in modules:
+        members = [lin for lin in getattr(module, "_exl3_linears", None) or [] if lin is not None]
+        if not members or getattr(module, "_exl3_linear_bf16_shards", []):
+            for m in modules:
+                m._exl3_dense_fan = None
+            _dense_group_fallback("registration", "a fan member has bf16 or no EXL3 shards", group_id)
+            return
+        positions[id(module)] = tuple(range(len(flat), len(flat) + len(members)))
+        flat.extend(members)
+    try:
+        fan = _dense_group_members(flat, group_id)
+    except ValueError as exc:
+        for m in modules:
+            m._exl3_dense_fan = None
+        _dense_group_fallback("registration", str(exc), group_id)
+        return
+    import weakref
+
+    device = fan["device"]
+    fan.update({"kind": kind, "positions": positions, "member_ids": frozenset(id(m) for m in modules),
+                "member_refs": tuple(weakref.ref(m) for m in modules), "cache": None, "last_completed": None,
+                "generation": 0, "prewarm_failed": True,
+                "outbuf": torch.empty(DENSE_GROUP_MAX_ROWS * sum(fan["ns"]), dtype=torch.float32, device=device)})
+    if device.type == "cuda":
+        fan["prewarm_failed"] = not _prewarm_group(fan, lambda rows: _fan_outputs(fan, rows))
+    for m in modules:
+        m._exl3_dense_fan = fan
+
+
+def _source_key(source: torch.Tensor):
+    base = source
+    while getattr(base, "_base", None) is not None:
+        base = base._base
+    return (id(base), int(source.data_ptr()), tuple(source.shape), source.dtype, str(source.device))
+
+
+def _run_fan(module, fan: dict, x_fp16: torch.Tensor, source: torch.Tensor, m: int):
+    """T1: the first member called on a source tensor runs the whole fan and
+    caches every member's output; the other members called on the same source
+    (same tensor object and storage, rows and stream) read their outputs from
+    that call.  A generation ends once every member has read it.  A call that
+    cannot read the open generation (another source, or a member reading it a
+    second time) starts a new one, so a member never gets outputs computed
+    from another input.  Like the reference, a source tensor rewritten in
+    place between the members' calls is not detected.  Returns this module's
+    outputs, or None after a logged decline (the caller runs its shards solo)."""
+    group_id = fan["group_id"]
+    if fan.get("prewarm_failed"):
+        _dense_group_fallback("prewarm", "fan was not prewarmed", group_id)
+        return None
+    if int(x_fp16.shape[1]) != fan["k"]:
+        _dense_group_fallback("input", f"fan k={fan['k']} got {x_fp16.shape[1]}", group_id)
+        return None
+    if source.dim() != 2 or not source.is_contiguous():
+        _dense_group_fallback("input", "source must be contiguous 2D", group_id)
+        return None
+    positions = fan["positions"].get(id(module))
+    if positions is None:
+        _dense_group_fallback("registration", "caller is not a registered member", group_id)
+        return None
+    key = _source_key(source)
+    stream = int(torch.cuda.current_stream(x_fp16.device).cuda_stream)
+    cache = fan["cache"]
+    if cache is not None and cache["key"] == key and cache["m"] == m and id(module) not in cache["used"]:
+        if cache["stream"] != stream:
+            _dense_group_fallback("stream", f"trigger stream changed {cache['stream']}->{stream}", group_id)
+            return None
+        cache["used"].add(id(module))
+        result = [cache["outs"][i] for i in positions]
+        _DENSE_GROUP_STATS["t1_cached"] += 1
+        if cache["used"] == fan["member_ids"]:
+            fan["last_completed"] = {"key": key, "m": m, "stream": stream}
+            fan["cache"] = None
+        return result
+    if cache is not None:
+        # the open generation's readers that did not come lose it (logged once)
+        _dense_group_fallback("generation", "a new input started a generation before every member read the "
+                              "previous one", group_id)
+        fan["cache"] = None
+    outs = _fan_outputs(fan, m)
+    try:
+        ops.gemm_group(x_fp16, fan["members"], fan["codebook"], torch.float32, outs=outs)
+    except Exception as exc:
+        _dense_group_fallback("error", repr(exc), group_id)
+        return None
+    fan["generation"] += 1
+    fan["cache"] = {"key": key, "m": m, "stream": stream, "used": {id(module)}, "outs": outs,
+                    "source_ref": source}
+    _dense_group_active(2, group_id)
+    return [outs[i] for i in positions]
 
 
 def run_exl3_group(module, x_fp16: torch.Tensor, out_dtype: torch.dtype = torch.float32, *,
                    source_tensor: torch.Tensor | None = None) -> list:
     """Forward every EXL3 shard of one module call on the same contiguous fp16
-    input (recipe-lna/vllm_exl3_exl3.py.lna:616-802).  With LNA_EXL3_DENSE_GROUP
-    = 1 (or 2) and the preconditions met, one fused same-input call replaces the
-    per-shard calls; any decline falls back to the per-linear forwards used when
-    the flag is off.  Returns one output per entry of module._exl3_linears, of
-    dtype `out_dtype`."""
-    del source_tensor            # keyed the reference's T1 output cache
+    input (recipe-lna/vllm_exl3_exl3.py.lna:616-802).  LNA_EXL3_DENSE_GROUP=1:
+    the module's shards in one fused call (T0); =2: the module's layer fan
+    (T1) when it is a member, else its T0 group.  Any decline falls back to
+    the per-linear forwards used when the flag is off.  Returns one output per
+    entry of module._exl3_linears, of dtype `out_dtype`.  T1 outputs are views
+    of the fan's buffer, which its next generation reuses: callers copy them
+    (apply concatenates or casts) before the fan runs again."""
     linears = getattr(module, "_exl3_linears", None) or []
     solo = lambda: [lin.forward(x_fp16, {}, out_dtype=out_dtype) for lin in linears]
     mode = dense_group_mode()
+    fan = getattr(module, "_exl3_dense_fan", None) if mode == 2 else None
     if mode == 0:
         return solo()
-    if len(linears) < 2:
+    if len(linears) < 2 and fan is None:
         _dense_group_fallback("registration", "no fused group is available for this single-shard module")
         return solo()
     if x_fp16.dtype is not torch.float16 or not x_fp16.is_contiguous() or x_fp16.dim() != 2:
-        _dense_group_fallback("input", "input must be contiguous 2D fp16")
+        _dense_group_fallback("input", "input must be contiguous 2D fp16", fan["group_id"] if fan else None)
         return solo()
     if out_dtype is not torch.float32:
-        _dense_group_fallback("dtype", f"unsupported C dtype {out_dtype}")
+        _dense_group_fallback("dtype", f"unsupported C dtype {out_dtype}", fan["group_id"] if fan else None)
         return solo()
     m = x_fp16.shape[0]
-    if m > 16 or m < 1:
-        _dense_group_fallback("rows", f"rows={m} outside fused range 1..16")
+    if m > DENSE_GROUP_MAX_ROWS or m < 1:
+        _dense_group_fallback("rows", f"rows={m} outside fused range 1..{DENSE_GROUP_MAX_ROWS}",
+                              fan["group_id"] if fan else None)
         return solo()
-    if mode == 2 and _in_dense_fan(module):
+    if mode == 2 and fan is None and _in_dense_fan(module):
+        _, base, _ = _fan_spec(getattr(module, "prefix", None))
         _dense_group_fallback("registration", "T1 fan is not complete; using the registered local T0 group",
-                              f"{getattr(module, 'prefix', '?')}:fan")
+                              f"{base}:fan")
+    if fan is not None:
+        res = _run_fan(module, fan, x_fp16, source_tensor if source_tensor is not None else x_fp16, m)
+        if res is not None:
+            return res
+        if len(linears) < 2:
+            return solo()
     group = getattr(module, "_exl3_dense_group", None)
     if group is None and not hasattr(module, "_exl3_dense_group"):
         if torch.cuda.is_current_stream_capturing():
@@ -517,28 +743,42 @@ def _validate_lna_pointer_contract(inners, hidden: int, intermediate: int) -> No
 
 
 _LNA2_SCRATCH: dict[int, torch.Tensor] = {}
+_LNA2_SCRATCH_RETIRED: list[torch.Tensor] = []
+LNA2_MAX_TOPK = 9            # routed top-k plus a shared expert appended as one more slot
 
 
 def _lna2_scratch_for(layer, device: torch.device) -> torch.Tensor:
     """The shared routed-MoE scratch of this device, zeroed once on creation and
-    self-resetting after (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296).  One
-    launch at a time per device: launches on concurrent streams would share it."""
+    self-resetting after (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296).  Sized
+    for the largest top-k the kernels take, so a route with a shared-expert
+    slot never needs a bigger buffer at apply time (which capture forbids).
+    One launch at a time per device: launches on concurrent streams would share
+    it.  A replaced buffer stays alive: graphs captured on it keep its address."""
     hidden = int(layer._exl3_hidden_size)
     inter = int(layer._exl3_intermediate_local)
-    topk = int(getattr(layer, "_exl3_topk", 8))
-    nbytes = ops.moe_scratch_bytes(hidden, inter, topk)
+    nbytes = ops.moe_scratch_bytes(hidden, inter, LNA2_MAX_TOPK)
     idx = device.index if device.index is not None else torch.cuda.current_device()
     buf = _LNA2_SCRATCH.get(int(idx))
     if buf is None or buf.numel() < nbytes:
         if torch.cuda.is_current_stream_capturing():
             raise RuntimeError("LNA2 scratch was not prewarmed for this device")
+        if buf is not None:
+            _LNA2_SCRATCH_RETIRED.append(buf)
         buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
         _LNA2_SCRATCH[int(idx)] = buf
     return buf
 
 
 def lna2_scratch_bytes_resident() -> int:
-    return sum(int(b.numel()) for b in _LNA2_SCRATCH.values())
+    return sum(int(b.numel()) for b in _LNA2_SCRATCH.values()) + \
+        sum(int(b.numel()) for b in _LNA2_SCRATCH_RETIRED)
+
+
+def lna2_scratch_error(device: torch.device, clear: bool = True) -> int:
+    """Error word of this device's routed-MoE scratch (ops.ERR_* bits, 0 = none)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    buf = _LNA2_SCRATCH.get(int(idx))
+    return 0 if buf is None else ops.moe_error(buf, clear)
 
 
 def _prepare_lna_state(layer, inners) -> None:
@@ -906,9 +1146,35 @@ class Exl3MoEMethod:
         return apply_exl3_experts(x, topk_ids, topk_weights, layer, limit=float(limit))
 
 
+_WO_A_SLICE_RE = re.compile(r"wo_a\.slice\.(?P<rank>\d+)")
+WO_A_TP_SIZE = 8
+
+
+def _wo_a_slice_rank(loaded_shard_id) -> int | None:
+    """Group rank named by a wo_a shard id: an int, a digit string or a
+    ``wo_a.slice.N`` name (recipe-lna/vllm_exl3_exl3.py.lna:833-843)."""
+    if isinstance(loaded_shard_id, int):
+        return loaded_shard_id
+    if loaded_shard_id is None:
+        return None
+    text = str(loaded_shard_id)
+    if text.isdigit():
+        return int(text)
+    match = _WO_A_SLICE_RE.search(text)
+    return int(match.group("rank")) if match else None
+
+
+def _is_wo_a_layer(layer) -> bool:
+    """The attention output's low-rank input projection, stored as one
+    pre-sliced group per TP rank (recipe-lna/vllm_exl3_exl3.py.lna:846-852)."""
+    prefix = str(getattr(layer, "prefix", ""))
+    return _prefix_has_suffix(prefix, "attn.wo_a") or (bool(getattr(layer, "is_bmm", False))
+                                                        and prefix.endswith(".wo_a"))
+
+
 class Exl3LinearMethod:
-    """EXL3 dense linear with one or more same-input output shards
-    (recipe-lna/vllm_exl3_exl3.py.lna:2310-2853, EXL3 shards only)."""
+    """EXL3 dense linear with one or more same-input output shards, some of
+    which may be plain bf16 (recipe-lna/vllm_exl3_exl3.py.lna:2310-2853)."""
 
     def __init__(self, quant_config=None, bits: int | None = None, tp_rank: int = 0, tp_size: int = 1):
         self.quant_config = quant_config
@@ -921,16 +1187,25 @@ class Exl3LinearMethod:
         """Fused parameters over the module's same-input output shards
         (recipe-lna/vllm_exl3_exl3.py.lna:2323-2493).  vLLM tells row from
         column parallelism by the layer class; here the caller says which.
+        Shards the config lists as bf16 (``non_routed_exl3.layers[prefix]
+        .bf16_shards``) load into a bf16 ``weight`` staging parameter instead;
+        a wo_a module holds one pre-sliced group per TP rank (TP 8 only).
         Every parameter gets a weight_loader bound to its tensor kind."""
-        del input_size, output_size, params_dtype, extra_weight_attrs
+        del input_size, output_size, extra_weight_attrs
         k = input_size_per_partition
         for i, n in enumerate(output_partition_sizes):
             if k % 16 or n % 16:
                 raise ValueError(f"EXL3 trellis tiles are 16-wide; shard {i}: in={k} out={n}")
+        is_wo_a = _is_wo_a_layer(layer)
+        if is_wo_a and self.tp_size != WO_A_TP_SIZE:
+            raise NotImplementedError("EXL3 wo_a requires TP=8 (one local group per rank); "
+                                      f"got tp_size={self.tp_size}")
         bf16 = self.quant_config._bf16_shards_for(getattr(layer, "prefix", "")) \
             if hasattr(self.quant_config, "_bf16_shards_for") else []
-        if bf16:
-            raise NotImplementedError(f"EXL3 bf16 shards {bf16} are not part of this build's linear path")
+        if bf16 and self.tp_size > 1:
+            raise RuntimeError(f"EXL3 bf16 shards are not supported with TP size > 1; tp_size={self.tp_size}")
+        if any(not 0 <= i < len(output_partition_sizes) for i in bf16):
+            raise ValueError(f"bf16 shard indices {bf16} outside the module's {len(output_partition_sizes)} shards")
         n_shards = len(output_partition_sizes)
         total_tiles = sum(n // 16 for n in output_partition_sizes)
         params = {
@@ -940,28 +1215,56 @@ class Exl3LinearMethod:
             "mcg": torch.zeros(n_shards, 1, dtype=torch.int32),
             "mul1": torch.zeros(n_shards, 1, dtype=torch.int32),
         }
+        if not is_wo_a:
+            bf16_rows = sum(output_partition_sizes[i] for i in bf16)
+            params["weight"] = torch.empty(bf16_rows, k, dtype=params_dtype or torch.bfloat16)
         for name, t in params.items():
             p = Parameter(t, requires_grad=False)
             p.weight_loader = self._make_weight_loader(name, n_shards, list(output_partition_sizes),
-                                                       is_row_parallel)
+                                                       is_row_parallel, list(bf16), is_wo_a)
             layer.register_parameter(name, p)
         layer._exl3_linear_n_shards = n_shards
         layer._exl3_linear_output_partition_sizes = list(output_partition_sizes)
         layer._exl3_linear_input_size_per_partition = k
         layer._exl3_linear_is_row_parallel = bool(is_row_parallel)
-        layer._exl3_linear_bf16_shards = []
+        layer._exl3_linear_bf16_shards = list(bf16)
+        layer._exl3_linear_is_wo_a = is_wo_a
         layer._exl3_linear_tp_size = self.tp_size
         layer._exl3_linear_tp_rank = self.tp_rank
 
-    def _make_weight_loader(self, suffix: str, n_shards: int, sizes: list[int], is_row_parallel: bool):
+    def _make_weight_loader(self, suffix: str, n_shards: int, sizes: list[int], is_row_parallel: bool,
+                            bf16: list[int], is_wo_a: bool):
         """weight_loader(param, loaded_weight[, shard_id]) for one tensor kind
         (recipe-lna/vllm_exl3_exl3.py.lna:2495-2633): shard ids "q"/"k"/"v" or
         an int name the fused output shard; trellis/suh/svh are TP-narrowed
         (row: trellis dim 0 + suh, column: trellis dim 1 + svh) and copied into
-        the shard's slice; mcg/mul1 store the marker value."""
+        the shard's slice; mcg/mul1 store the marker value; ``weight`` keeps
+        only the bf16 shards' rows (an EXL3 shard's stale bf16 copy is
+        dropped).  For wo_a the shard id is the group rank (``wo_a.slice.N``)
+        and only this rank's group, already sliced, is kept."""
         tp_rank, tp_size = self.tp_rank, self.tp_size
 
+        def load_wo_a(param: Parameter, loaded_weight: torch.Tensor, loaded_shard_id) -> None:
+            rank = _wo_a_slice_rank(loaded_shard_id)
+            if rank is None:
+                raise ValueError("EXL3 wo_a loader requires a wo_a.slice.N shard id")
+            if rank != tp_rank:
+                return
+            loaded = loaded_weight.detach().contiguous()
+            if suffix in ("mcg", "mul1"):
+                param.data[0, 0] = int(loaded.item()) if loaded.numel() else 0
+                return
+            dest = {"trellis": param.data, "suh": param.data[0], "svh": param.data}.get(suffix)
+            if dest is None:
+                raise ValueError(f"unknown EXL3 wo_a suffix={suffix}")
+            if tuple(dest.shape) != tuple(loaded.shape):
+                raise RuntimeError(f"EXL3 wo_a load shape mismatch slice={rank} suffix={suffix}: "
+                                   f"dest {tuple(dest.shape)} != loaded {tuple(loaded.shape)}")
+            dest.copy_(loaded)
+
         def weight_loader(param: Parameter, loaded_weight: torch.Tensor, loaded_shard_id=None) -> None:
+            if is_wo_a:
+                return load_wo_a(param, loaded_weight, loaded_shard_id)
             shard_idx = 0
             if isinstance(loaded_shard_id, str):
                 shard_map = {"q": 0, "k": 1, "v": 2}
@@ -977,6 +1280,16 @@ class Exl3LinearMethod:
                 if tuple(dest.shape) != (1,):
                     raise RuntimeError(f"EXL3 {suffix} marker shape mismatch: expected (1,) got {tuple(dest.shape)}")
                 dest[0] = int(loaded_weight.detach().item()) if loaded_weight.numel() > 0 else 0
+                return
+            if suffix == "weight":
+                want = (sizes[shard_idx], param.shape[1])
+                loaded = loaded_weight.detach()
+                if tuple(loaded.shape) != want:
+                    raise RuntimeError(f"EXL3 weight load shape mismatch shard={shard_idx}: expected {want} "
+                                       f"got {tuple(loaded.shape)}")
+                if shard_idx in bf16:
+                    r0 = sum(sizes[i] for i in bf16[: bf16.index(shard_idx)])
+                    param.data[r0:r0 + sizes[shard_idx]].copy_(loaded)
                 return
             loaded = loaded_weight.detach().contiguous()
             sharded = (shard_exl3_row if is_row_parallel else shard_exl3_col)(loaded, suffix, tp_rank, tp_size)
@@ -998,33 +1311,99 @@ class Exl3LinearMethod:
         return weight_loader
 
     def process_weights_after_loading(self, layer) -> None:
+        """The reference's post-load lifecycle (recipe-lna/vllm_exl3_exl3.py.lna:2649-2768):
+        check each EXL3 shard's codebook marker; build one LinearEXL3 per EXL3
+        shard (None for bf16 shards, whose rows are kept as
+        ``_exl3_bf16_weight``); free the fused staging parameters, so only the
+        per-shard tensors stay resident; register the module's T0 group (and
+        its T1 fan); then run every linear and the group once per
+        LNA_EXL3_PREWARM_ROWS row count, so the shared scratch exists before
+        any graph capture."""
+        if not hasattr(layer, "trellis"):
+            return
         sizes = layer._exl3_linear_output_partition_sizes
+        bf16 = list(getattr(layer, "_exl3_linear_bf16_shards", []))
+        mcg_vals = [int(v) for v in layer.mcg.reshape(-1).tolist()]
+        mul1_vals = [int(v) for v in layer.mul1.reshape(-1).tolist()]
         linears, t0, o0 = [], 0, 0
         for i, n in enumerate(sizes):
-            mcg = layer.mcg[i] if int(layer.mcg[i].item()) == MCG_MARKER_SIGNED_INT32 else None
-            mul1 = layer.mul1[i] if int(layer.mul1[i].item()) == MUL1_MARKER_SIGNED_INT32 else None
-            if mcg is None and mul1 is None and (int(layer.mcg[i].item()) or int(layer.mul1[i].item())):
-                raise RuntimeError(f"EXL3 shard {i}: unknown codebook marker")
-            trellis = layer.trellis[:, t0:t0 + n // 16].contiguous()
-            linears.append(make_linear_exl3(trellis, layer.suh[i], layer.svh[o0:o0 + n], mcg, mul1))
+            if i in bf16:
+                linears.append(None)
+            else:
+                mcg_set, mul1_set = mcg_vals[i] != 0, mul1_vals[i] != 0
+                if mcg_set == mul1_set:
+                    raise RuntimeError(f"EXL3 linear shard {i}: {'both' if mcg_set else 'neither'} mcg and mul1 "
+                                       "markers are set; exactly one codebook marker must be present")
+                if mcg_set and mcg_vals[i] != MCG_MARKER_SIGNED_INT32:
+                    raise RuntimeError(f"EXL3 linear shard {i}: mcg marker is {mcg_vals[i]}, expected "
+                                       f"{MCG_MARKER_SIGNED_INT32}")
+                if mul1_set and mul1_vals[i] != MUL1_MARKER_SIGNED_INT32:
+                    raise RuntimeError(f"EXL3 linear shard {i}: mul1 marker is {mul1_vals[i]}, expected "
+                                       f"{MUL1_MARKER_SIGNED_INT32}")
+                trellis = layer.trellis[:, t0:t0 + n // 16].contiguous()
+                if trellis.data_ptr() == layer.trellis.data_ptr() and len(sizes) > 1:
+                    trellis = trellis.clone()
+                linears.append(make_linear_exl3(trellis, layer.suh[i].clone(), layer.svh[o0:o0 + n].clone(),
+                                                layer.mcg[i].clone() if mcg_set else None,
+                                                layer.mul1[i].clone() if mul1_set else None))
             t0 += n // 16
             o0 += n
         layer._exl3_linears = linears
+        weight = getattr(layer, "weight", None)
+        layer._exl3_bf16_weight = weight.data.clone() if bf16 and weight is not None else None
+        for name in ("weight", "trellis", "suh", "svh", "mcg", "mul1"):
+            if hasattr(layer, name):
+                delattr(layer, name)
+        build_exl3_dense_group(layer)
+        self._prewarm(layer)
+
+    @staticmethod
+    def _prewarm(layer) -> None:
+        lins = [lin for lin in layer._exl3_linears if lin is not None]
+        if not lins or lins[0].trellis.device.type != "cuda":
+            return
+        dev = lins[0].trellis.device
+        try:
+            for rows in sorted(set(_dense_prewarm_rows()) | {DENSE_GROUP_MAX_ROWS}):
+                for lin in lins:
+                    ops.prepare_gemm(dev, rows, int(lin.in_features), int(lin.out_features))
+            prewarm_exl3_dense_group(layer)
+        except Exception as exc:
+            logger.warning("EXL3 prewarm skipped for %s: %s", getattr(layer, "prefix", "?"), exc)
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+        """recipe-lna/vllm_exl3_exl3.py.lna:2770-2853: EXL3 shards on a
+        contiguous fp16 copy of x (through the module's T0 group or T1 fan when
+        LNA_EXL3_DENSE_GROUP asks for one), bf16 shards as plain linears,
+        outputs concatenated in shard order, cast to x's dtype, + bias."""
         linears = getattr(layer, "_exl3_linears", None)
         if not linears:
             raise RuntimeError("EXL3 linear layers were not built after weight load")
         orig = x.shape
         x2 = x.reshape(-1, orig[-1])
         xh = x2.to(torch.float16).contiguous()
-        outs = []
-        for i, lin in enumerate(linears):
-            if lin is None:
-                raise RuntimeError(f"EXL3 linear shard {i} is None")
-            outs.append(lin.forward(xh, {}, out_dtype=torch.float32))
-        y = torch.cat(outs, dim=1) if len(outs) > 1 else outs[0]
-        y = y.to(dtype=x.dtype)
+        bf16 = getattr(layer, "_exl3_linear_bf16_shards", [])
+        sizes = layer._exl3_linear_output_partition_sizes
+        if not bf16 and (len(linears) > 1 or (dense_group_mode() == 2
+                                              and getattr(layer, "_exl3_dense_fan", None) is not None)):
+            outs = run_exl3_group(layer, xh, torch.float32, source_tensor=x2)
+        else:
+            outs = []
+            weight = getattr(layer, "_exl3_bf16_weight", None)
+            for i, lin in enumerate(linears):
+                if i in bf16:
+                    if weight is None:
+                        raise RuntimeError(f"EXL3 bf16 shard {i} but _exl3_bf16_weight is missing")
+                    r0 = sum(sizes[j] for j in bf16[: bf16.index(i)])
+                    outs.append(F.linear(x2.to(weight.dtype), weight[r0:r0 + sizes[i]]).to(torch.float32))
+                elif lin is None:
+                    raise RuntimeError(f"EXL3 linear shard {i} is None")
+                else:
+                    outs.append(lin.forward(xh, {}, out_dtype=torch.float32))
+        # a fresh tensor always: fused-fan outputs are views its next call reuses
+        y = torch.cat(outs, dim=1) if len(outs) > 1 else outs[0].to(x.dtype, copy=True)
+        if y.dtype != x.dtype:
+            y = y.to(x.dtype)
         if bias is not None:
             y = y + bias
         return y.reshape(*orig[:-1], y.shape[-1])

@@ -107,6 +107,25 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
  */
 int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk);
 int exl3_moe_max_rows(void);
+
+/*
+ * Byte offset of the int32 error word inside a decode or prefill scratch
+ * buffer (the host-side counterpart of the reference's TORCH_CHECK failures
+ * and LNA_EXL3_DEBUG_FINITE signal, recipe-lna/lna2/lna_moe_ticket.cu:516-553,
+ * lna_moe_decode.cu:707; there no error crosses the kernel boundary).  Bits:
+ *   1  an expert of a width outside bits_mask was routed and not decoded
+ *      (decode: a width the kernel instance chosen for bits_mask lacks;
+ *      prefill: any width outside bits_mask); its contribution is zero and
+ *      the items still complete, so the scratch stays consistent;
+ *   2  (decode, ticket schedule) a bounded wait gave up.
+ * Decode scratch: the word is zero in the zeroed buffer, the kernels only set
+ * bits, and the caller reads and clears it (a 4-byte copy, outside any
+ * captured region).  Prefill scratch: the first launch of every call rewrites
+ * it, so it reports that call.  Widths are also checked where the entry points
+ * can see them: a host-side caller that builds expert_bits should check it
+ * against bits_mask before launching (the kernels cannot refuse a launch).
+ */
+int64_t exl3_moe_error_offset(void);
 int exl3_moe_decode(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
                     int64_t intermediate, int64_t n_experts, int64_t topk,
                     const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,

@@ -296,7 +296,8 @@ def moe(x16: np.ndarray, ids: np.ndarray, weights: np.ndarray, experts: list[dic
     topk = ids.shape[1]
     n_exp = len(experts)
     down_rows: dict[tuple[int, int], np.ndarray] = {}
-    for e in sorted({int(v) for v in ids.reshape(-1) if 0 <= int(v) < n_exp}):
+
+    def expert_rows(e):
         rows = sorted({r for r in range(m) if e in [int(v) for v in ids[r]]})
         ex = experts[e]
         b = ex["bits"]
@@ -319,8 +320,22 @@ def moe(x16: np.ndarray, ids: np.ndarray, weights: np.ndarray, experts: list[dic
         u = lin(h, "up")
         act = to_half_rne(swiglu_clamp(g, u, limit))
         d = lin(act, "down")
-        for i, r in enumerate(rows):
-            down_rows[(e, r)] = d[i]
+        return [((e, r), d[i]) for i, r in enumerate(rows)]
+
+    # Experts are independent: large layers run them on a thread pool (the C
+    # reconstruct and numpy's matmul release the GIL); the slot-order sum below
+    # is the same whatever the order they finish in.
+    active = sorted({int(v) for v in ids.reshape(-1) if 0 <= int(v) < n_exp})
+    workers = min(16, os.cpu_count() or 1, len(active))
+    if workers > 1 and len(active) >= 8:
+        from concurrent.futures import ThreadPoolExecutor
+
+        with ThreadPoolExecutor(max_workers=workers) as pool:
+            for pairs in pool.map(expert_rows, active):
+                down_rows.update(pairs)
+    else:
+        for e in active:
+            down_rows.update(expert_rows(e))
     out = np.zeros((m, H), np.float32)
     for r in range(m):
         acc = np.zeros(H, np.float32)

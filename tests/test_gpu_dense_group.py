@@ -220,3 +220,180 @@ def test_run_exl3_group_t1_falls_back_to_t0(dev):
     assert stats["t0_active"] == 1 and any(k.startswith("registration:") for k in stats["fallbacks"])
     for j, out in enumerate(outs):
         assert_close(out.cpu().numpy(), fan.ref(x.cpu().numpy(), j), what=f"T0 member {j}")
+
+
+# ---------------------------------------------------------------- the quant method's lifecycle and T1 fans
+
+
+def _quant_module(dev, prefix, k, shards, bits, seed, bf16=(), cfg=None, tp_rank=0, tp_size=1):
+    """A dense module built the way vLLM builds it: create_weights, one
+    weight_loader call per (tensor kind, shard), process_weights_after_loading.
+    Returns (layer, host shards); bf16 shards get a random bf16 weight."""
+    import torch
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    host = [synth.dense(k, n, bits, seed=seed + 13 * j) for j, n in enumerate(shards)]
+    layer = torch.nn.Module()
+    layer.prefix = prefix
+    meth = V.Exl3LinearMethod(cfg, bits=bits, tp_rank=tp_rank, tp_size=tp_size)
+    with torch.device(dev):
+        meth.create_weights(layer, k, list(shards), k, sum(shards), params_dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(seed)
+    for j, h in enumerate(host):
+        if j in bf16:
+            h["bf16"] = (torch.randn((shards[j], k), generator=g) / k ** 0.5).to(torch.bfloat16)
+            layer.weight.weight_loader(layer.weight, h["bf16"].to(dev), j)
+            continue
+        for suffix in ("trellis", "suh", "svh"):
+            p = getattr(layer, suffix)
+            p.weight_loader(p, torch.from_numpy(h[suffix]).to(dev), j)
+        layer.mcg.weight_loader(layer.mcg, torch.tensor(V.MCG_MARKER_SIGNED_INT32, dtype=torch.int32), j)
+    meth.process_weights_after_loading(layer)
+    return layer, meth, host
+
+
+def _module_ref(host, x16, bf16=()):
+    outs = []
+    for j, h in enumerate(host):
+        if j in bf16:
+            outs.append(x16.astype(np.float32) @ h["bf16"].float().numpy().T)
+        else:
+            outs.append(O.linear(x16, h["trellis"], h["suh"], h["svh"], h["bits"]))
+    return np.concatenate(outs, axis=1)
+
+
+def test_linear_method_prewarms_groups_and_captures(dev):
+    """LNA_EXL3_DENSE_GROUP=1: after process_weights_after_loading the
+    module's shards run as one fused call, the scratch is reserved for every
+    decode row count (no prepare_gemm by hand), and a graph captured at each
+    row count 1..16 replays to the oracle's result."""
+    import torch
+    from dsv4_carve_amd import ops, vllm_exl3 as V
+
+    V.reset_dense_group_state()
+    with dense_group(1):
+        layer, meth, host = _quant_module(dev, "model.layers.2.ffn.shared_experts.gate_up_proj", 1024,
+                                          [512, 512], 4, seed=1200)
+        assert V.dense_group_stats()["prewarm_groups"] == 1
+        before = ops.SCRATCH.resident_bytes()
+        for rows in range(1, 17):
+            x16 = synth.activations(rows, 1024, seed=1300 + rows)
+            x = to_dev(x16.astype(np.float32), dev)          # fp32 in and out: no output cast on the bar
+            static_out = None
+            stream = torch.cuda.Stream()
+            stream.wait_stream(torch.cuda.current_stream())
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                static_out = meth.apply(layer, x)
+            for rep in range(2):
+                graph.replay()
+                torch.cuda.synchronize()
+                assert_close(static_out.cpu().numpy(), _module_ref(host, x16),
+                             what=f"captured apply rows={rows} replay {rep}")
+        assert ops.SCRATCH.resident_bytes() == before, "capture needed scratch the prewarm did not reserve"
+    assert V.dense_group_call_counts()[1] > 0
+
+
+def _attention_fans(dev, k=1024, seed=1400):
+    """One attention layer's T1 members: the h-fan (fused_wqa_wkv with two
+    shards, compressor and indexer compressor with two each) and the q-fan
+    (wq_b and indexer.wq_b, one shard each, reading a 512-wide latent)."""
+    base = "model.layers.7.attn"
+    spec = {"qkv": (f"{base}.fused_wqa_wkv", k, [512, 256]),
+            "compressor": (f"{base}.compressor.fused_wkv_wgate", k, [256, 256]),
+            "indexer_compressor": (f"{base}.indexer.compressor.fused_wkv_wgate", k, [128, 128]),
+            "qb": (f"{base}.wq_b", 512, [1024]),
+            "indexer_qb": (f"{base}.indexer.wq_b", 512, [512])}
+    return {role: _quant_module(dev, prefix, kk, shards, 6, seed=seed + 97 * i)
+            for i, (role, (prefix, kk, shards)) in enumerate(spec.items())}
+
+
+def test_t1_fans_one_fused_call_per_input(dev):
+    """LNA_EXL3_DENSE_GROUP=2: the first h-fan member called on the hidden
+    state runs all six matrices in one call, the other two modules take their
+    outputs from it; likewise the q-fan.  Outputs match the oracle, eagerly
+    and replayed from a captured graph."""
+    import torch
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    V.reset_dense_group_state()
+    with dense_group(2):
+        mods = _attention_fans(dev)
+        for role, (layer, _, _) in mods.items():
+            assert getattr(layer, "_exl3_dense_fan", None) is not None, f"{role} did not join its fan"
+
+        def step(h, q):
+            return {r: mods[r][1].apply(mods[r][0], h if r in ("qkv", "compressor", "indexer_compressor") else q)
+                    for r in ("qkv", "qb", "compressor", "indexer_qb", "indexer_compressor")}
+
+        for rows in (1, 5, 16):
+            h16 = synth.activations(rows, 1024, seed=1500 + rows)
+            q16 = synth.activations(rows, 512, seed=1600 + rows)
+            h, q = to_dev(h16.astype(np.float32), dev), to_dev(q16.astype(np.float32), dev)
+            calls = V.dense_group_call_counts()[2]
+            out = step(h, q)
+            torch.cuda.synchronize()
+            assert V.dense_group_call_counts()[2] == calls + 2, "one fused call per fan and input"
+            for r, y in out.items():
+                x16 = h16 if r in ("qkv", "compressor", "indexer_compressor") else q16
+                assert_close(y.cpu().numpy(), _module_ref(mods[r][2], x16), what=f"T1 {r} rows={rows}")
+        assert V.dense_group_stats()["t1_cached"] >= 6
+        # the same step captured once and replayed
+        h = to_dev(synth.activations(4, 1024, seed=1700).astype(np.float32), dev)
+        q = to_dev(synth.activations(4, 512, seed=1701).astype(np.float32), dev)
+        eager = {r: y.clone() for r, y in step(h, q).items()}
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            static = step(h, q)
+        for rep in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            for r in eager:
+                assert torch.equal(static[r], eager[r]), f"T1 {r}: replay {rep} differs from the eager step"
+    V.reset_dense_group_state()
+
+
+def test_bf16_shards_apply(dev):
+    """A module with a bf16 shard between two EXL3 shards: EXL3 shards
+    through the GEMV, the bf16 one as a plain linear, concatenated in order."""
+    import torch
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    prefix = "model.layers.1.attn.fused_qkv"
+    cfg = V.Exl3Config(bits=3, non_routed_exl3={"layers": {prefix: {"bf16_shards": [1]}}})
+    layer, meth, host = _quant_module(dev, prefix, 512, [256, 128, 256], 3, seed=1800, bf16=(1,), cfg=cfg)
+    for rows in (1, 6, 40):
+        x16 = synth.activations(rows, 512, seed=1900 + rows)
+        y = meth.apply(layer, to_dev(x16.astype(np.float32), dev))
+        ref = _module_ref(host, x16, bf16=(1,))
+        assert_close(y[:, :256].cpu().numpy(), ref[:, :256], what="EXL3 shard 0")
+        assert_close(y[:, 384:].cpu().numpy(), ref[:, 384:], what="EXL3 shard 2")
+        # the bf16 shard is a bf16 product (the reference's F.linear on the bf16 weight): bf16's bar
+        assert rel_l2(y[:, 256:384].cpu().numpy(), ref[:, 256:384]) < 1e-2
+
+
+def test_wo_a_rank_slice_apply(dev):
+    """wo_a at TP8, rank 5: of the eight pre-sliced groups only rank 5's is
+    loaded, and the module computes that group's product."""
+    import torch
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    layer = torch.nn.Module()
+    layer.prefix = "model.layers.9.attn.wo_a"
+    meth = V.Exl3LinearMethod(bits=4, tp_rank=5, tp_size=8)
+    with torch.device(dev):
+        meth.create_weights(layer, 512, [256], 4096, 2048)
+    groups = [synth.dense(512, 256, 4, seed=2000 + r) for r in range(8)]
+    for r, h in enumerate(groups):
+        for suffix in ("trellis", "suh", "svh"):
+            p = getattr(layer, suffix)
+            p.weight_loader(p, torch.from_numpy(h[suffix]).to(dev), f"wo_a.slice.{r}")
+        layer.mcg.weight_loader(layer.mcg, torch.tensor(V.MCG_MARKER_SIGNED_INT32, dtype=torch.int32),
+                                f"wo_a.slice.{r}")
+    meth.process_weights_after_loading(layer)
+    x = synth.activations(3, 512, seed=2100)
+    y = meth.apply(layer, to_dev(x, dev))
+    h = groups[5]
+    assert_close(y.float().cpu().numpy(), O.linear(x, h["trellis"], h["suh"], h["svh"], 4), what="wo_a rank 5")

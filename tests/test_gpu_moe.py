@@ -80,6 +80,9 @@ class Layer:
         widths = dict(bits=self.bits[0]) if uniform else dict(expert_bits=self.ebits, bits_mask=self.mask)
         ops.moe_decode(xd, out, self.tables, to_dev(ids.astype(np.int32), dev), to_dev(w.astype(np.float32), dev),
                        intermediate=self.I, swiglu_limit=limit, scratch=scratch, **widths)
+        # the kernels' error word (widths, bounded waits) must stay clear
+        used = scratch if scratch is not None else ops.SCRATCH.current(dev, "moe")
+        assert ops.moe_error(used) == 0, "MoE decode set its error word"
         return out
 
     def ref(self, x16, ids, w, limit=LIMIT):
@@ -136,8 +139,7 @@ def inputs(m, name, H=512):
 def check(layer, x16, ids, w, what, **kw):
     got = layer.run(x16, ids, w, **kw).cpu().numpy()
     ref = layer.ref(x16, ids, w)
-    scale = max(1.0, float(np.abs(ref).max()))
-    assert_close(got / scale, ref / scale, what=what)
+    assert_close(got, ref, what=what)
     return got, ref
 
 
@@ -242,7 +244,16 @@ def test_cancel_and_zero_weights(small):
     assert np.all(got0 == 0.0)
 
 
-@pytest.mark.parametrize("name", ["zero", "amplified", "clamp-9.99", "clamp-10.0", "clamp-10.01"])
+# Outputs of the benchmark-shaped inputs (N(0,1) activations) stay below ~8 in
+# magnitude, where the absolute bar 2e-2 is 2.5e-3 of the output range.  The
+# amplified and clamp-saturating inputs below drive outputs to ~170: every
+# error source (fp16 activation and weight roundings) is relative, so these
+# cases keep rel-L2 1e-3 and apply the absolute bar at that same 2.5e-3 of
+# their output range.
+EXTREME_MAX_ABS_FRAC = 2e-2 / 8.0
+
+
+@pytest.mark.parametrize("name", ["zero", "real", "amplified", "clamp-9.99", "clamp-10.0", "clamp-10.01"])
 def test_inputs(small, name):
     m = 4
     ids, w = synth.routing(m, 16, 6, seed=7)
@@ -251,9 +262,12 @@ def test_inputs(small, name):
     ref = small.ref(x, ids, w)
     if name == "zero":
         assert np.all(got == 0.0)
+    elif name == "real":
+        assert_close(got, ref, what=name)
     else:
-        scale = max(1.0, float(np.abs(ref).max()))
-        assert_close(got / scale, ref / scale, what=name)
+        span = float(np.abs(ref).max())
+        assert span > 50.0, f"{name}: expected a saturating output range, got {span}"
+        assert_close(got, ref, max_abs=EXTREME_MAX_ABS_FRAC * span, what=name)
 
 
 @pytest.mark.parametrize("out_dtype", ["float16", "bfloat16"])
@@ -466,3 +480,98 @@ def test_lna2_signature_and_info(tp_slice, dev):
                         t["up_svh"], t["down_trellis"], t["down_suh"], t["down_svh"],
                         to_dev(ids.astype(np.int32), dev), to_dev(w, dev), 2, 10.0, scratch)
     assert_close(out.float().cpu().numpy(), layer.ref(x, ids, w), max_abs=2e-2 + 8e-3, what="lna2 signature")
+
+
+# ---------------------------------------------------------------- width tables and the error word
+
+
+def test_width_outside_mask_rejected_before_launch(small, dev):
+    """A per-expert width table that names a width outside bits_mask is refused
+    on the host, before any launch (decode and prefill)."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    x = to_dev(inputs(2, "real"), dev)
+    out = torch.empty((2, 512), dtype=torch.float32, device=dev)
+    ids = to_dev(route_ids(2, "unique"), dev)
+    w = to_dev(route_weights(2, "normal"), dev)
+    bad_mask = small.mask & ~(1 << 4)               # the table holds 4-bit experts
+    with pytest.raises(RuntimeError, match="outside bits_mask"):
+        ops.moe_decode(x, out, small.tables, ids, w, intermediate=256, expert_bits=small.ebits, bits_mask=bad_mask)
+    with pytest.raises(RuntimeError, match="outside bits_mask"):
+        ops.moe_prefill(x, out, small.tables, ids, w, intermediate=256, expert_bits=small.ebits, bits_mask=bad_mask)
+
+
+@pytest.mark.parametrize("path", ["phased", "ticket", "prefill"])
+def test_unlisted_width_sets_error_word(dev, path):
+    """Through the C ABI with the host check bypassed: experts of a width the
+    launch does not cover contribute nothing, the error word reports it, every
+    kernel completes, and the same scratch then serves a correct call."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    print(f"unlisted width {path}", flush=True)
+    bits = [3, 2, 5, 3, 2, 5, 3, 2]                  # experts 2 and 5 are 5-bit
+    layer = Layer(dev, 8, 512, 256, bits, seed=41)
+    m = 6
+    ids, w = synth.routing(m, 8, 4, seed=42)
+    x = inputs(m, "real")
+    keep = np.where(np.isin(ids, [2, 5]), 0.0, w).astype(np.float32)
+    assert (keep != w).any(), "the route must reach a 5-bit expert"
+    lacking = (1 << 2) | (1 << 3)                     # launch covers 2 and 3 bits only
+    xd, idd, wd = to_dev(x, dev), to_dev(ids, dev), to_dev(w, dev)
+    out = torch.empty((m, 512), dtype=torch.float32, device=dev)
+    args = (*[layer.tables[k] for k in ops.MOE_TABLE_KEYS], idd, wd, None, layer.ebits, 0)
+    if path == "prefill":
+        scratch = torch.zeros(ops.moe_prefill_scratch_bytes(m, 512, 256, 4, 8), dtype=torch.uint8, device=dev)
+        run = lambda mask: torch.ops.exl3_amd.moe_prefill(xd, out, *args, mask, ops.CB_MCG, LIMIT, 512, 256, scratch)
+    else:
+        scratch = torch.zeros(ops.moe_scratch_bytes(512, 256, 4), dtype=torch.uint8, device=dev)
+        run = lambda mask: torch.ops.exl3_amd.moe_decode(xd, out, *args, mask, ops.CB_MCG, LIMIT, 512, 256, scratch)
+    with moe_path("ticket" if path == "ticket" else "phased"):
+        run(lacking)
+        torch.cuda.synchronize()
+        assert ops.moe_error(scratch) == ops.ERR_WIDTH
+        assert_close(out.cpu().numpy(), layer.ref(x, ids, keep), what=f"{path}: unlisted width dropped")
+        run(layer.mask)                                 # the full mask: every expert decoded
+        torch.cuda.synchronize()
+        assert ops.moe_error(scratch) == 0
+        assert_close(out.cpu().numpy(), layer.ref(x, ids, w), what=f"{path}: full mask after the error")
+
+
+# ---------------------------------------------------------------- graph capture
+
+
+@pytest.mark.parametrize("path", ["phased", "ticket", "prefill"])
+def test_graph_replay_matches_eager(small, dev, path):
+    """A captured layer call replays bitwise like the eager call, also with
+    eager calls on the same scratch (other routes) between the replays."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    print(f"graph replay {path}", flush=True)
+    m = 24 if path == "prefill" else 7
+    op = ops.moe_prefill if path == "prefill" else ops.moe_decode
+    kw = dict(intermediate=256, expert_bits=small.ebits, bits_mask=small.mask, swiglu_limit=LIMIT)
+    ids, w = synth.routing(m, 16, 6, seed=60 + m)
+    xd, idd, wd = to_dev(inputs(m, "real"), dev), to_dev(ids, dev), to_dev(w, dev)
+    other_ids, other_w = synth.routing(m, 16, 6, seed=61 + m)
+    oid, ow = to_dev(other_ids, dev), to_dev(other_w, dev)
+    out = torch.empty((m, 512), dtype=torch.float32, device=dev)
+    scratch_out = torch.empty_like(out)
+    with moe_path("ticket" if path == "ticket" else "phased"):
+        op(xd, out, small.tables, idd, wd, **kw)        # reserves the scratch before capture
+        torch.cuda.synchronize()
+        eager = out.clone()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op(xd, out, small.tables, idd, wd, **kw)
+        for rep in range(3):
+            out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"{path}: replay {rep} differs from the eager call"
+            op(xd, scratch_out, small.tables, oid, ow, **kw)     # eager work on the same scratch
+            torch.cuda.synchronize()
+    assert_close(eager.cpu().numpy(), small.ref(inputs(m, "real"), ids, w), what=f"{path} eager")

@@ -31,6 +31,7 @@ def run_prefill(layer, x, ids, w, out_dtype=None, limit=LIMIT, uniform=False):
     widths = dict(bits=layer.bits[0]) if uniform else dict(expert_bits=layer.ebits, bits_mask=layer.mask)
     ops.moe_prefill(xd, out, layer.tables, to_dev(ids.astype(np.int32), dev), to_dev(w.astype(np.float32), dev),
                     intermediate=layer.I, swiglu_limit=limit, **widths)
+    assert ops.moe_error(ops.SCRATCH.current(dev, "moe_prefill")) == 0, "prefill set its error word"
     return out
 
 

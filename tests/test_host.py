@@ -398,9 +398,89 @@ def test_linear_method_shards():
     assert tuple(layer.trellis.shape) == (8, 24, 32) and tuple(layer.suh.shape) == (2, 128)
     layer.mcg.data.fill_(V.MCG_MARKER_SIGNED_INT32)
     layer.trellis.data.copy_(torch.arange(layer.trellis.numel(), dtype=torch.int32).reshape(8, 24, 32).to(torch.int16))
+    fused = layer.trellis.detach().clone()
     meth.process_weights_after_loading(layer)
     a, b = layer._exl3_linears
     assert (a.out_features, b.out_features) == (256, 128)
-    assert torch.equal(b.trellis, layer.trellis[:, 16:]) and b.trellis.is_contiguous()
+    assert torch.equal(a.trellis, fused[:, :16]) and torch.equal(b.trellis, fused[:, 16:])
+    assert a.trellis.is_contiguous() and b.trellis.is_contiguous()
+    # the fused staging parameters are freed once the shards are built
+    names = {n for n, _ in layer.named_parameters()}
+    assert not names & {"trellis", "suh", "svh", "mcg", "mul1", "weight"}, names
     with pytest.raises(RuntimeError, match="not built"):
         meth.apply(torch.nn.Module(), torch.zeros(1, 128))
+
+
+def test_linear_method_markers_checked():
+    """Exactly one codebook marker per EXL3 shard, with the marker's value
+    (recipe-lna/vllm_exl3_exl3.py.lna:2655-2690)."""
+    for fill, msg in (((0, 0), "neither"), ((V.MCG_MARKER_SIGNED_INT32, V.MUL1_MARKER_SIGNED_INT32), "both"),
+                      ((123, 0), "mcg marker is 123")):
+        layer = torch.nn.Module()
+        meth = V.Exl3LinearMethod(bits=2)
+        meth.create_weights(layer, 128, [128], 128, 128)
+        layer.mcg.data.fill_(fill[0])
+        layer.mul1.data.fill_(fill[1])
+        with pytest.raises(RuntimeError, match=msg):
+            meth.process_weights_after_loading(layer)
+
+
+def test_linear_method_bf16_shards_and_loader():
+    """Shards the config lists as bf16 load into the bf16 staging weight (the
+    EXL3 shards' stale bf16 copies are dropped) and are kept after processing
+    as _exl3_bf16_weight, with no LinearEXL3 (recipe-lna/vllm_exl3_exl3.py.lna:2467-2600)."""
+    cfg = V.Exl3Config(bits=2, non_routed_exl3={"layers": {"model.layers.0.attn.fused_qkv": {"bf16_shards": [1]}}})
+    layer = torch.nn.Module()
+    layer.prefix = "model.layers.0.attn.fused_qkv"
+    meth = V.Exl3LinearMethod(cfg, bits=2)
+    meth.create_weights(layer, 128, [128, 64, 128], 128, 320, params_dtype=torch.bfloat16)
+    assert tuple(layer.weight.shape) == (64, 128) and layer.weight.dtype == torch.bfloat16
+    w1 = torch.randn(64, 128).to(torch.bfloat16)
+    layer.weight.weight_loader(layer.weight, torch.randn(128, 128).to(torch.bfloat16), 0)   # EXL3 shard: dropped
+    layer.weight.weight_loader(layer.weight, w1, 1)
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        layer.weight.weight_loader(layer.weight, torch.zeros(32, 128, dtype=torch.bfloat16), 1)
+    layer.mcg.data.fill_(V.MCG_MARKER_SIGNED_INT32)
+    layer.mcg.data[1] = 0                      # a bf16 shard carries no marker
+    meth.process_weights_after_loading(layer)
+    lins = layer._exl3_linears
+    assert lins[1] is None and lins[0] is not None and lins[2] is not None
+    assert torch.equal(layer._exl3_bf16_weight, w1)
+    tp2 = torch.nn.Module()
+    tp2.prefix = "model.layers.0.attn.fused_qkv"
+    with pytest.raises(RuntimeError, match="TP size"):
+        V.Exl3LinearMethod(cfg, bits=2, tp_rank=0, tp_size=2).create_weights(tp2, 128, [128, 64, 128])
+    bad = torch.nn.Module()
+    bad.prefix = "model.layers.0.attn.fused_qkv"
+    with pytest.raises(ValueError, match="outside"):
+        V.Exl3LinearMethod(cfg, bits=2).create_weights(bad, 128, [128], 128, 128)
+
+
+def test_wo_a_loader_keeps_this_ranks_slice():
+    """wo_a: one pre-sliced group per TP8 rank; the loader keeps the slice
+    whose rank matches and never narrows it again
+    (recipe-lna/vllm_exl3_exl3.py.lna:2355-2362, 2533-2568)."""
+    layer = torch.nn.Module()
+    layer.prefix = "model.layers.5.attn.wo_a"
+    with pytest.raises(NotImplementedError, match="TP=8"):
+        V.Exl3LinearMethod(bits=2, tp_rank=0, tp_size=2).create_weights(layer, 256, [128])
+    layer = torch.nn.Module()
+    layer.prefix = "model.layers.5.attn.wo_a"
+    meth = V.Exl3LinearMethod(bits=2, tp_rank=3, tp_size=8)
+    meth.create_weights(layer, 256, [128], 2048, 1024)
+    assert not hasattr(layer, "weight")
+    for rank in range(8):
+        t = torch.full((16, 8, 32), rank, dtype=torch.int16)
+        layer.trellis.weight_loader(layer.trellis, t, f"wo_a.slice.{rank}")
+        layer.svh.weight_loader(layer.svh, torch.full((128,), float(rank), dtype=torch.float16), rank)
+        layer.suh.weight_loader(layer.suh, torch.full((256,), float(rank), dtype=torch.float16), str(rank))
+        layer.mcg.weight_loader(layer.mcg, torch.tensor(V.MCG_MARKER_SIGNED_INT32, dtype=torch.int32),
+                                f"wo_a.slice.{rank}")
+    assert int(layer.trellis.float().mean()) == 3 and float(layer.svh[0]) == 3.0 and float(layer.suh[0, 0]) == 3.0
+    with pytest.raises(ValueError, match="wo_a.slice.N"):
+        layer.trellis.weight_loader(layer.trellis, torch.zeros((16, 8, 32), dtype=torch.int16), "q")
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        layer.trellis.weight_loader(layer.trellis, torch.zeros((8, 8, 32), dtype=torch.int16), "wo_a.slice.3")
+    meth.process_weights_after_loading(layer)
+    (lin,) = layer._exl3_linears
+    assert lin.in_features == 256 and lin.out_features == 128 and int(lin.trellis.float().mean()) == 3
