@@ -27,6 +27,7 @@ import time
 import numpy as np
 
 HIDDEN, INTER, EXPERTS, TOPK = 4096, 2048, 256, 8
+LATENCY_ITERS = 40
 HBM_PEAK_GBS = 8000.0
 POOL = 64
 
@@ -64,9 +65,42 @@ class DeviceLayer:
         self.mask = sum(1 << b for b in set(self.bits))
 
 
+REPLAYS = 5             # timed graph replays per measurement (the median is reported)
+STABLE_TOL = 0.01       # warm-up replays continue until two in a row agree this closely
+MAX_WARM_REPLAYS = 10
+
+
+def _replay_timed(graph) -> float:
+    """ms of one replay, timed with events on the current stream (where the
+    replay runs)."""
+    import torch
+
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b)
+
+
+def replay_median(graph, steps: int) -> tuple[float, list[float]]:
+    """us per step: untimed replays until two consecutive ones agree within
+    STABLE_TOL (clocks settled, graph uploaded), then the median of REPLAYS
+    timed replays; also returns every timed replay's us per step."""
+    prev = None
+    for _ in range(MAX_WARM_REPLAYS):
+        t = _replay_timed(graph)
+        if prev is not None and abs(t - prev) <= STABLE_TOL * prev:
+            break
+        prev = t
+    per = sorted(_replay_timed(graph) * 1000.0 / steps for _ in range(REPLAYS))
+    return per[len(per) // 2], per
+
+
 def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, eager=False):
     """Returns (us per step, mean algorithmic bytes per step).  The K steps are
-    replayed from one HIP graph; `eager` launches them one by one instead (for
+    replayed from one HIP graph, the median over REPLAYS timed replays after
+    the clock has settled; `eager` launches them one by one instead (for
     counter collection, which sees every dispatch)."""
     import torch
     from dsv4_carve_amd import ops, synth
@@ -102,14 +136,51 @@ def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, 
         for i in range(steps):
             launch(i)
     torch.cuda.synchronize()
-    graph.replay()                       # one untimed replay (graph upload)
-    torch.cuda.synchronize()
-    # the replay runs on the current stream, where the events are recorded
-    start.record()
-    graph.replay()
-    end.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(end) * 1000.0 / steps, nbytes
+    us, _ = replay_median(graph, steps)
+    return us, nbytes
+
+
+def layer_latency(layer, dev, rows, topk, iters, seed, cold: bool) -> dict:
+    """Per-call latency distribution: `iters` layer calls launched one by one,
+    each bracketed by events.  Cold: fresh routing per call and a 1 GiB read
+    of another buffer before it (untimed), so neither the experts nor the
+    256 MB MALL hold anything the call reads; warm: the same routing and no
+    flush.  Returns p50/p95/mean in us."""
+    import ctypes
+
+    import torch
+    from dsv4_carve_amd import build as B
+    from dsv4_carve_amd import ops, synth
+
+    n_exp = len(layer.bits)
+    pool = [synth.routing(rows, n_exp, topk, seed=seed * 1000 + (i if cold else 0)) for i in range(POOL)]
+    ids = torch.tensor(np.stack([p[0] for p in pool]), dtype=torch.int32, device=dev)
+    wts = torch.tensor(np.stack([p[1] for p in pool]), dtype=torch.float32, device=dev)
+    x = torch.from_numpy(synth.activations(rows, layer.hidden, seed=seed)).to(dev)
+    out = torch.empty((rows, layer.hidden), dtype=torch.float32, device=dev)
+    scratch = ops.moe_scratch(dev, layer.hidden, layer.inter, topk)
+    probe = ctypes.CDLL(B.PROBE_LIB)
+    probe.exl3_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    flush = torch.ones((1 << 30) // 4, dtype=torch.int32, device=dev) if cold else None
+    blocks = torch.cuda.get_device_properties(dev).multi_processor_count * 8
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    stream = int(torch.cuda.current_stream(dev).cuda_stream)
+    times = []
+    for i in range(iters + 3):
+        if cold:
+            probe.exl3_probe_read(flush.data_ptr(), flush.numel() * 4, sink.data_ptr(), blocks, stream)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        ops.moe_decode(x, out, layer.tables, ids[i % POOL], wts[i % POOL], intermediate=layer.inter,
+                       expert_bits=layer.ebits, bits_mask=layer.mask, scratch=scratch)
+        b.record()
+        torch.cuda.synchronize()
+        if i >= 3:
+            times.append(a.elapsed_time(b) * 1000.0)
+    del flush
+    t = np.array(times)
+    return {"p50_us": round(float(np.percentile(t, 50)), 2), "p95_us": round(float(np.percentile(t, 95)), 2),
+            "mean_us": round(float(t.mean()), 2), "iters": iters}
 
 
 def time_glue(layer, dev, rows, topk, steps=40, seed=77):
@@ -155,14 +226,7 @@ def time_glue(layer, dev, rows, topk, steps=40, seed=77):
         with torch.cuda.graph(graph, stream=stream):
             for i in range(steps):
                 fn(i, m)
-        graph.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        graph.replay()
-        end.record()
-        torch.cuda.synchronize()
-        return round(start.elapsed_time(end) * 1000.0 / steps, 2)
+        return round(replay_median(graph, steps)[0], 2)
 
     res = {"kernel_only_us": timed(kernel, None)}
     for name, m in (("no_map", None), ("expert_map", emap)):
@@ -226,14 +290,7 @@ def time_fan(dev, k, ns, bits, rows_list, steps=40):
             with torch.cuda.graph(graph, stream=stream):
                 for i in order:
                     call(pool[i])
-            graph.replay()
-            torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            graph.replay()
-            b.record()
-            torch.cuda.synchronize()
-            out[mode] = a.elapsed_time(b) * 1000.0 / steps
+            out[mode] = replay_median(graph, steps)[0]
         nb = sum(dense_bytes(k, n, bits, rows) for n in ns)
         res[str(rows)] = {"fused_us": round(out["fused"], 2), "solo_us": round(out["solo"], 2),
                           "fused_GBps": round(nb / (out["fused"] * 1e-6) / 1e9, 1)}
@@ -274,14 +331,7 @@ def time_dense(dev, k, n, bits, rows_list, steps=40):
             with torch.cuda.graph(graph, stream=stream):
                 for i in order:
                     ops.gemm_into(x, pool[i], suh, svh, y)
-            graph.replay()
-            torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            graph.replay()
-            b.record()
-            torch.cuda.synchronize()
-            out[mode] = a.elapsed_time(b) * 1000.0 / steps
+            out[mode] = replay_median(graph, steps)[0]
         nb = dense_bytes(k, n, bits, rows)
         res[str(rows)] = {"us": round(out["cold"], 2), "GBps": round(nb / (out["cold"] * 1e-6) / 1e9, 1),
                           "warm_us": round(out["warm"], 2)}
@@ -320,14 +370,7 @@ def time_prefill(layer, dev, tokens, topk, steps, warmup, seed):
     with torch.cuda.graph(graph, stream=stream):
         for i in range(steps):
             launch(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1000.0 / steps
+    us = replay_median(graph, steps)[0]
     flops = float(np.mean([2.0 * 3 * layer.hidden * layer.inter * int(((p[0] >= 0) & (p[0] < n_exp)).sum())
                            for p in pool]))
     nbytes = float(np.mean([step_bytes(p[0], layer.bits, layer.hidden, layer.inter) for p in pool]))
@@ -426,14 +469,7 @@ def time_stack(dev, rows, steps, warmup):
     with torch.cuda.graph(graph, stream=stream):
         for i in range(steps):
             step(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record()
-    graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1000.0 / steps
+    us = replay_median(graph, steps)[0]
     del layers, graph
     torch.cuda.empty_cache()
     return us, nbytes
@@ -558,6 +594,9 @@ def main() -> int:
     us, nbytes = time_layer(layer, dev, a.rows, TOPK, a.steps, a.warmup, seed=a.rows, eager=a.eager)
     gbs = nbytes / (us * 1e-6) / 1e9
     print(f"[bench] rows={a.rows}: {us:.1f} us/layer, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    latency = {"cold": layer_latency(layer, dev, a.rows, TOPK, LATENCY_ITERS, seed=a.rows, cold=True),
+               "warm": layer_latency(layer, dev, a.rows, TOPK, LATENCY_ITERS, seed=a.rows, cold=False)}
+    print(f"[bench] per-call latency rows={a.rows}: {latency}", file=sys.stderr, flush=True)
 
     extra = {}
     if "ceiling" in legs:
@@ -566,8 +605,8 @@ def main() -> int:
     if "sweep" in legs:
         sweep = {}
         for m in (1, 2, 4, 8, 16):
-            u, b = time_layer(layer, dev, m, TOPK, 40, 3, seed=m)
-            uw, bw = time_layer(layer, dev, m, TOPK, 40, 3, seed=m, same_routing=True)
+            u, b = time_layer(layer, dev, m, TOPK, a.steps, 3, seed=m)
+            uw, bw = time_layer(layer, dev, m, TOPK, a.steps, 3, seed=m, same_routing=True)
             sweep[str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1),
                              "frac": round(b / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(b),
                              "warm_us": round(uw, 2), "warm_GBps": round(bw / (uw * 1e-6) / 1e9, 1)}
@@ -649,11 +688,15 @@ def main() -> int:
         print(f"[bench] calibration copy: {a.calib_copy_mib} MiB read + {a.calib_copy_mib} MiB written",
               file=sys.stderr, flush=True)
 
-    traffic = None
+    # HBM bytes per layer from the committed counter profile of this workload
+    # at 16 rows (not measured in this run; reported only at that row count)
+    traffic, traffic_source = None, None
     prof = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "moe_c2_m16_traffic.json")
-    if os.path.isfile(prof):
+    if a.rows == 16 and os.path.isfile(prof):
         with open(prof) as f:
-            traffic = json.load(f).get("hbm_bytes_per_layer")
+            meta = json.load(f)
+        traffic = meta.get("hbm_bytes_per_layer")
+        traffic_source = meta.get("source") or "profiles/moe_c2_m16_traffic.json (rocprofv3 --pmc, 16 rows)"
 
     line = {
         "metric": "routed-MoE decode us/layer + achieved HBM GB/s (% of 8 TB/s), rows 1-16",
@@ -672,8 +715,9 @@ def main() -> int:
                                "experts 0-127 3-bit / 128-255 2-bit EXL3 MCG, fresh routing each step",
                    "rows": a.rows, "experts": EXPERTS, "topk": TOPK, "hidden": HIDDEN, "intermediate": INTER},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_source,
                      "bytes_per_layer": int(nbytes)},
+        "latency_per_call": latency,
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -265,9 +265,10 @@ __device__ inline void build_plan(const Params& P, Plan& pl, char* tmp) {
 
 // ---------------------------------------------------------------- device sync helpers
 
+// One atomic per wave (its lane 0), the old value broadcast to the wave.
 __device__ __forceinline__ int wave_atomic_add(int* p, int v) {
     int old = 0;
-    if (threadIdx.x == 0) old = atomicAdd(p, v);
+    if ((threadIdx.x & (WAVE - 1)) == 0) old = atomicAdd(p, v);
     return __shfl(old, 0, WAVE);
 }
 
@@ -646,7 +647,7 @@ __device__ __forceinline__ void dispatch_bits(int bits, int* err, F&& body) {
         }
     });
     if (!done) {
-        if (threadIdx.x == 0) atomicOr(err, ERR_WIDTH);
+        if ((threadIdx.x & (WAVE - 1)) == 0) atomicOr(err, ERR_WIDTH);
         body(std::integral_constant<int, 0>{});
     }
 }
