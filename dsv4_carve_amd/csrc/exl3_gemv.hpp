@@ -379,6 +379,18 @@ __device__ __forceinline__ void had_in_load(const void* x, size_t x_off, const u
         }
 }
 
+// The lane's two rotated elements (2l, 2l+1) of one 128-block, packed as fp16
+// in natural order, from its loaded input pair v2 (x_kind) and sign pair s2.
+__device__ __forceinline__ uint32_t had_in_pair(uint32_t v2, uint32_t s2, int x_kind) {
+    if (x_kind != 0)
+        v2 = (uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 & 0xffffu))) |
+             ((uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 >> 16))) << 16);
+    float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 & 0xffffu) * f16_bits_to_f32(s2 & 0xffffu)));
+    float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 >> 16) * f16_bits_to_f32(s2 >> 16)));
+    fwht128_x2(v0, v1);
+    return (uint32_t)f32_to_f16_bits(v0 * HAD_NORM) | ((uint32_t)f32_to_f16_bits(v1 * HAD_NORM) << 16);
+}
+
 __device__ __forceinline__ void had_in_store(const RowIn& in, int x_kind, uint16_t* xa, int m, int nblocks,
                                              int nsteps_cap) {
     const int lane = threadIdx.x & (WAVE - 1);

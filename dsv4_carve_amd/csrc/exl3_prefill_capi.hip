@@ -108,69 +108,80 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     }
 }
 
-// ---------------------------------------------------------------- 2. input rotation (one wave per pair and projection)
+// ---------------------------------------------------------------- 2. input rotation (one wave per pair, projection and 512 columns)
+//
+// Every wave issues all of its loads before any arithmetic: one wave looping
+// over the 32 blocks of a 4096-wide row waited for each block's loads in
+// turn (50 us per layer at 512 tokens).
 
 __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     const PfLayout& L = P.L;
-    const int p = blockIdx.x >> 1, proj = blockIdx.x & 1;
+    const int nch = (P.H + 511) / 512;
+    const int p = blockIdx.x / (2 * nch);
+    const int rem = blockIdx.x - p * 2 * nch;
+    const int proj = rem / nch, ch = rem - (rem / nch) * nch;
     if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
     const int lane = threadIdx.x;
     const int s = pat<int>(P.scratch, L.pair_slot)[p];
     const int tok = s / P.topk, e = P.rt.local(s, P.E);
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>((proj ? P.usu : P.gsu)[e]);
-    const uint32_t* xr = reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint16_t*>(P.x) + (size_t)tok * P.H);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(pat<uint16_t>(P.scratch, L.Xh) + ((size_t)proj * P.P + p) * P.H);
-    const uint32_t* sp = reinterpret_cast<const uint32_t*>(suh);
-    for (int b = 0; b < P.H / 128; ++b) {
-        uint32_t v2 = xr[64 * b + lane];
-        const uint32_t s2 = sp[64 * b + lane];
-        if (P.x_kind != 0)
-            v2 = (uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 & 0xffffu))) |
-                 ((uint32_t)f32_to_f16_bits(bf16_to_f32((uint16_t)(v2 >> 16))) << 16);
-        float v0 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 & 0xffffu) * f16_bits_to_f32(s2 & 0xffffu)));
-        float v1 = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(v2 >> 16) * f16_bits_to_f32(s2 >> 16)));
-        fwht128_x2(v0, v1);
-        dst[64 * b + lane] = (uint32_t)f32_to_f16_bits(v0 * HAD_NORM) | ((uint32_t)f32_to_f16_bits(v1 * HAD_NORM) << 16);
-    }
+    const int k0 = ch * 512, nblocks = min(HAD_MAX_BLOCKS, (P.H - k0) / 128);
+    const uint16_t* suh = reinterpret_cast<const uint16_t*>((proj ? P.usu : P.gsu)[e]) + k0;
+    RowIn in;
+    had_in_load(P.x, (size_t)tok * P.H + k0, suh, nblocks, in);
+    uint32_t* dst = reinterpret_cast<uint32_t*>(pat<uint16_t>(P.scratch, L.Xh) + ((size_t)proj * P.P + p) * P.H + k0);
+#pragma unroll
+    for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
+        if (b < nblocks) dst[64 * b + lane] = had_in_pair(in.x[b], in.s[b], P.x_kind);
 }
 
-// ---------------------------------------------------------------- 4. activation + down input rotation (one wave per pair)
+// ---------------------------------------------------------------- 4. activation + down input rotation (one wave per pair and 256 columns)
 
 __global__ __launch_bounds__(64) void pf_act_kernel(PfParams P) {
     const PfLayout& L = P.L;
-    const int p = blockIdx.x;
+    const int ncb = P.I / COLS;
+    const int p = blockIdx.x / ncb, c0 = (blockIdx.x - p * ncb) * COLS;
     if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
     const int lane = threadIdx.x;
     const int e = P.rt.local(pat<int>(P.scratch, L.pair_slot)[p], P.E);
-    const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I;
-    const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I;
+    const int col = c0 + 128 * (lane >> 5) + 4 * (lane & 31);
+    const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I + col;
+    const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I + col;
     const size_t kstride = (size_t)2 * P.P * P.I;     // between k-parts
-    const uint16_t* dsu = reinterpret_cast<const uint16_t*>(P.dsu[e]);
-    uint16_t* AD = pat<uint16_t>(P.scratch, L.AD) + (size_t)p * P.I;
-    const int col = 128 * (lane >> 5) + 4 * (lane & 31);
-    for (int c0 = 0; c0 < P.I; c0 += COLS) {
-        float4_t g4 = *reinterpret_cast<const float4_t*>(G + c0 + col);
-        float4_t u4 = *reinterpret_cast<const float4_t*>(U + c0 + col);
-        for (int ks = 1; ks < L.ks_up; ++ks) {      // k-parts added in order
-            g4 += *reinterpret_cast<const float4_t*>(G + ks * kstride + c0 + col);
-            u4 += *reinterpret_cast<const float4_t*>(U + ks * kstride + c0 + col);
-        }
-        float dv[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float gg = g4[i], uu = u4[i];
-            if (gg > P.limit) gg = P.limit;
-            if (uu < -P.limit) uu = -P.limit;
-            if (uu > P.limit) uu = P.limit;
-            const uint16_t act = f32_to_f16_bits((gg / (1.0f + expf(-gg))) * uu);
-            dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[c0 + col + i])));
-        }
-        fwht128_x4(dv);
-        uint2 packed;
-        packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
-        packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
-        *reinterpret_cast<uint2*>(AD + c0 + col) = packed;
+    uint16_t dsu[4];
+    {
+        const uint2 d = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(P.dsu[e]) + col);
+        dsu[0] = (uint16_t)d.x; dsu[1] = (uint16_t)(d.x >> 16); dsu[2] = (uint16_t)d.y; dsu[3] = (uint16_t)(d.y >> 16);
     }
+    // every k-part's loads first, then the sums in k-part order
+    float4_t gp[4], up[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        if (ks < L.ks_up) {
+            gp[ks] = *reinterpret_cast<const float4_t*>(G + ks * kstride);
+            up[ks] = *reinterpret_cast<const float4_t*>(U + ks * kstride);
+        }
+    float4_t g4 = gp[0], u4 = up[0];
+#pragma unroll
+    for (int ks = 1; ks < 4; ++ks)
+        if (ks < L.ks_up) {
+            g4 += gp[ks];
+            u4 += up[ks];
+        }
+    float dv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        float gg = g4[i], uu = u4[i];
+        if (gg > P.limit) gg = P.limit;
+        if (uu < -P.limit) uu = -P.limit;
+        if (uu > P.limit) uu = P.limit;
+        const uint16_t act = f32_to_f16_bits((gg / (1.0f + expf(-gg))) * uu);
+        dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[i])));
+    }
+    fwht128_x4(dv);
+    uint2 packed;
+    packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
+    packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
+    *reinterpret_cast<uint2*>(pat<uint16_t>(P.scratch, L.AD) + (size_t)p * P.I + col) = packed;
 }
 
 // ---------------------------------------------------------------- 6. gather (one wave per token and 256-column block)
@@ -183,16 +194,30 @@ __global__ __launch_bounds__(64) void pf_gather_kernel(PfParams P) {
     const int col = cb * COLS + 4 * lane;
     const int* pos = pat<int>(P.scratch, L.pos);
     const float* D = pat<float>(P.scratch, L.D);
-    float s4[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int j = 0; j < P.topk; ++j) {
-        const int p = pos[tok * P.topk + j];
-        if (p < 0) continue;
-        const float wt = P.rt.weight(tok * P.topk + j);
-        float4_t d = *reinterpret_cast<const float4_t*>(D + (size_t)p * P.H + col);
-        for (int ks = 1; ks < L.ks_down; ++ks)      // k-parts added in order
-            d += *reinterpret_cast<const float4_t*>(D + ((size_t)ks * P.P + p) * P.H + col);
+    // every slot's loads first (pair index, weight, both k-parts), then the
+    // fp32 sum in top-k slot order
+    int pp[PF_MAX_TOPK];
+    float wt[PF_MAX_TOPK];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt * d[i];
+    for (int j = 0; j < PF_MAX_TOPK; ++j) {
+        pp[j] = j < P.topk ? pos[tok * P.topk + j] : -1;
+        wt[j] = j < P.topk ? P.rt.weight(tok * P.topk + j) : 0.f;
+    }
+    float4_t d0[PF_MAX_TOPK], d1[PF_MAX_TOPK];
+#pragma unroll
+    for (int j = 0; j < PF_MAX_TOPK; ++j)
+        if (pp[j] >= 0) {
+            d0[j] = *reinterpret_cast<const float4_t*>(D + (size_t)pp[j] * P.H + col);
+            if (L.ks_down > 1) d1[j] = *reinterpret_cast<const float4_t*>(D + ((size_t)P.P + pp[j]) * P.H + col);
+        }
+    float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < PF_MAX_TOPK; ++j) {
+        if (pp[j] < 0) continue;
+        float4_t d = d0[j];
+        if (L.ks_down > 1) d += d1[j];                // k-parts added in order
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s4[i] = s4[i] + wt[j] * d[i];
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) store_out(P.out, (size_t)tok * P.H + col + i, P.out_kind, s4[i]);
@@ -288,12 +313,12 @@ static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, 
     int rc;
     hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(1024), 0, s, P);
     if ((rc = check_launch())) return rc;
-    hipLaunchKernelGGL(pf_rotate_kernel, dim3(2 * P.P), dim3(WAVE), 0, s, P);
+    hipLaunchKernelGGL(pf_rotate_kernel, dim3(2 * P.P * ((hidden + 511) / 512)), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
     const int64_t tiles = P.L.max_tiles;
     if ((rc = launch_widths(P, mask, codebook, false, (int)(tiles * 2 * (intermediate / COLS) * P.L.ks_up), s)))
         return rc;
-    hipLaunchKernelGGL(pf_act_kernel, dim3(P.P), dim3(WAVE), 0, s, P);
+    hipLaunchKernelGGL(pf_act_kernel, dim3(P.P * (intermediate / COLS)), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
     if ((rc = launch_widths(P, mask, codebook, true, (int)(tiles * (hidden / COLS) * P.L.ks_down), s))) return rc;
     hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)(tokens * (hidden / COLS))), dim3(WAVE), 0, s, P);
