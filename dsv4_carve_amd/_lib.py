@@ -25,6 +25,8 @@ EXPORTS = (
     "exl3_moe_error_offset",
     "exl3_moe_decode",
     "exl3_moe_decode_routed",
+    "exl3_moe_noalloc_scratch_bytes",
+    "exl3_moe_decode_noalloc",
     "exl3_moe_info",
     "exl3_moe_prefill_scratch_bytes",
     "exl3_moe_prefill",
@@ -56,6 +58,11 @@ _SIGS = {
                                 _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                 _P, _I, _P, _I, _P, _L,
                                 _P, _I, _I, _I, _F, _P, _L, _P], _I),
+    "exl3_moe_noalloc_scratch_bytes": ([], _L),
+    "exl3_moe_decode_noalloc": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,
+                                 _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                 _P, _I, _P, _I, _P, _L,
+                                 _P, _I, _I, _I, _F, _P], _I),
     "exl3_moe_info": ([ctypes.POINTER(ctypes.c_int64), _I], _I),
     "exl3_moe_prefill_scratch_bytes": ([_L, _L, _L, _L, _L], _L),
     "exl3_moe_prefill": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,

@@ -3,6 +3,7 @@
 //   exl3_moe_scratch_bytes  <- lna2_moe_scratch_bytes  :481
 //   exl3_moe_max_rows       <- lna2_moe_max_rows       :484
 //   exl3_moe_info           <- lna2_moe_info           :494-505
+//   exl3_moe_decode_noalloc    (no counterpart: the routed decode on a fixed scratch)
 #include <math.h>
 #include <stddef.h>
 #include <stdlib.h>
@@ -228,6 +229,81 @@ int exl3_moe_decode_routed(const void* x, int x_kind, void* out, int out_kind, i
     return moe_decode_impl(x, x_kind, out, out_kind, m, hidden, intermediate, n_experts, topk, gate_trellis,
                            gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh, rt,
                            expert_bits, bits, bits_mask, codebook, swiglu_limit, scratch, scratch_bytes, stream);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- fixed scratch (no allocation)
+//
+// The scratch of exl3_moe_decode_noalloc: one array per GPU inside the
+// library's code object, held until the process ends.  Host code never passes
+// the array's name to a kernel: hipGetSymbolAddress gives each device's own
+// address, kept per device, and only that address is used.
+
+constexpr int64_t NOALLOC_SCRATCH_BYTES = (int64_t)128 << 20;
+static __device__ __align__(256) char fixed_scratch[NOALLOC_SCRATCH_BYTES];
+
+__global__ __launch_bounds__(256) void zero_fill_kernel(uint4* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// This device's fixed scratch.  On the first call on a device its control
+// words (the fixed region at the head of every layout) are zeroed by a fill
+// kernel on `stream`, ahead of the layer's launches.  A fill recorded into a
+// graph being captured is not remembered: the next call outside a capture
+// fills again.
+static int fixed_scratch_for(hipStream_t stream, char** out) {
+    static char* addr[MAX_DEVICES] = {};
+    static bool zeroed[MAX_DEVICES] = {};
+    static std::mutex mu;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return fail("no HIP device");
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(fixed_scratch)) != hipSuccess || !p)
+            return fail("cannot locate the fixed MoE scratch on this device");
+        addr[dev] = reinterpret_cast<char*>(p);
+    }
+    if (!zeroed[dev]) {
+        const int64_t ctrl_bytes = layout(COLS, COLS, 1).PA;     // the same for every shape
+        hipLaunchKernelGGL(zero_fill_kernel, dim3(256), dim3(256), 0, stream, reinterpret_cast<uint4*>(addr[dev]),
+                           ctrl_bytes / 16);
+        if (int rc = check_launch()) return rc;
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        if (hipStreamIsCapturing(stream, &st) == hipSuccess && st == hipStreamCaptureStatusNone) zeroed[dev] = true;
+    }
+    *out = addr[dev];
+    return 0;
+}
+
+extern "C" {
+
+int64_t exl3_moe_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+int exl3_moe_decode_noalloc(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                            int64_t intermediate, int64_t n_experts, int64_t topk,
+                            const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                            const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                            const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                            const void* topk_ids, int ids_kind, const void* topk_weights, int weights_kind,
+                            const int64_t* expert_map, int64_t n_global,
+                            const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                            float swiglu_limit, void* stream) {
+    clear_error();
+    const int64_t need = exl3_moe_scratch_bytes(hidden, intermediate, topk);
+    if (need < 0) return (int)need;
+    if (need > NOALLOC_SCRATCH_BYTES)
+        return fail("layer needs more scratch than the fixed 128 MiB (see exl3_moe_scratch_bytes)");
+    Route rt;
+    if (int rc = make_route(topk_ids, ids_kind, topk_weights, weights_kind, expert_map, n_global, rt)) return rc;
+    char* scratch = nullptr;
+    if (int rc = fixed_scratch_for(reinterpret_cast<hipStream_t>(stream), &scratch)) return rc;
+    return moe_decode_impl(x, x_kind, out, out_kind, m, hidden, intermediate, n_experts, topk, gate_trellis,
+                           gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh, rt,
+                           expert_bits, bits, bits_mask, codebook, swiglu_limit, scratch, NOALLOC_SCRATCH_BYTES,
+                           stream);
 }
 
 }  // extern "C"

@@ -162,6 +162,31 @@ int exl3_moe_decode_routed(const void* x, int x_kind, void* out, int out_kind, i
                            float swiglu_limit, void* scratch, int64_t scratch_bytes, void* stream);
 
 /*
+ * exl3_moe_decode_routed without a scratch argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * scratch is a fixed device array inside the library, one per GPU, of
+ * exl3_moe_noalloc_scratch_bytes() = 128 MiB, held until the process ends; a
+ * layer whose exl3_moe_scratch_bytes(hidden, intermediate, topk) exceeds it is
+ * rejected (hidden 4096, intermediate 2048, top-9 needs about 126 MB).  The
+ * call allocates nothing.  Its control words are zeroed by a fill kernel on
+ * `stream` at the first call on each device and reset themselves afterwards.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race, so issue them on one stream.  Results
+ * are bitwise those of exl3_moe_decode_routed.
+ */
+int64_t exl3_moe_noalloc_scratch_bytes(void);
+int exl3_moe_decode_noalloc(const void* x, int x_kind, void* out, int out_kind, int64_t m, int64_t hidden,
+                            int64_t intermediate, int64_t n_experts, int64_t topk,
+                            const int64_t* gate_trellis, const int64_t* gate_suh, const int64_t* gate_svh,
+                            const int64_t* up_trellis, const int64_t* up_suh, const int64_t* up_svh,
+                            const int64_t* down_trellis, const int64_t* down_suh, const int64_t* down_svh,
+                            const void* topk_ids, int ids_kind, const void* topk_weights, int weights_kind,
+                            const int64_t* expert_map, int64_t n_global,
+                            const int8_t* expert_bits, int bits, int bits_mask, int codebook,
+                            float swiglu_limit, void* stream);
+
+/*
  * Routed-MoE layer for many tokens (prefill), same mathematics as
  * exl3_moe_decode: tokens are routed by expert on the device and each expert's
  * weights are decoded once per 32 routed rows, feeding fp16 MFMA with fp32
