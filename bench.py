@@ -236,7 +236,8 @@ def time_glue(layer, dev, rows, topk, steps=40, seed=77):
 
 DENSE_SHAPES = ((4096, 4096), (4096, 1536), (1536, 4096), (4096, 12288))
 DENSE_BITS = (2, 3, 4, 6)
-DENSE_ROWS = (1, 2, 4, 8, 16)
+DENSE_ROWS = (1, 2, 4, 8, 16, 32, 64, 144)     # above 16: 32-row blocks, the LinearEXL3 GEMV range
+FAN_ROWS = (1, 2, 4, 8, 16)                     # the row range the plugin fuses
 
 
 def dense_bytes(k: int, n: int, bits: int, rows: int) -> int:
@@ -662,7 +663,7 @@ def main() -> int:
     if "fan" in legs:
         fans = {}
         for name, (k, ns, b) in FANS.items():
-            fans[name] = time_fan(dev, k, ns, b, DENSE_ROWS)
+            fans[name] = time_fan(dev, k, ns, b, FAN_ROWS)
             print(f"[bench] fan {name}: {fans[name]}", file=sys.stderr, flush=True)
         extra["dense_fan_cold"] = fans
 

@@ -72,8 +72,9 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
     float* partials = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) +
                                                align_up((int64_t)p.n_cb * 4, 256));
     const size_t c_elem = c_kind == OUT_F32 ? 4 : 2;
-    for (int64_t r0 = 0; r0 < m; r0 += MAX_ROWS) {
-        const int R = (int)(m - r0 < MAX_ROWS ? m - r0 : MAX_ROWS);
+    const int64_t block = gemv_block_rows(m);
+    for (int64_t r0 = 0; r0 < m; r0 += block) {
+        const int R = (int)(m - r0 < block ? m - r0 : block);
         const uint16_t* ar = a + r0 * k;
         void* cr = reinterpret_cast<char*>(c) + (size_t)r0 * n * c_elem;
         const GemvArgs args{ar, b, suh, svh, cr, c_kind, R, (int)k, (int)n, p, codebook, counters, partials, s};
@@ -81,7 +82,7 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
         EXL3_BITS_SWITCH(bits, rc = launch_gemv<B_>(args));
         if (rc) return rc;
         if (p.split_reduce) {
-            hipLaunchKernelGGL((gemv_reduce_kernel<16>), dim3(p.n_cb * R), dim3(64), 0, s, partials, svh, cr,
+            hipLaunchKernelGGL(gemv_reduce_kernel<RED_BATCH>, dim3((int)(n / 128) * R), dim3(64), 0, s, partials, svh, cr,
                                c_kind, R, (int)n, p.n_kc);
             if ((rc = check_launch())) return rc;
         }
@@ -89,18 +90,18 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
     return 0;
 }
 
-// Fan scratch: per member, partials [n_kc][min(m, 16)][n_j] fp32, each member's
-// region 256-byte aligned.
+// Fan scratch: per member, its split-K partials (gemv_partial_bytes), each
+// member's region 256-byte aligned.
 static int64_t fan_scratch(int64_t m, int64_t k, int64_t count, const int64_t* n_list, int cus, GemvPlan* plan,
                            int64_t* offsets) {
     int64_t total_cb = 0;
     for (int64_t j = 0; j < count; ++j) total_cb += (n_list[j] + COLS - 1) / COLS;
-    const GemvPlan p = gemv_fan_plan(k, total_cb, cus);
-    const int64_t rows = m < MAX_ROWS ? m : MAX_ROWS;
+    const GemvPlan p = gemv_fan_plan(m, k, total_cb, cus);
+    const int64_t rows = m < GEMV_MAX_ROWS ? m : GEMV_MAX_ROWS;
     int64_t o = 0;
     for (int64_t j = 0; j < count; ++j) {
         if (offsets) offsets[j] = o;
-        o = align_up(o + (int64_t)p.n_kc * rows * n_list[j] * 4, 256);
+        o = align_up(o + gemv_partial_bytes(rows, (n_list[j] + COLS - 1) / COLS, p.n_kc), 256);
     }
     if (plan) *plan = p;
     return o;
@@ -143,8 +144,9 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
     if (scratch_bytes < fan_scratch(m, k, count, n_list, cus, &p, offsets)) return fail("scratch too small");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const size_t c_elem = c_kind == OUT_F32 ? 4 : 2;
-    for (int64_t r0 = 0; r0 < m; r0 += MAX_ROWS) {
-        const int R = (int)(m - r0 < MAX_ROWS ? m - r0 : MAX_ROWS);
+    const int64_t block = gemv_block_rows(m);
+    for (int64_t r0 = 0; r0 < m; r0 += block) {
+        const int R = (int)(m - r0 < block ? m - r0 : block);
         FanParams P{};
         P.x = a + r0 * k;
         P.R = R; P.K = (int)k; P.nsteps = p.nsteps; P.n_kc = p.n_kc; P.count = (int)count; P.out_kind = c_kind;
@@ -159,17 +161,17 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
             P.block0[j] = blocks;
             P.rblock0[j] = rblocks;
             blocks += n_cb * p.n_kc;
-            rblocks += n_cb * R;
+            rblocks += (int)(n_list[j] / 128) * R;
         }
         P.block0[count] = blocks;
         P.rblock0[count] = rblocks;
         for (int b = 1; b <= 8; ++b) {
             if (!(widths & (1u << b))) continue;
             int rc = 0;
-            EXL3_BITS_SWITCH(b, rc = launch_gemv_fan<B_>(P, codebook, blocks, s));
+            EXL3_BITS_SWITCH(b, rc = launch_gemv_fan<B_>(P, codebook, p.waves, blocks, s));
             if (rc) return rc;
         }
-        hipLaunchKernelGGL((gemv_fan_reduce_kernel<16>), dim3(rblocks), dim3(64), 0, s, P);
+        hipLaunchKernelGGL(gemv_fan_reduce_kernel<RED_BATCH>, dim3(rblocks), dim3(64), 0, s, P);
         if (int rc = check_launch()) return rc;
     }
     return 0;

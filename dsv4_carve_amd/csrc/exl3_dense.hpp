@@ -3,6 +3,8 @@
 // exl3_dense_inst.hip instantiates them once per bit width.
 #pragma once
 
+#include <stdlib.h>
+
 #include "exl3_gemv.hpp"
 #include "exl3_capi_util.hpp"
 
@@ -108,79 +110,307 @@ __global__ __launch_bounds__(64) void dequant_had_kernel(const int16_t* __restri
 }
 
 // ---------------------------------------------------------------- dense GEMV
+//
+// An item is (256-column block cb, k-chunk kc of `nsteps` 64-row steps) of
+// y = had_in(x) . Wq for rows 0..R-1.  Its workgroup has W waves (1, 2 or 4):
+// wave w accumulates the output columns n in [w*16/W, (w+1)*16/W) of each of
+// the block's 16 n-tiles, so one step's decode is spread over W SIMDs with no
+// cross-wave sum.  Every wave loads the whole tile (a lane's windows interleave
+// the column groups); the repeats hit the CU's L1.  At few rows the call is
+// latency-bound: the plan shortens items and splits columns until there is a
+// wave per SIMD, so each wave decodes as little as possible.
 
 constexpr int GEMV_NSTEP_CAP = 8;   // k rows per item <= 512
+constexpr int GEMV_MAX_WAVES = 4;   // column groups per item
+constexpr int GEMV_MAX_ROWS = 32;   // rows per call: one or two 16-row MFMA blocks share each decode
 
 struct GemvPlan {
-    int nsteps;         // steps (64 k-rows) per item, even
+    int nsteps;         // steps (64 k-rows) per item
     int n_kc;           // k-chunks
     int n_cb;           // 256-column blocks
+    int waves;          // waves per item (column groups), 1, 2 or 4
     bool split_reduce;  // partial sums finished by gemv_reduce_kernel
 };
 
-inline GemvPlan gemv_plan(int64_t rows, int64_t k, int64_t n, int cus) {
+// Rows of x per call of the kernels: up to 16 rows one MFMA row block, 17 and
+// more two (32 rows).
+inline int64_t gemv_block_rows(int64_t m) { return m > MAX_ROWS ? GEMV_MAX_ROWS : MAX_ROWS; }
+
+// EXL3_GEMV_STEPS / EXL3_GEMV_WAVES override the plan's steps per item
+// (1, 2, 4, 8; kept only if it divides the k steps) and waves per item
+// (1, 2, 4); EXL3_GEMV_LAST_ARRIVER=1 finishes every call in the last
+// arriving workgroup of each column block instead of a reduction launch.
+// 0 or unset: the plan below.
+inline int gemv_override(const char* name) {
+    const char* v = getenv(name);
+    const int x = v && *v ? atoi(v) : 0;
+    return (x == 1 || x == 2 || x == 4 || x == 8) ? x : 0;
+}
+
+inline GemvPlan gemv_plan_cb(int64_t rows, int64_t k, int64_t total_cb, int cus) {
+    static const int env_steps = gemv_override("EXL3_GEMV_STEPS");
+    static const int env_waves = gemv_override("EXL3_GEMV_WAVES");
+    static const bool env_last = gemv_override("EXL3_GEMV_LAST_ARRIVER") == 1;
     GemvPlan p;
-    p.n_cb = (int)((n + COLS - 1) / COLS);
+    p.n_cb = (int)total_cb;
     const int ksteps = (int)(k / STEP_K);
-    // Aim for >= ~4 waves per CU: small matrices need short k-chunks to spread
-    // over 256 CUs (the partials are small next to the weights either way).
+    const int64_t r = rows < GEMV_MAX_ROWS ? rows : GEMV_MAX_ROWS;
+    // Two waves per SIMD, with four column groups per item first: splitting
+    // columns costs nothing but repeated (L1-hit) tile loads, while shorter
+    // items cost fp32 partials (k-chunks x rows x 256 x 4 bytes per column
+    // block) and finish loads.  Measured at 1, 16, 32 and 144 rows on
+    // 4096x4096, 4096x1536, 1536x4096 and 4096x12288: four groups beat one
+    // and two at every shape, 2-step items beat 1-step ones, and the items
+    // this loop picks were the fastest or within 4% of them.
+    const int64_t target = 8LL * cus;
+    const int min_steps = 2;
     int nsteps = GEMV_NSTEP_CAP;
-    while (nsteps > 2 && (int64_t)p.n_cb * (ksteps / nsteps) < 4LL * cus) nsteps /= 2;
+    while (nsteps > min_steps && total_cb * (ksteps / nsteps) * GEMV_MAX_WAVES < target) nsteps /= 2;
+    if (env_steps && ksteps % env_steps == 0) nsteps = env_steps;
     while (ksteps % nsteps) nsteps /= 2;
-    if (nsteps < 2) nsteps = 2;
+    const int64_t items = total_cb * (ksteps / nsteps);
+    int waves = GEMV_MAX_WAVES;
+    while (waves > 1 && items * (waves / 2) >= target) waves /= 2;
+    if (env_waves && env_waves <= GEMV_MAX_WAVES) waves = env_waves;
+    if (r > MAX_ROWS && waves < 2) waves = 2;    // 32-row blocks are built for 2 and 4 groups
     p.nsteps = nsteps;
     p.n_kc = ksteps / nsteps;
+    p.waves = waves;
     // The last arriver of a 256-column block would sum rows * n_kc partial
     // vectors behind a device-scope counter; beyond a handful, a separate
-    // reduction launch (one wave per column block and row) is shorter.
-    p.split_reduce = (int64_t)(rows < MAX_ROWS ? rows : MAX_ROWS) * p.n_kc > 4;
+    // reduction launch is shorter.
+    p.split_reduce = r * p.n_kc > 4 && !env_last;
     return p;
+}
+
+inline GemvPlan gemv_plan(int64_t rows, int64_t k, int64_t n, int cus) {
+    return gemv_plan_cb(rows, k, (n + COLS - 1) / COLS, cus);
+}
+
+// Split-K partials of a matrix: [column block][row][k-chunk][256] fp32, so
+// the finish of one (column block, row) reads its k-chunks from one
+// contiguous range (strided reads of the same offset in every k-chunk all
+// fell on a few memory channels).
+inline int64_t gemv_partial_bytes(int64_t rows, int64_t n_cb, int64_t n_kc) {
+    return n_cb * (rows < GEMV_MAX_ROWS ? rows : GEMV_MAX_ROWS) * n_kc * COLS * 4;
+}
+__device__ __forceinline__ size_t gemv_partial_off(int cb, int row, int kc, int R, int n_kc) {
+    return ((size_t)(cb * R + row) * n_kc + kc) * COLS;
 }
 
 inline int64_t gemv_scratch_bytes(int64_t rows, int64_t k, int64_t n, int cus) {
     const GemvPlan p = gemv_plan(rows, k, n, cus);
     const int64_t ctr = align_up((int64_t)p.n_cb * 4, 256);
-    return ctr + (int64_t)p.n_kc * (rows < 16 ? rows : 16) * n * 4;
+    return ctr + gemv_partial_bytes(rows, p.n_cb, p.n_kc);
 }
 
-// Partial sums of one (256-column block cb, k-chunk kc) item of
-// y = had_in(x) . Wq for rows 0..R-1, stored as fp32 to
-// partials[kc][row][N] (DEV: device-scope stores, read in the same launch;
-// otherwise plain stores, read by a later launch).  xa: the block's LDS.
-template <int BITS, int CB, bool DEV>
-__device__ __forceinline__ void gemv_partials(const uint16_t* __restrict__ x, const int16_t* __restrict__ trellis,
-                                              const uint16_t* __restrict__ suh, int R, int K, int N, int nsteps,
-                                              int cb, int kc, float* __restrict__ partials, uint16_t* xa) {
+// Input rotation of one item: rows 0..R-1, k in [k0, k0 + span), into the LDS
+// A tile, by the item's W waves.  A job is (row, 128-block); for a 64-row
+// item the block is rotated whole and its other half dropped.  A batch's
+// loads are all issued before its arithmetic.
+constexpr int ROT_BATCH = 16;
+
+struct RotJobs {
+    int kb0, nblk, jobs, span;
+};
+struct RotBatch {
+    uint32_t x[ROT_BATCH], s[ROT_BATCH];
+};
+
+__device__ __forceinline__ RotJobs rot_jobs(int k0, int nsteps, int R) {
+    RotJobs j;
+    j.span = nsteps * STEP_K;
+    j.kb0 = k0 & ~127;
+    j.nblk = (k0 + j.span - j.kb0 + 127) >> 7;
+    j.jobs = R * j.nblk;
+    return j;
+}
+
+__device__ __forceinline__ void rot_load(const uint16_t* x, int K, const uint16_t* suh, const RotJobs& J, int j0,
+                                         int stride, RotBatch& b) {
+    const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+    for (int i = 0; i < ROT_BATCH; ++i) {
+        const int j = j0 + i * stride;
+        if (j < J.jobs) {
+            const int m = j / J.nblk, blk = j - m * J.nblk;
+            const int kk = J.kb0 + 128 * blk + 2 * lane;
+            b.x[i] = *reinterpret_cast<const uint32_t*>(x + (size_t)m * K + kk);
+            b.s[i] = *reinterpret_cast<const uint32_t*>(suh + kk);
+        }
+    }
+}
+
+__device__ __forceinline__ void rot_store(const RotJobs& J, int k0, int j0, int stride, const RotBatch& b,
+                                          uint16_t* xa) {
+    const int lane = threadIdx.x & (WAVE - 1);
+#pragma unroll
+    for (int i = 0; i < ROT_BATCH; ++i) {
+        const int j = j0 + i * stride;
+        if (j < J.jobs) {
+            const int m = j / J.nblk, blk = j - m * J.nblk;
+            const uint32_t h = had_in_pair(b.x[i], b.s[i], 0);
+            const int kr = J.kb0 + 128 * blk + 2 * lane - k0;   // even: both halves in one step
+            if (kr >= 0 && kr < J.span) {
+                xa[xa_index(m, kr >> 6, GEMV_NSTEP_CAP, kr & 63)] = (uint16_t)(h & 0xffffu);
+                xa[xa_index(m, kr >> 6, GEMV_NSTEP_CAP, (kr & 63) + 1)] = (uint16_t)(h >> 16);
+            }
+        }
+    }
+}
+
+// Decodes output columns [N0, N0+NC) of each n-tile of the lane's tile and
+// accumulates them into each of the RB 16-row blocks (acc[rb][j] = column
+// N0 + j); the MFMA sequence per column and row block is the one mma_tile
+// issues.
+template <int BITS, int CB, int N0, int NC, int RB>
+__device__ __forceinline__ void mma_tile_cols(const uint32_t* W, const half8_t (&A)[RB][4],
+                                              float4_t (&acc)[RB][NC]) {
+    static_for<NC>([&](auto JI) {
+        constexpr int j = decltype(JI)::value;
+        constexpr int n = N0 + j;
+        static_for<4>([&](auto RI) {
+            constexpr int r = decltype(RI)::value;
+            constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+            u32x4_t b;
+            b[0] = decode_pair<BITS, CB, T0 + 0>(W);
+            b[1] = decode_pair<BITS, CB, T0 + 1>(W);
+            b[2] = decode_pair<BITS, CB, T0 + 2>(W);
+            b[3] = decode_pair<BITS, CB, T0 + 3>(W);
+#pragma unroll
+            for (int rb = 0; rb < RB; ++rb)
+                acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rb][r], __builtin_bit_cast(half8_t, b),
+                                                                     acc[rb][j], 0, 0, 0);
+        });
+    });
+}
+
+// The item's `nsteps` steps (any count >= 1) for columns [N0, N0+NC).  `first`
+// holds step 0's tile (loaded by the caller); later tiles are loaded one step
+// ahead.  The load two steps on sits behind a branch, unlike mma_steps: the
+// short dense items then keep 2 waves per SIMD resident.
+template <int BITS, int CB, int N0, int NC, int RB>
+__device__ __forceinline__ void gemv_mma(TileRegs<BITS>& first, const u32x4_t* p, int n16, int nsteps, int R,
+                                         const uint16_t* xa, float4_t (&acc)[RB][NC]) {
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int g = lane >> 4, c = lane & 15;
+    const size_t step = (size_t)4 * n16 * tile_vecs<BITS>();
+    // A rows >= R repeat row R-1 (a valid row, no branch): their outputs are never stored
+    int arow[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) arow[rb] = min(16 * rb + c, R - 1);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < NC; ++i) acc[rb][i] = float4_t{0.f, 0.f, 0.f, 0.f};
+    auto step_mma = [&](const TileRegs<BITS>& t, int si) {
+        half8_t A[RB][4];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) A[rb][r] = a_operand(xa, arow[rb], si, GEMV_NSTEP_CAP, g, r);
+        mma_tile_cols<BITS, CB, N0, NC, RB>(t.words(), A, acc);
+    };
+    TileRegs<BITS> second;
+    int s = 0;
+    for (; s + 1 < nsteps; s += 2) {
+        load_tile<BITS>(second, p + (s + 1) * step);
+        step_mma(first, s);
+        if (s + 2 < nsteps) load_tile<BITS>(first, p + (s + 2) * step);
+        step_mma(second, s + 1);
+    }
+    if (nsteps & 1) step_mma(first, s);
+}
+
+// One item by its W waves: fp32 partial sums of rows < R stored to the
+// partials at gemv_partial_off(cb, row, kc) (DEV: device-scope stores, read in the same launch;
+// otherwise plain stores, read by a later launch).  xa: the item's LDS.
+template <int BITS, int CB, int W, int RB, bool DEV>
+__device__ __forceinline__ void gemv_item(const uint16_t* __restrict__ x, const int16_t* __restrict__ trellis,
+                                          const uint16_t* __restrict__ suh, int R, int K, int N, int nsteps, int cb,
+                                          int kc, float* __restrict__ partials, uint16_t* xa) {
+    constexpr int NC = 16 / W;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x / WAVE));
     const int k0 = kc * nsteps * STEP_K;
-    // weights for step 0 are in flight while the input rotation runs
     const u32x4_t* tp = tile_ptr<BITS>(trellis, N / 16, k0 / 16, cb * 16);
+
+    // first rotation batch's loads, then step 0's tile, then the rotation
+    const RotJobs J = rot_jobs(k0, nsteps, R);
+    RotBatch rb;
+    rot_load(x, K, suh, J, w, W, rb);
     TileRegs<BITS> first;
-    rotate_rows_and_load<BITS>(x, K, k0, 0, suh + k0, R >= 32 ? ~0u : (1u << R) - 1u, xa, nsteps * STEP_K / 128,
-                               GEMV_NSTEP_CAP, first, tp);
+    load_tile<BITS>(first, tp);
+    rot_store(J, k0, w, W, rb, xa);
+    for (int j0 = w + W * ROT_BATCH; j0 < J.jobs; j0 += W * ROT_BATCH) {
+        rot_load(x, K, suh, J, j0, W, rb);
+        rot_store(J, k0, j0, W, rb, xa);
+    }
     __syncthreads();
 
-    float4_t acc[16];
-    mma_steps<BITS, CB, false>(first, tp, N / 16, nsteps, xa, GEMV_NSTEP_CAP, R, acc);
+    float4_t acc[RB][NC];
+    if constexpr (W == 1) {
+        gemv_mma<BITS, CB, 0, NC, RB>(first, tp, N / 16, nsteps, R, xa, acc);
+    } else if constexpr (W == 2) {
+        if (w == 0) gemv_mma<BITS, CB, 0, NC, RB>(first, tp, N / 16, nsteps, R, xa, acc);
+        else gemv_mma<BITS, CB, NC, NC, RB>(first, tp, N / 16, nsteps, R, xa, acc);
+    } else {
+        static_assert(W == 4, "1, 2 or 4 waves per item");
+        if (w == 0) gemv_mma<BITS, CB, 0, NC, RB>(first, tp, N / 16, nsteps, R, xa, acc);
+        else if (w == 1) gemv_mma<BITS, CB, NC, NC, RB>(first, tp, N / 16, nsteps, R, xa, acc);
+        else if (w == 2) gemv_mma<BITS, CB, 2 * NC, NC, RB>(first, tp, N / 16, nsteps, R, xa, acc);
+        else gemv_mma<BITS, CB, 3 * NC, NC, RB>(first, tp, N / 16, nsteps, R, xa, acc);
+    }
 
+    // Transpose through LDS (the A tile is free once every wave is past its
+    // MFMAs) so each store instruction writes one contiguous 1 KB row.
+    __syncthreads();
+    float* tbuf = reinterpret_cast<float*>(xa);
+    {
+        const int c = lane & 15, rg = lane >> 4;
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * rb + 4 * rg + i;
+                if (row < R) {
+                    float4_t* t = reinterpret_cast<float4_t*>(tbuf + row * COLS + 16 * c + w * NC);
+#pragma unroll
+                    for (int q = 0; q < NC / 4; ++q)
+                        t[q] = float4_t{acc[rb][4 * q][i], acc[rb][4 * q + 1][i], acc[rb][4 * q + 2][i],
+                                        acc[rb][4 * q + 3][i]};
+                }
+            }
+    }
+    __syncthreads();
     const int cols = min(COLS, N - cb * COLS);
-    store_partials<DEV>(acc, partials + (size_t)kc * R * N + cb * COLS, N, R, cols, reinterpret_cast<float*>(xa));
+    const int n_kc = K / (nsteps * STEP_K);
+    if (4 * lane < cols)
+        for (int row = w; row < R; row += W) {
+            const float4_t v = reinterpret_cast<const float4_t*>(tbuf + row * COLS)[lane];
+            float* d = partials + gemv_partial_off(cb, row, kc, R, n_kc) + 4 * lane;
+            if constexpr (DEV) st_dev4(d, v);
+            else *reinterpret_cast<float4_t*>(d) = v;
+        }
 }
 
 // SPLIT: store the partials and stop (gemv_reduce_kernel finishes them);
-// otherwise the last arriver of each column block finishes it.
-template <int BITS, int CB, bool SPLIT>
-__global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x,
-                                                  const int16_t* __restrict__ trellis,
-                                                  const uint16_t* __restrict__ suh,
-                                                  const uint16_t* __restrict__ svh, void* __restrict__ out,
-                                                  int out_kind, int R, int K, int N, int nsteps, int n_kc,
-                                                  int* __restrict__ counters, float* __restrict__ partials) {
-    __shared__ uint16_t xa[MAX_ROWS * GEMV_NSTEP_CAP * STEP_K];
-    const int lane = threadIdx.x;
+// otherwise the last arriver of each column block finishes it (wave 0).
+template <int BITS, int CB, int W, int RB, bool SPLIT>
+__global__ __launch_bounds__(64 * W) void gemv_kernel(const uint16_t* __restrict__ x,
+                                                      const int16_t* __restrict__ trellis,
+                                                      const uint16_t* __restrict__ suh,
+                                                      const uint16_t* __restrict__ svh, void* __restrict__ out,
+                                                      int out_kind, int R, int K, int N, int nsteps, int n_kc,
+                                                      int* __restrict__ counters, float* __restrict__ partials) {
+    __shared__ uint16_t xa[MAX_ROWS * RB * GEMV_NSTEP_CAP * STEP_K];
     const int cb = blockIdx.x / n_kc, kc = blockIdx.x - cb * n_kc;
-    gemv_partials<BITS, CB, !SPLIT>(x, trellis, suh, R, K, N, nsteps, cb, kc, partials, xa);
+    gemv_item<BITS, CB, W, RB, !SPLIT>(x, trellis, suh, R, K, N, nsteps, cb, kc, partials, xa);
     if constexpr (SPLIT) return;
     publish_fence();
+    __syncthreads();
+    if (threadIdx.x >= WAVE) return;
+    const int lane = threadIdx.x;
     int old = 0;
     if (lane == 0) old = atomicAdd(&counters[cb], 1);
     old = __shfl(old, 0, 64);
@@ -195,7 +425,8 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     for (int m = 0; m < R; ++m) {
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         if (ok) {
-            const float4_t t = sum_partials(partials + (size_t)m * N, (uint32_t)col * 4u, (size_t)R * N, n_kc);
+            const float4_t t = sum_partials(partials + gemv_partial_off(cb, m, 0, R, n_kc),
+                                            (uint32_t)(col - cb * COLS) * 4u, (size_t)COLS, n_kc);
             v[0] = t[0]; v[1] = t[1]; v[2] = t[2]; v[3] = t[3];
         }
         fwht128_x4(v);
@@ -205,46 +436,48 @@ __global__ __launch_bounds__(64) void gemv_kernel(const uint16_t* __restrict__ x
     if (lane == 0) __hip_atomic_store(&counters[cb], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Split-K finish of (256-column block cb, row m): the partials of chunks
+// Split-K finish of (128-column block hb, row m): the partials of chunks
 // 0..n_kc-1 summed in chunk order (as the last-arriver path does), output
-// Hadamard, svh, store.  Plain loads: a previous launch wrote the partials.
+// Hadamard, svh, store; two columns per lane, up to RED_BATCH loads in
+// flight.  Plain loads: a previous launch wrote the partials.
+constexpr int RED_BATCH = 64;
+
 template <int BATCH>
 __device__ __forceinline__ void gemv_reduce_block(const float* __restrict__ partials, const uint16_t* __restrict__ svh,
                                                   void* __restrict__ out, int out_kind, int R, int N, int n_kc,
-                                                  int cb, int m) {
+                                                  int hb, int m) {
     const int lane = threadIdx.x & (WAVE - 1);
-    const int col = cb * COLS + 128 * (lane >> 5) + 4 * (lane & 31);
-    const bool ok = col < N;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (ok) {
-        const float* p = partials + (size_t)m * N + col;
-        const size_t stride = (size_t)R * N;
-        for (int k0 = 0; k0 < n_kc; k0 += BATCH) {
-            float4_t t[BATCH];
+    const int col = hb * 128 + 2 * lane;
+    const uint32_t s2 = *reinterpret_cast<const uint32_t*>(svh + col);
+    const int cb = hb >> 1;
+    const float* p = partials + gemv_partial_off(cb, m, 0, R, n_kc) + (col - cb * COLS);
+    const size_t stride = COLS;
+    float v0 = 0.f, v1 = 0.f;
+    for (int k0 = 0; k0 < n_kc; k0 += BATCH) {
+        float2 t[BATCH];
 #pragma unroll
-            for (int j = 0; j < BATCH; ++j)
-                t[j] = k0 + j < n_kc ? *reinterpret_cast<const float4_t*>(p + (size_t)(k0 + j) * stride)
-                                     : float4_t{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < BATCH; ++j)
+            if (k0 + j < n_kc) t[j] = *reinterpret_cast<const float2*>(p + (size_t)(k0 + j) * stride);
 #pragma unroll
-            for (int j = 0; j < BATCH; ++j)
-                if (k0 + j < n_kc)
-                    for (int e = 0; e < 4; ++e) v[e] = v[e] + t[j][e];
-        }
+        for (int j = 0; j < BATCH; ++j)
+            if (k0 + j < n_kc) {
+                v0 = v0 + t[j].x;
+                v1 = v1 + t[j].y;
+            }
     }
-    fwht128_x4(v);
-    if (ok)
-        for (int e = 0; e < 4; ++e)
-            store_out(out, (size_t)m * N + col + e, out_kind, v[e] * HAD_NORM * f16_bits_to_f32(svh[col + e]));
+    fwht128_x2(v0, v1);
+    store_out(out, (size_t)m * N + col, out_kind, v0 * HAD_NORM * f16_bits_to_f32(s2 & 0xffffu));
+    store_out(out, (size_t)m * N + col + 1, out_kind, v1 * HAD_NORM * f16_bits_to_f32(s2 >> 16));
 }
 
-// Split-K finish, one wave per (256-column block, row).  Runs after
+// Split-K finish, one wave per (128-column block, row).  Runs after
 // gemv_kernel<.., true> on the same stream.
 template <int BATCH>
 __global__ __launch_bounds__(64) void gemv_reduce_kernel(const float* __restrict__ partials,
                                                          const uint16_t* __restrict__ svh, void* __restrict__ out,
                                                          int out_kind, int R, int N, int n_kc) {
-    const int cb = blockIdx.x / R, m = blockIdx.x - (blockIdx.x / R) * R;
-    gemv_reduce_block<BATCH>(partials, svh, out, out_kind, R, N, n_kc, cb, m);
+    const int hb = blockIdx.x / R, m = blockIdx.x - (blockIdx.x / R) * R;
+    gemv_reduce_block<BATCH>(partials, svh, out, out_kind, R, N, n_kc, hb, m);
 }
 
 // ---------------------------------------------------------------- same-input fan
@@ -269,7 +502,7 @@ struct FanParams {
     int N[MAX_FAN];
     int bits[MAX_FAN];
     int block0[MAX_FAN + 1];    // partial-sum items: member j owns [block0[j], block0[j+1])
-    int rblock0[MAX_FAN + 1];   // finish items: member j owns [rblock0[j], rblock0[j+1])
+    int rblock0[MAX_FAN + 1];   // finish items (128 columns x row): member j owns [rblock0[j], rblock0[j+1])
 };
 
 __device__ __forceinline__ int fan_member(const int (&first)[MAX_FAN + 1], int count, int blk) {
@@ -280,36 +513,28 @@ __device__ __forceinline__ int fan_member(const int (&first)[MAX_FAN + 1], int c
 
 // Items of the members with bit width BITS; the other members' items return
 // at once (one launch per width present).
-template <int BITS, int CB>
-__global__ __launch_bounds__(64) void gemv_fan_kernel(FanParams P) {
-    __shared__ uint16_t xa[MAX_ROWS * GEMV_NSTEP_CAP * STEP_K];
+template <int BITS, int CB, int W, int RB>
+__global__ __launch_bounds__(64 * W) void gemv_fan_kernel(FanParams P) {
+    __shared__ uint16_t xa[MAX_ROWS * RB * GEMV_NSTEP_CAP * STEP_K];
     const int j = fan_member(P.block0, P.count, blockIdx.x);
     if (P.bits[j] != BITS) return;
     const int local = blockIdx.x - P.block0[j];
     const int cb = local / P.n_kc, kc = local - (local / P.n_kc) * P.n_kc;
-    gemv_partials<BITS, CB, false>(P.x, P.trellis[j], P.suh[j], P.R, P.K, P.N[j], P.nsteps, cb, kc,
-                                   P.partials[j], xa);
+    gemv_item<BITS, CB, W, RB, false>(P.x, P.trellis[j], P.suh[j], P.R, P.K, P.N[j], P.nsteps, cb, kc, P.partials[j], xa);
 }
 
 template <int BATCH>
 __global__ __launch_bounds__(64) void gemv_fan_reduce_kernel(FanParams P) {
     const int j = fan_member(P.rblock0, P.count, blockIdx.x);
     const int local = blockIdx.x - P.rblock0[j];
-    const int cb = local / P.R, m = local - (local / P.R) * P.R;
-    gemv_reduce_block<BATCH>(P.partials[j], P.svh[j], P.out[j], P.out_kind, P.R, P.N[j], P.n_kc, cb, m);
+    const int hb = local / P.R, m = local - (local / P.R) * P.R;
+    gemv_reduce_block<BATCH>(P.partials[j], P.svh[j], P.out[j], P.out_kind, P.R, P.N[j], P.n_kc, hb, m);
 }
 
-// k-chunking of a fan: as gemv_plan, over the column blocks of every member.
-inline GemvPlan gemv_fan_plan(int64_t k, int64_t total_cb, int cus) {
-    GemvPlan p;
-    p.n_cb = (int)total_cb;
-    const int ksteps = (int)(k / STEP_K);
-    int nsteps = GEMV_NSTEP_CAP;
-    while (nsteps > 2 && total_cb * (ksteps / nsteps) < 4LL * cus) nsteps /= 2;
-    while (ksteps % nsteps) nsteps /= 2;
-    if (nsteps < 2) nsteps = 2;
-    p.nsteps = nsteps;
-    p.n_kc = ksteps / nsteps;
+// k-chunking of a fan: as gemv_plan, over the column blocks of every member;
+// always finished by the reduction launch.
+inline GemvPlan gemv_fan_plan(int64_t rows, int64_t k, int64_t total_cb, int cus) {
+    GemvPlan p = gemv_plan_cb(rows, k, total_cb, cus);
     p.split_reduce = true;
     return p;
 }
@@ -329,6 +554,6 @@ struct GemvArgs {
 // Defined in exl3_dense_inst.hip, one translation unit per BITS.
 template <int BITS> int launch_dequant(const DequantArgs& a);
 template <int BITS> int launch_gemv(const GemvArgs& a);
-template <int BITS> int launch_gemv_fan(const FanParams& P, int codebook, int blocks, hipStream_t stream);
+template <int BITS> int launch_gemv_fan(const FanParams& P, int codebook, int waves, int blocks, hipStream_t stream);
 
 }  // namespace exl3

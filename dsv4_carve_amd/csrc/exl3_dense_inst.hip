@@ -30,19 +30,32 @@ int launch_dequant<EXL3_BITS>(const DequantArgs& a) {
     return check_launch();
 }
 
+template <int B, int C, int W, int RB>
+static void launch_gemv_w(const GemvArgs& a) {
+    const dim3 grid(a.plan.n_cb * a.plan.n_kc), block(64 * W);
+    if (a.plan.split_reduce)
+        hipLaunchKernelGGL((gemv_kernel<B, C, W, RB, true>), grid, block, 0, a.stream, a.x, a.trellis, a.suh,
+                           a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps, a.plan.n_kc, a.counters,
+                           a.partials);
+    else
+        hipLaunchKernelGGL((gemv_kernel<B, C, W, RB, false>), grid, block, 0, a.stream, a.x, a.trellis, a.suh,
+                           a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps, a.plan.n_kc, a.counters,
+                           a.partials);
+}
+
+// Up to 16 rows: one MFMA row block, 1, 2 or 4 column groups; 17-32 rows:
+// two row blocks, 2 or 4 column groups (the plan never picks 1 there).
 template <>
 int launch_gemv<EXL3_BITS>(const GemvArgs& a) {
     constexpr int B = EXL3_BITS;
     auto go = [&](auto cbc) {
         constexpr int C = decltype(cbc)::value;
-        if (a.plan.split_reduce)
-            hipLaunchKernelGGL((gemv_kernel<B, C, true>), dim3(a.plan.n_cb * a.plan.n_kc), dim3(64), 0, a.stream,
-                               a.x, a.trellis, a.suh, a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps,
-                               a.plan.n_kc, a.counters, a.partials);
-        else
-            hipLaunchKernelGGL((gemv_kernel<B, C, false>), dim3(a.plan.n_cb * a.plan.n_kc), dim3(64), 0, a.stream,
-                               a.x, a.trellis, a.suh, a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps,
-                               a.plan.n_kc, a.counters, a.partials);
+        if (a.R > MAX_ROWS) {
+            if (a.plan.waves == 4) launch_gemv_w<B, C, 4, 2>(a);
+            else launch_gemv_w<B, C, 2, 2>(a);
+        } else if (a.plan.waves == 4) launch_gemv_w<B, C, 4, 1>(a);
+        else if (a.plan.waves == 2) launch_gemv_w<B, C, 2, 1>(a);
+        else launch_gemv_w<B, C, 1, 1>(a);
     };
     switch (a.codebook) {
         case CB_MCG: go(std::integral_constant<int, CB_MCG>{}); break;
@@ -53,11 +66,17 @@ int launch_gemv<EXL3_BITS>(const GemvArgs& a) {
 }
 
 template <>
-int launch_gemv_fan<EXL3_BITS>(const FanParams& P, int codebook, int blocks, hipStream_t stream) {
+int launch_gemv_fan<EXL3_BITS>(const FanParams& P, int codebook, int waves, int blocks, hipStream_t stream) {
     constexpr int B = EXL3_BITS;
     auto go = [&](auto cbc) {
         constexpr int C = decltype(cbc)::value;
-        hipLaunchKernelGGL((gemv_fan_kernel<B, C>), dim3(blocks), dim3(64), 0, stream, P);
+        const dim3 grid(blocks);
+        if (P.R > MAX_ROWS) {
+            if (waves == 4) hipLaunchKernelGGL((gemv_fan_kernel<B, C, 4, 2>), grid, dim3(256), 0, stream, P);
+            else hipLaunchKernelGGL((gemv_fan_kernel<B, C, 2, 2>), grid, dim3(128), 0, stream, P);
+        } else if (waves == 4) hipLaunchKernelGGL((gemv_fan_kernel<B, C, 4, 1>), grid, dim3(256), 0, stream, P);
+        else if (waves == 2) hipLaunchKernelGGL((gemv_fan_kernel<B, C, 2, 1>), grid, dim3(128), 0, stream, P);
+        else hipLaunchKernelGGL((gemv_fan_kernel<B, C, 1, 1>), grid, dim3(64), 0, stream, P);
     };
     switch (codebook) {
         case CB_MCG: go(std::integral_constant<int, CB_MCG>{}); break;

@@ -99,12 +99,32 @@ def test_gemm_c0_config(ops, dev):
     assert_close(got, ref, what="C0")
 
 
-@pytest.mark.parametrize("rows", [17, 40])
+@pytest.mark.parametrize("rows", [17, 31, 32, 33, 40, 64, 100, 144])
 def test_gemm_many_rows(ops, dev, rows):
+    """More than 16 rows run in 32-row blocks (two MFMA row blocks per
+    decoded step), the last block ragged."""
     import torch
 
     got, ref = _gemm_case(ops, dev, 256, 512, 3, rows, torch.float32)
     assert_close(got, ref, what=f"rows={rows}")
+
+
+@pytest.mark.parametrize("bits,rows", [(2, 1), (6, 20), (4, 37), (3, 16)])
+def test_gemm_half_column_block(ops, dev, bits, rows):
+    """n = 640: the last 256-column block holds 128 columns; k = 384: six
+    64-row steps, so items of 2 steps."""
+    import torch
+
+    got, ref = _gemm_case(ops, dev, 384, 640, bits, rows, torch.float32, seed=77)
+    assert_close(got, ref, what=f"384x640 K{bits} rows={rows}")
+
+
+@pytest.mark.parametrize("k,n,bits,rows", [(4096, 4096, 6, 32), (4096, 1536, 2, 144), (1536, 4096, 3, 48)])
+def test_gemm_baseline_shapes_many_rows(ops, dev, k, n, bits, rows):
+    import torch
+
+    got, ref = _gemm_case(ops, dev, k, n, bits, rows, torch.float32, seed=k + n + rows)
+    assert_close(got, ref, what=f"{k}x{n} K{bits} rows={rows}")
 
 
 @pytest.mark.parametrize("out_dtype", ["float16", "bfloat16"])

@@ -47,7 +47,7 @@ def _run(fan, dev, rows, seed, out_dtype=None):
     return x, xd, outs
 
 
-@pytest.mark.parametrize("rows", [1, 2, 5, 16, 21])
+@pytest.mark.parametrize("rows", [1, 2, 5, 16, 21, 32, 45])
 def test_mixed_fan_against_oracle_and_solo(dev, rows):
     import torch
     from dsv4_carve_amd import ops
