@@ -82,7 +82,11 @@ constexpr int64_t PLAN_BYTES = 4096;          // bound on the route plan (LDS)
 __host__ __device__ inline int64_t al(int64_t v) { return (v + 255) / 256 * 256; }
 
 // stepsA/stepsB: steps per gate/up and per down item (2, 4 or 8; the scratch
-// size is taken at 2, the most partials).
+// size is taken at 2, the most partials).  Split-K partials are fp32
+// PA [pair][projection][I-block][k-chunk][256] and PB [pair][H-block][k-chunk][256]:
+// the finish of one (pair, column block) reads its k-chunks from one
+// contiguous range (the same offset read in every k-chunk of a
+// [k-chunk][columns] layout fell on a few memory channels).
 __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2, int stepsB = 2) {
     Layout L;
     L.nI = I / COLS;
@@ -423,7 +427,7 @@ __device__ __forceinline__ void gateup_partials(const Params& P, int e, int pb, 
     }
 
     float* PA = at<float>(P.scratch, L.PA);
-    store_partials<DEV>(acc, PA + ((size_t)((rowmap ? 0 : pb) * 2 + p) * L.SA + kc) * P.I + cb * COLS,
+    store_partials<DEV>(acc, PA + ((((size_t)(rowmap ? 0 : pb) * 2 + p) * L.nI + cb) * L.SA + kc) * COLS,
                         (size_t)2 * L.SA * P.I, R, COLS, reinterpret_cast<float*>(xa), rowmap);
 }
 
@@ -440,8 +444,10 @@ __device__ __forceinline__ uint2 down_input4(const Params& P, int pair, int col,
     float4_t ga, ua;
     // uniform buffer bases, the pair in the per-lane offset: `pair` may differ
     // between the half-waves (< 1 GB of partials, inside the 32-bit offset)
-    sum_partials2<CPOL>(PA, PA + (size_t)L.SA * P.I, ((uint32_t)pair * 2u * (uint32_t)(L.SA * P.I) + (uint32_t)col) * 4u,
-                        P.I, L.SA, ga, ua);
+    const uint32_t cb = (uint32_t)col / COLS, c = (uint32_t)col % COLS;
+    sum_partials2<CPOL>(PA, PA + (size_t)L.SA * P.I,
+                        ((uint32_t)pair * 2u * (uint32_t)(L.SA * P.I) + cb * (uint32_t)(L.SA * COLS) + c) * 4u,
+                        COLS, L.SA, ga, ua);
     float gv[4] = {ga[0], ga[1], ga[2], ga[3]}, uv[4] = {ua[0], ua[1], ua[2], ua[3]};
     fwht128_x4(gv);
     fwht128_x4(uv);
@@ -503,7 +509,7 @@ __device__ __forceinline__ void down_partials(const Params& P, int pb, int R, ui
     }
 
     float* PB = at<float>(P.scratch, L.PB);
-    store_partials<DEV>(acc, PB + ((size_t)pb * L.SB + kc) * P.H + cb * COLS, (size_t)L.SB * P.H, R, COLS,
+    store_partials<DEV>(acc, PB + (((size_t)pb * L.nH + cb) * L.SB + kc) * COLS, (size_t)L.SB * P.H, R, COLS,
                         reinterpret_cast<float*>(xa));
 }
 
@@ -512,8 +518,9 @@ __device__ __forceinline__ void down_partials(const Params& P, int pb, int R, ui
 template <int CPOL>
 __device__ __forceinline__ float4_t down_value(const Params& P, int pair, const uint16_t (&dsv)[4], int col) {
     const Layout& L = P.L;
+    const uint32_t cb = (uint32_t)col / COLS, c = (uint32_t)col % COLS;
     const float4_t t = sum_partials<CPOL>(at<float>(P.scratch, L.PB) + (size_t)pair * L.SB * P.H,
-                                          (uint32_t)col * 4u, P.H, L.SB);
+                                          (cb * (uint32_t)(L.SB * COLS) + c) * 4u, COLS, L.SB);
     float v[4] = {t[0], t[1], t[2], t[3]};
     fwht128_x4(v);
     float4_t o;
@@ -944,7 +951,7 @@ __global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
             mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, g.R, acc);
             tr(EV_B_MMA);
         }
-        store_partials<false>(acc, at<float>(P.scratch, L.PB) + (size_t)kc * P.H + cb * COLS, (size_t)L.SB * P.H,
+        store_partials<false>(acc, at<float>(P.scratch, L.PB) + ((size_t)cb * L.SB + kc) * COLS, (size_t)L.SB * P.H,
                               g.R, COLS, reinterpret_cast<float*>(xa), pslot);
     });
     tr(EV_B_END);
