@@ -518,6 +518,65 @@ def time_read_ceiling(dev, gib: int = 2, reps: int = 10) -> dict:
             **res}
 
 
+def time_decode_ceiling(dev, iters: int = 512, reps: int = 5) -> dict:
+    """Decode-rate ceiling: the decode kernels' inner loop (decode + MFMA on
+    tiles held in registers, csrc/exl3_probe.hip) at their residency of two
+    single-wave workgroups per SIMD, per bit width.  Returns the decoded
+    weights per second (median of `reps` timed launches after one warm-up),
+    the shader clock the loop ran at, and the SIMD cycles it spends per 64
+    weights (one weight per lane)."""
+    import ctypes
+
+    import torch
+    from dsv4_carve_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_LIB)
+    lib.exl3_probe_decode.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    lib.exl3_probe_decode.restype = ctypes.c_int
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    simds = 4 * cus
+    blocks = 2 * simds
+    g = torch.Generator().manual_seed(11)
+    words = torch.randint(0, 2 ** 31 - 1, (64 * 8 * 6,), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
+    sink = torch.empty(blocks * 64, dtype=torch.float32, device=dev)
+    clk = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    stream = int(torch.cuda.current_stream(dev).cuda_stream)
+    res = {}
+    for bits in (2, 3, 4, 6):
+        times = []
+        for _ in range(reps + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            assert lib.exl3_probe_decode(bits, blocks, iters, words.data_ptr(), sink.data_ptr(), clk.data_ptr(),
+                                         stream) == 0
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) * 1e-3)
+        t = sorted(times[1:])[reps // 2]
+        c = clk.view(blocks, 2).double().sum(0).tolist()
+        ghz = c[0] / c[1] * 0.1                      # reference ticks at 100 MHz
+        weights = blocks * iters * 16384.0
+        res[f"K{bits}"] = {"Gweights_per_s": round(weights / t / 1e9, 1), "clock_GHz": round(ghz, 3),
+                           "simd_cycles_per_64_weights": round(t * ghz * 1e9 * simds / (weights / 64.0), 2)}
+    del words, sink, clk
+    return {"workgroups": blocks, "iters": iters, "codebook": "MCG", **res}
+
+
+def decode_floor_us(rate: dict, rows: int, bits: list[int], hidden: int, inter: int, topk: int, seed: int) -> float:
+    """Lower bound on one routed layer's time from the decode rate alone: the
+    mean, over the headline's routing pool, of each distinct expert's
+    3*hidden*inter weights divided by its width's decode rate."""
+    from dsv4_carve_amd import synth
+
+    per = []
+    for i in range(POOL):
+        ids = synth.routing(rows, len(bits), topk, seed=seed * 1000 + i)[0]
+        active = {int(e) for e in ids.reshape(-1) if 0 <= e < len(bits)}
+        per.append(sum(3.0 * hidden * inter / (rate[f"K{bits[e]}"]["Gweights_per_s"] * 1e9) for e in active))
+    return float(np.mean(per)) * 1e6
+
+
 CPU_SAMPLE = 10          # experts per bit width timed on the CPU
 
 
@@ -603,6 +662,13 @@ def main() -> int:
     if "ceiling" in legs:
         extra["hbm_read_ceiling"] = time_read_ceiling(dev)
         print(f"[bench] read ceiling: {extra['hbm_read_ceiling']}", file=sys.stderr, flush=True)
+        dc = time_decode_ceiling(dev)
+        floor = decode_floor_us(dc, a.rows, layer.bits, HIDDEN, INTER, TOPK, seed=a.rows)
+        mem = nbytes / (extra["hbm_read_ceiling"]["best_p50_GBps"] * 1e9) * 1e6
+        dc[f"layer_floor_us_rows{a.rows}"] = {"decode": round(floor, 1), "memory_at_read_ceiling": round(mem, 1),
+                                              "measured": round(us, 1)}
+        extra["decode_ceiling"] = dc
+        print(f"[bench] decode ceiling: {dc}", file=sys.stderr, flush=True)
     if "sweep" in legs:
         sweep = {}
         for m in (1, 2, 4, 8, 16):

@@ -1,15 +1,27 @@
-// HBM read-ceiling probe for the benchmark (not part of the decode path's ABI).
+// Ceiling probes for the benchmark (not part of the decode path's ABI).
 //
+// 1. HBM read ceiling.
 // Streams `bytes` of a device buffer once with 16-byte loads, eight in flight
 // per lane, and folds them into one word per lane so no load is dead.  Timed
 // by the caller on `stream`; with the buffer far larger than the 256 MB
 // Infinity Cache and a flush between runs, the rate is the achievable cold
 // read bandwidth that the decode kernels' weight streams are measured against
 // (the role of recipe-lna/lna2/cold_read_bw.cu:23-153 on the reference's card).
+//
+// 2. Decode-rate ceiling.  The decode kernels' inner loop (exl3_gemv.hpp
+// mma_tile: trellis windows, codebook, MFMA accumulate) run on tiles that stay
+// in registers, with no memory traffic and no item overheads, at the decode
+// kernels' residency (single-wave workgroups, two per SIMD).  Its rate in
+// decoded weights per second bounds any launch built on that loop: a layer of
+// W weights cannot finish in less than W / rate, whatever the memory system
+// delivers.  The tile words are made opaque to the compiler every iteration,
+// so each iteration decodes and multiplies all 256 weights of the lane's tile.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+#include "exl3_gemv.hpp"
+
+using exl3::u32x4_t;
 
 constexpr int PROBE_THREADS = 256;
 constexpr int PROBE_UNROLL = 8;
@@ -32,6 +44,38 @@ __global__ __launch_bounds__(PROBE_THREADS) void probe_read_kernel(const u32x4_t
     sink[tid] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
+template <int BITS>
+__global__ __launch_bounds__(64, 2) void probe_decode_kernel(const uint32_t* __restrict__ words, int iters,
+                                                            float* __restrict__ sink, uint64_t* __restrict__ clk) {
+    using namespace exl3;
+    const int lane = threadIdx.x;
+    uint32_t W[8 * BITS];
+#pragma unroll
+    for (int i = 0; i < 8 * BITS; ++i) W[i] = words[lane * 8 * BITS + i];
+    half8_t A[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) A[r][j] = (_Float16)((float)((lane + 3 * r + j) & 7) * 0.125f - 0.4375f);
+    float4_t acc[16];
+    zero_acc(acc);
+    const uint64_t c0 = __builtin_amdgcn_s_memtime(), t0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 8 * BITS; ++i) asm volatile("" : "+v"(W[i]));
+        mma_tile<BITS, CB_MCG>(W, A, acc);
+    }
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), t1 = __builtin_amdgcn_s_memrealtime();
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sum += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+    sink[blockIdx.x * 64 + lane] = sum;
+    if (lane == 0) {
+        clk[2 * blockIdx.x] = c1 - c0;
+        clk[2 * blockIdx.x + 1] = t1 - t0;
+    }
+}
+
 extern "C" {
 
 // Launches the probe over bytes (a multiple of 16) at buf; sink holds one
@@ -45,5 +89,25 @@ int exl3_probe_read(const void* buf, int64_t bytes, uint32_t* sink, int blocks, 
 }
 
 int exl3_probe_threads(void) { return PROBE_THREADS; }
+
+// Launches `blocks` single-wave workgroups of the decode-rate probe at `bits`
+// (2, 3, 4 or 6; MCG codebook), each decoding 16384 weights per iteration for
+// `iters` iterations.  words: 64 * 8 * bits uint32 of tile data (any values);
+// sink: blocks * 64 floats; clk: 2 * blocks uint64 (per workgroup the shader
+// clock cycles and the 100 MHz reference ticks of its loop, which give the
+// clock the loop ran at).  Returns 0, or -1 on a bad argument or launch error.
+int exl3_probe_decode(int bits, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                      void* stream) {
+    if (!words || !sink || !clk || blocks < 1 || iters < 1) return -1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    switch (bits) {
+        case 2: hipLaunchKernelGGL(probe_decode_kernel<2>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
+        case 3: hipLaunchKernelGGL(probe_decode_kernel<3>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
+        case 4: hipLaunchKernelGGL(probe_decode_kernel<4>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
+        case 6: hipLaunchKernelGGL(probe_decode_kernel<6>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
+        default: return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 }  // extern "C"
