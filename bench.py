@@ -111,7 +111,7 @@ def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, 
     wts = torch.tensor(np.stack([p[1] for p in pool]), dtype=torch.float32, device=dev)
     x = torch.from_numpy(synth.activations(rows, layer.hidden, seed=seed)).to(dev)
     out = torch.empty((rows, layer.hidden), dtype=torch.float32, device=dev)
-    scratch = ops.moe_scratch(dev, layer.hidden, layer.inter, topk)
+    scratch = ops.moe_scratch(dev, layer.hidden, layer.inter, topk, rows=rows)
 
     def launch(i):
         ops.moe_decode(x, out, layer.tables, ids[i % POOL], wts[i % POOL], intermediate=layer.inter,
@@ -158,7 +158,7 @@ def layer_latency(layer, dev, rows, topk, iters, seed, cold: bool) -> dict:
     wts = torch.tensor(np.stack([p[1] for p in pool]), dtype=torch.float32, device=dev)
     x = torch.from_numpy(synth.activations(rows, layer.hidden, seed=seed)).to(dev)
     out = torch.empty((rows, layer.hidden), dtype=torch.float32, device=dev)
-    scratch = ops.moe_scratch(dev, layer.hidden, layer.inter, topk)
+    scratch = ops.moe_scratch(dev, layer.hidden, layer.inter, topk, rows=rows)
     probe = ctypes.CDLL(B.PROBE_LIB)
     probe.exl3_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     flush = torch.ones((1 << 30) // 4, dtype=torch.int32, device=dev) if cold else None
@@ -344,15 +344,17 @@ def time_dense(dev, k, n, bits, rows_list, steps=40):
 MFMA_PEAK_F16 = 2.5e15
 
 
-def time_prefill(layer, dev, tokens, topk, steps, warmup, seed):
+def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True):
     """Prefill-shaped layer (grouped GEMMs): us per layer over `tokens` tokens
-    with Zipf(1.1) top-k routing, fresh routing each step from a pool of 4.
+    with Zipf(1.1) top-k routing (`zipf`; otherwise the decode benchmark's
+    N(0,1)-logit routing), fresh routing each step from a pool of 4.
     Returns (us, algorithmic flops, algorithmic bytes, mean distinct experts)."""
     import torch
     from dsv4_carve_amd import ops, synth
 
     n_exp = len(layer.bits)
-    pool = [synth.zipf_routing(tokens, n_exp, topk, seed=seed + i) for i in range(4)]
+    route = synth.zipf_routing if zipf else synth.routing
+    pool = [route(tokens, n_exp, topk, seed=seed + i) for i in range(4)]
     ids = [torch.from_numpy(p[0]).to(dev) for p in pool]
     wts = [torch.from_numpy(p[1]).to(dev) for p in pool]
     x = torch.from_numpy(synth.activations(tokens, layer.hidden, seed=seed)).to(dev)
@@ -614,7 +616,7 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
     }
 
 
-EXTRA_LEGS = ("ceiling", "sweep", "tp8", "prefill", "stack", "dense", "fan", "glue")
+EXTRA_LEGS = ("ceiling", "sweep", "rows17", "tp8", "prefill", "stack", "dense", "fan", "glue")
 
 
 def main() -> int:
@@ -679,6 +681,17 @@ def main() -> int:
                              "warm_us": round(uw, 2), "warm_GBps": round(bw / (uw * 1e-6) / 1e9, 1)}
             print(f"[bench] sweep m={m}: {sweep[str(m)]}", file=sys.stderr, flush=True)
         extra["rows_sweep"] = sweep
+    if "rows17" in legs:
+        # 17-32 rows (the reference's lna2 takes up to 24): the decode
+        # launches, and the grouped-GEMM (prefill) path on the same routing.
+        big = {}
+        for m in (17, 20, 24, 32):
+            u, b = time_layer(layer, dev, m, TOPK, a.steps, 3, seed=m)
+            up, _, _, _ = time_prefill(layer, dev, m, TOPK, 20, 2, seed=m * 1000, zipf=False)
+            big[str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1),
+                           "frac": round(b / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "grouped_gemm_us": round(up, 2)}
+            print(f"[bench] rows m={m}: {big[str(m)]}", file=sys.stderr, flush=True)
+        extra["rows_17_32"] = big
     if "tp8" in legs:
         # The reference's own geometry: one GPU's share of the layer under TP8
         # (hidden 4096, intermediate 256, top-6, all experts at one width).

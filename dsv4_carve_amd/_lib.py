@@ -21,6 +21,7 @@ EXPORTS = (
     "exl3_gemm_group_scratch_bytes",
     "exl3_gemm_group",
     "exl3_moe_scratch_bytes",
+    "exl3_moe_scratch_bytes_rows",
     "exl3_moe_max_rows",
     "exl3_moe_error_offset",
     "exl3_moe_decode",
@@ -49,6 +50,7 @@ _SIGS = {
     "exl3_gemm_group_scratch_bytes": ([_L, _L, _L, _P], _L),
     "exl3_gemm_group": ([_P, _L, _L, _L, _P, _P, _P, _P, _P, _I, _P, _I, _P, _L, _P], _I),
     "exl3_moe_scratch_bytes": ([_L, _L, _L], _L),
+    "exl3_moe_scratch_bytes_rows": ([_L, _L, _L, _L], _L),
     "exl3_moe_max_rows": ([], _I),
     "exl3_moe_error_offset": ([], _L),
     "exl3_moe_decode": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,

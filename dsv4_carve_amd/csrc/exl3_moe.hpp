@@ -49,9 +49,16 @@
 namespace exl3 {
 namespace moe {
 
-constexpr int MAX_M = 16;
+// Rows per call: up to 32 on the phased launches (the reference's lna2 takes
+// 24, lna_moe_ticket.cu:40-51), up to 16 on the ticket kernel, whose route
+// plan and control words are sized for 16.  The scratch size function without
+// a row count covers 16 rows; larger batches ask exl3_moe_scratch_bytes_rows.
+constexpr int MAX_M = 32;
+constexpr int TICKET_MAX_M = 16;
+constexpr int SCRATCH_ROWS = 16;
 constexpr int MAX_TOPK = 9;                   // e.g. 8 routed slots + a shared expert
-constexpr int MAX_SLOTS = MAX_M * MAX_TOPK;   // also the bound on groups and pairs
+constexpr int MAX_SLOTS = TICKET_MAX_M * MAX_TOPK;   // ticket kernel: bound on groups and pairs
+constexpr int PHASED_MAX_SLOTS = MAX_M * MAX_TOPK;   // phased launches: slots of one call
 constexpr int MAX_EXPERTS = 2048;             // route-plan bitmask capacity
 constexpr int MAX_BLOCKS = 64;                // hidden/256 and intermediate/256 (both <= 16384)
 constexpr int NSTEP_CAP = 8;
@@ -82,12 +89,14 @@ constexpr int64_t PLAN_BYTES = 4096;          // bound on the route plan (LDS)
 __host__ __device__ inline int64_t al(int64_t v) { return (v + 255) / 256 * 256; }
 
 // stepsA/stepsB: steps per gate/up and per down item (2, 4 or 8; the scratch
-// size is taken at 2, the most partials).  Split-K partials are fp32
+// size is taken at 2, the most partials).  rows: the row capacity the data
+// regions are laid out for (the call's row count, at least 16).  Split-K partials are fp32
 // PA [pair][projection][I-block][k-chunk][256] and PB [pair][H-block][k-chunk][256]:
 // the finish of one (pair, column block) reads its k-chunks from one
 // contiguous range (the same offset read in every k-chunk of a
 // [k-chunk][columns] layout fell on a few memory channels).
-__host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2, int stepsB = 2) {
+__host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2, int stepsB = 2,
+                                        int rows = SCRATCH_ROWS) {
     Layout L;
     L.nI = I / COLS;
     L.nH = H / COLS;
@@ -95,7 +104,7 @@ __host__ __device__ inline Layout layout(int H, int I, int topk, int stepsA = 2,
     L.stepsB = stepsB;
     L.SA = H / STEP_K / L.stepsA;
     L.SB = I / STEP_K / L.stepsB;
-    const int64_t P = (int64_t)MAX_M * topk;      // max pairs = max groups
+    const int64_t P = (int64_t)rows * topk;       // max pairs = max groups
     // The control words sit at fixed offsets with fixed strides whatever the
     // geometry, so one scratch buffer can serve layers of different shapes:
     // every counter is back at zero after a launch and every flag holds an
@@ -691,7 +700,8 @@ __device__ void item_b(const Params& P, const Plan& pl, uint16_t* xa, int t, int
 // partials, 1 KB per row) or the route-plan workspace, whichever is larger.
 // Sized by the batch, so small batches leave room for more resident waves.
 inline int moe_lds_kb(int64_t m, int64_t n_experts) {
-    const int64_t a = m * NSTEP_CAP * STEP_K * 2, b = 6 * n_experts;
+    const int64_t rows = m < MAX_ROWS ? m : MAX_ROWS;     // an item takes at most 16 rows per pass
+    const int64_t a = rows * NSTEP_CAP * STEP_K * 2, b = 6 * n_experts;
     return (int)(((a > b ? a : b) + 1023) / 1024);
 }
 
@@ -782,26 +792,34 @@ struct SlotGroup {
 // Expert of slot o, its rows and each row's pair slot (pslot[r], LDS, for the
 // r-th row in ascending order).  False when slot o holds no valid expert or is
 // not the first slot holding it.
+constexpr int SLOTS_PER_LANE = (PHASED_MAX_SLOTS + WAVE - 1) / WAVE;
 __device__ __forceinline__ bool slot_group(const Params& P, int o, SlotGroup& g, int16_t* pslot) {
     const int lane = threadIdx.x & (WAVE - 1);
-    const int S = P.m * P.topk;                 // <= MAX_SLOTS = 3 * WAVE: three slots per lane
-    static_assert(MAX_SLOTS <= 3 * WAVE, "slot ids fit three per lane");
-    const int sl[3] = {lane, lane + WAVE, lane + 2 * WAVE};
-    int v[3];
+    const int S = P.m * P.topk;                 // <= PHASED_MAX_SLOTS: SLOTS_PER_LANE slots per lane
+    int sl[SLOTS_PER_LANE];
+#pragma unroll
+    for (int i = 0; i < SLOTS_PER_LANE; ++i) sl[i] = lane + i * WAVE;
+    int v[SLOTS_PER_LANE];
     P.rt.local_n(sl, S, P.E, v);
     const int oi = o / WAVE;
-    const int e = __builtin_amdgcn_readlane(oi == 0 ? v[0] : oi == 1 ? v[1] : v[2], o & (WAVE - 1));
-    if (e < 0) return false;
-    uint64_t mk[3];
+    int vo = v[0];
 #pragma unroll
-    for (int i = 0; i < 3; ++i) mk[i] = __ballot(v[i] == e);
-    const int first = mk[0] ? __builtin_ctzll(mk[0])
-                    : mk[1] ? WAVE + __builtin_ctzll(mk[1]) : 2 * WAVE + __builtin_ctzll(mk[2]);
+    for (int i = 1; i < SLOTS_PER_LANE; ++i)
+        if (oi == i) vo = v[i];
+    const int e = __builtin_amdgcn_readlane(vo, o & (WAVE - 1));
+    if (e < 0) return false;
+    uint64_t mk[SLOTS_PER_LANE];
+#pragma unroll
+    for (int i = 0; i < SLOTS_PER_LANE; ++i) mk[i] = __ballot(v[i] == e);
+    int first = -1;
+#pragma unroll
+    for (int i = SLOTS_PER_LANE - 1; i >= 0; --i)
+        if (mk[i]) first = WAVE * i + __builtin_ctzll(mk[i]);
     if (first != o) return false;
     uint32_t mask = 0u;
     int R = 0;
 #pragma unroll
-    for (int i = 0; i < 3; ++i) {
+    for (int i = 0; i < SLOTS_PER_LANE; ++i) {
         uint64_t bits = mk[i];
         while (bits) {
             const int s = WAVE * i + __builtin_ctzll(bits);
@@ -850,6 +868,20 @@ __device__ __forceinline__ void down_input_chunk(const Params& P, int e, int R, 
     }
 }
 
+// The rows of `mask` from the `skip`-th set bit on, at most MAX_ROWS of them:
+// an expert routed by more than 16 rows of a batch runs its item in passes of
+// 16 rows (each pass streams and decodes the item's weights again; the LDS
+// A tile stays at 16 rows, so residency does not depend on the batch).
+__device__ __forceinline__ uint32_t row_pass(uint32_t mask, int skip) {
+    for (int i = 0; i < skip; ++i) mask &= mask - 1u;
+    uint32_t pass = 0u;
+    for (int i = 0; i < MAX_ROWS && mask; ++i) {
+        pass |= mask & (0u - mask);
+        mask &= mask - 1u;
+    }
+    return pass;
+}
+
 // Launch 1: item = (slot, projection, column block of I, k-chunk).
 template <uint32_t MASK, int CB>
 __global__ __launch_bounds__(64, 2) void moe_slot_gateup(Params P) {
@@ -869,7 +901,11 @@ __global__ __launch_bounds__(64, 2) void moe_slot_gateup(Params P) {
     rem -= p * L.nI * L.SA;
     const int cb = rem / L.SA, kc = rem - (rem / L.SA) * L.SA;
     dispatch_bits<MASK>(g.bits, &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
-        gateup_partials<decltype(BI)::value, CB, false>(P, g.e, 0, g.mask, xa, p, cb, kc, tr, pslot);
+        for (int r0 = 0; r0 < g.R; r0 += MAX_ROWS) {
+            if (r0) __syncthreads();                  // the previous pass is done with xa
+            gateup_partials<decltype(BI)::value, CB, false>(P, g.e, 0, row_pass(g.mask, r0), xa, p, cb, kc, tr,
+                                                            pslot + r0);
+        }
     });
     tr(EV_A_END);
 }
@@ -921,38 +957,43 @@ __global__ __launch_bounds__(64, 2) void moe_slot_down(Params P) {
     dispatch_bits<MASK>(g.bits, &at<Ctrl>(P.scratch, L.ctrl)->error, [&](auto BI) {
         constexpr int B = decltype(BI)::value;
         const int kchunk = L.stepsB * STEP_K;
-        float4_t acc[16];
-        if constexpr (B == 0) {
-            zero_acc(acc);
-        } else {
-            const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[g.e]), P.H / 16, kc * kchunk / 16,
-                                            cb * 16);
-            TileRegs<B> first;
-            if (P.fuse_act) {
-                load_tile<B>(first, tp);
-                down_input_chunk(P, g.e, g.R, pslot, xa, kc * kchunk, kchunk);
+        for (int r0 = 0; r0 < g.R; r0 += MAX_ROWS) {
+            const int R = min(g.R - r0, MAX_ROWS);
+            const int16_t* ps = pslot + r0;
+            if (r0) __syncthreads();                  // the previous pass is done with xa
+            float4_t acc[16];
+            if constexpr (B == 0) {
+                zero_acc(acc);
             } else {
-                // the first rows' input is requested before the step-0 tile, so
-                // waiting for it (loads complete in issue order) skips the tile
-                const uint16_t* DI = at<uint16_t>(P.scratch, L.DI) + (size_t)kc * kchunk;
-                uint32_t v[IN_AHEAD][HAD_MAX_BLOCKS];
+                const u32x4_t* tp = tile_ptr<B>(reinterpret_cast<const int16_t*>(P.dt[g.e]), P.H / 16,
+                                                kc * kchunk / 16, cb * 16);
+                TileRegs<B> first;
+                if (P.fuse_act) {
+                    load_tile<B>(first, tp);
+                    down_input_chunk(P, g.e, R, ps, xa, kc * kchunk, kchunk);
+                } else {
+                    // the first rows' input is requested before the step-0 tile, so
+                    // waiting for it (loads complete in issue order) skips the tile
+                    const uint16_t* DI = at<uint16_t>(P.scratch, L.DI) + (size_t)kc * kchunk;
+                    uint32_t v[IN_AHEAD][HAD_MAX_BLOCKS];
 #pragma unroll
-                for (int i = 0; i < IN_AHEAD; ++i)
-                    if (i < g.R) copy_row_load<false>(DI + (size_t)pslot[i] * P.I, kchunk / 128, v[i]);
-                load_tile<B>(first, tp);
+                    for (int i = 0; i < IN_AHEAD; ++i)
+                        if (i < R) copy_row_load<false>(DI + (size_t)ps[i] * P.I, kchunk / 128, v[i]);
+                    load_tile<B>(first, tp);
 #pragma unroll
-                for (int i = 0; i < IN_AHEAD; ++i)
-                    if (i < g.R) copy_row_store(v[i], xa, i, kchunk / 128, NSTEP_CAP);
-                for (int r = IN_AHEAD; r < g.R; ++r)
-                    copy_row<false>(DI + (size_t)pslot[r] * P.I, xa, r, kchunk / 128, NSTEP_CAP);
+                    for (int i = 0; i < IN_AHEAD; ++i)
+                        if (i < R) copy_row_store(v[i], xa, i, kchunk / 128, NSTEP_CAP);
+                    for (int r = IN_AHEAD; r < R; ++r)
+                        copy_row<false>(DI + (size_t)ps[r] * P.I, xa, r, kchunk / 128, NSTEP_CAP);
+                }
+                __syncthreads();
+                tr(EV_B_WAITED);
+                mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, R, acc);
+                tr(EV_B_MMA);
             }
-            __syncthreads();
-            tr(EV_B_WAITED);
-            mma_steps<B, CB, true>(first, tp, P.H / 16, L.stepsB, xa, NSTEP_CAP, g.R, acc);
-            tr(EV_B_MMA);
+            store_partials<false>(acc, at<float>(P.scratch, L.PB) + ((size_t)cb * L.SB + kc) * COLS,
+                                  (size_t)L.SB * P.H, R, COLS, reinterpret_cast<float*>(xa), ps);
         }
-        store_partials<false>(acc, at<float>(P.scratch, L.PB) + ((size_t)cb * L.SB + kc) * COLS, (size_t)L.SB * P.H,
-                              g.R, COLS, reinterpret_cast<float*>(xa), pslot);
     });
     tr(EV_B_END);
 }

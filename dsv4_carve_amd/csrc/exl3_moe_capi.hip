@@ -1,6 +1,8 @@
 // C-ABI entry points of the routed-MoE decode (declared in include/exl3_amd.h):
 //   exl3_moe_decode         <- lna2_moe_decode   recipe-lna/lna2/lna_moe_ticket.cu:507-581
-//   exl3_moe_scratch_bytes  <- lna2_moe_scratch_bytes  :481
+//   exl3_moe_scratch_bytes  <- lna2_moe_scratch_bytes  :481 (16 rows)
+//   exl3_moe_scratch_bytes_rows   (the same for up to `rows` rows; the reference
+//                                  sizes its scratch for LNA2_MAX_M at build time, :40-53)
 //   exl3_moe_max_rows       <- lna2_moe_max_rows       :484
 //   exl3_moe_info           <- lna2_moe_info           :494-505
 //   exl3_moe_decode_noalloc    (no counterpart: the routed decode on a fixed scratch)
@@ -75,10 +77,15 @@ static bool fuse_act(int64_t m, int64_t topk, int64_t intermediate) {
 // device-scope hand-offs) stays available: EXL3_MOE_PHASED_MAX_ROWS, when
 // set, selects by row count (0: always the ticket kernel).
 static bool use_phased(int64_t m) {
+    if (m > TICKET_MAX_M) return true;        // the ticket kernel's plan holds 16 rows
     const char* v = getenv("EXL3_MOE_PHASED_MAX_ROWS");
     if (v && *v) return m <= atoi(v);
     return true;
 }
+
+// Row capacity of a call's data regions: 16 rows (the default scratch) up to
+// 16 rows, else the call's row count.
+static int scratch_rows(int64_t m) { return m > SCRATCH_ROWS ? (int)m : SCRATCH_ROWS; }
 
 }  // namespace moe
 }  // namespace exl3
@@ -88,14 +95,19 @@ using namespace exl3::moe;
 
 extern "C" {
 
-int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk) {
+int64_t exl3_moe_scratch_bytes_rows(int64_t hidden, int64_t intermediate, int64_t topk, int64_t rows) {
     clear_error();
     if (hidden <= 0 || hidden % COLS || intermediate <= 0 || intermediate % COLS)
         return fail("hidden and intermediate must be positive multiples of 256");
     if (hidden > COLS * MAX_BLOCKS || intermediate > COLS * MAX_BLOCKS)
         return fail("hidden and intermediate must be at most 16384");
     if (topk < 1 || topk > MAX_TOPK) return fail("topk must be in 1..9");
-    return layout((int)hidden, (int)intermediate, (int)topk).total + trace_bytes();
+    if (rows < 1 || rows > MAX_M) return fail("row count out of range (1 <= rows <= exl3_moe_max_rows())");
+    return layout((int)hidden, (int)intermediate, (int)topk, 2, 2, scratch_rows(rows)).total + trace_bytes();
+}
+
+int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk) {
+    return exl3_moe_scratch_bytes_rows(hidden, intermediate, topk, SCRATCH_ROWS);
 }
 
 int exl3_moe_max_rows(void) { return MAX_M; }
@@ -111,7 +123,7 @@ int exl3_moe_info(int64_t* out, int n) {
     const int cus = device_cus();
     const int kb = moe_lds_kb(MAX_M, 256);
     const int64_t lds = (int64_t)kb * 1024 + (int64_t)sizeof(Plan);
-    const int64_t v[] = {cus, (int64_t)cus * cached_waves(4, kb), WAVE, MAX_M, MAX_SLOTS, STEP_K, COLS,
+    const int64_t v[] = {cus, (int64_t)cus * cached_waves(4, kb), WAVE, MAX_M, PHASED_MAX_SLOTS, STEP_K, COLS,
                          layout(COLS, COLS, 1).PA, lds};
     const int k = n < 9 ? n : 9;
     for (int i = 0; i < k; ++i) out[i] = v[i];
@@ -151,8 +163,11 @@ static int moe_decode_impl(const void* x, int x_kind, void* out, int out_kind, i
         if (bits < 1 || bits > 8) return fail("bits must be in 1..8");
         mask = 1u << bits;
     }
-    const int64_t trace_off = layout((int)hidden, (int)intermediate, (int)topk).total;
-    if (scratch_bytes < trace_off + trace_bytes()) return fail("scratch too small (see exl3_moe_scratch_bytes)");
+    const int rows = scratch_rows(m);
+    const int64_t trace_off = layout((int)hidden, (int)intermediate, (int)topk, 2, 2, rows).total;
+    if (scratch_bytes < trace_off + trace_bytes())
+        return fail(m > SCRATCH_ROWS ? "scratch too small for this row count (see exl3_moe_scratch_bytes_rows)"
+                                     : "scratch too small (see exl3_moe_scratch_bytes)");
 
     int idx = -1;
     const int ninst = (int)(sizeof(kInstances) / sizeof(kInstances[0]));
@@ -163,12 +178,12 @@ static int moe_decode_impl(const void* x, int x_kind, void* out, int out_kind, i
     // Distinct experts are at most min(E, m * topk); size the items for that.
     const int64_t groups = n_experts < m * topk ? n_experts : m * topk;
     const int lds_kb = moe_lds_kb(m, n_experts);
-    static_assert(MAX_M * NSTEP_CAP * STEP_K * 2 <= MAX_LDS_KB * 1024 && 6 * MAX_EXPERTS <= MAX_LDS_KB * 1024,
+    static_assert(MAX_ROWS * NSTEP_CAP * STEP_K * 2 <= MAX_LDS_KB * 1024 && 6 * MAX_EXPERTS <= MAX_LDS_KB * 1024,
                   "dynamic LDS bound");
     const int64_t resident = (int64_t)device_cus() * cached_waves(idx, lds_kb);
     const int stepsA = item_steps((int)hidden, groups * 2 * (intermediate / COLS), resident);
     const int stepsB = item_steps((int)intermediate, groups * (hidden / COLS), resident);
-    const Layout L = layout((int)hidden, (int)intermediate, (int)topk, stepsA, stepsB);
+    const Layout L = layout((int)hidden, (int)intermediate, (int)topk, stepsA, stepsB, rows);
 
     Params P;
     P.x = x; P.x_kind = x_kind; P.out = out; P.out_kind = out_kind;
@@ -292,10 +307,10 @@ int exl3_moe_decode_noalloc(const void* x, int x_kind, void* out, int out_kind, 
                             const int8_t* expert_bits, int bits, int bits_mask, int codebook,
                             float swiglu_limit, void* stream) {
     clear_error();
-    const int64_t need = exl3_moe_scratch_bytes(hidden, intermediate, topk);
+    const int64_t need = exl3_moe_scratch_bytes_rows(hidden, intermediate, topk, m);
     if (need < 0) return (int)need;
     if (need > NOALLOC_SCRATCH_BYTES)
-        return fail("layer needs more scratch than the fixed 128 MiB (see exl3_moe_scratch_bytes)");
+        return fail("layer needs more scratch than the fixed 128 MiB (see exl3_moe_scratch_bytes_rows)");
     Route rt;
     if (int rc = make_route(topk_ids, ids_kind, topk_weights, weights_kind, expert_map, n_global, rt)) return rc;
     char* scratch = nullptr;

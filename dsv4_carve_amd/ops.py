@@ -402,13 +402,17 @@ def check_expert_bits(expert_bits: torch.Tensor, bits_mask: int) -> None:
     _WIDTHS_CHECKED[key] = True
 
 
-def moe_scratch_bytes(hidden: int, intermediate: int, topk: int) -> int:
-    return int(_lib.check(_lib.load().exl3_moe_scratch_bytes(hidden, intermediate, topk)))
+def moe_scratch_bytes(hidden: int, intermediate: int, topk: int, rows: int = 16) -> int:
+    """Scratch bytes for calls of up to `rows` rows (16 rows and fewer share one size)."""
+    lib = _lib.load()
+    if rows <= 16:
+        return int(_lib.check(lib.exl3_moe_scratch_bytes(hidden, intermediate, topk)))
+    return int(_lib.check(lib.exl3_moe_scratch_bytes_rows(hidden, intermediate, topk, rows)))
 
 
-def moe_scratch(device: torch.device, hidden: int, intermediate: int, topk: int) -> torch.Tensor:
+def moe_scratch(device: torch.device, hidden: int, intermediate: int, topk: int, rows: int = 16) -> torch.Tensor:
     """The shared per-device MoE scratch (zeroed once, self-resetting afterwards)."""
-    return SCRATCH.get(device, "moe", moe_scratch_bytes(hidden, intermediate, topk))
+    return SCRATCH.get(device, "moe", moe_scratch_bytes(hidden, intermediate, topk, rows))
 
 
 def moe_info() -> list[int]:
@@ -479,7 +483,7 @@ def moe_decode(x: torch.Tensor, out: torch.Tensor, tables, expert_ids: torch.Ten
         _check(bits is not None and 1 <= int(bits) <= 8, "bits must be in 1..8")
         b, mask = int(bits), 0
     if scratch is None:
-        scratch = moe_scratch(x.device, hidden, intermediate, expert_ids.shape[1])
+        scratch = moe_scratch(x.device, hidden, intermediate, expert_ids.shape[1], rows=m)
     torch.ops.exl3_amd.moe_decode(x, out, *tabs, expert_ids, routing_weights, expert_map, expert_bits, b, mask,
                                   int(codebook), float(swiglu_limit), int(hidden), int(intermediate), scratch)
     return out
@@ -498,7 +502,7 @@ def lna2_moe_decode(x, out, gate_trellis, gate_suh, gate_svh, up_trellis, up_suh
     limit = float(swiglu_limit)
     _check(limit > 0.0 and limit == limit and limit != float("inf"), "requires a finite positive SwiGLU limit")
     _check(scratch.is_cuda and scratch.dtype == torch.uint8 and scratch.is_contiguous() and
-           scratch.numel() >= moe_scratch_bytes(x.shape[1], intermediate, expert_ids.shape[1]),
+           scratch.numel() >= moe_scratch_bytes(x.shape[1], intermediate, expert_ids.shape[1], rows=x.shape[0]),
            "scratch too small")
     if isinstance(bits, torch.Tensor):
         mask = bits_mask if bits_mask is not None else bits_mask_of(bits.cpu().tolist())
@@ -510,7 +514,9 @@ def lna2_moe_decode(x, out, gate_trellis, gate_suh, gate_svh, up_trellis, up_suh
 
 
 def lna2_moe_scratch_bytes(hidden: int = 4096, intermediate: int = 256, topk: int = 6) -> int:
-    return moe_scratch_bytes(hidden, intermediate, topk)
+    """Enough for every row count lna2_moe_max_rows() allows, as the
+    reference's size is for its build-time row capacity."""
+    return moe_scratch_bytes(hidden, intermediate, topk, rows=moe_max_rows())
 
 
 def lna2_moe_max_rows() -> int:

@@ -750,13 +750,14 @@ LNA2_MAX_TOPK = 9            # routed top-k plus a shared expert appended as one
 def _lna2_scratch_for(layer, device: torch.device) -> torch.Tensor:
     """The shared routed-MoE scratch of this device, zeroed once on creation and
     self-resetting after (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296).  Sized
-    for the largest top-k the kernels take, so a route with a shared-expert
-    slot never needs a bigger buffer at apply time (which capture forbids).
+    for the largest top-k and row count the decode kernels take, so a route
+    with a shared-expert slot or a batch of up to lna2_max_rows() rows never
+    needs a bigger buffer at apply time (which capture forbids).
     One launch at a time per device: launches on concurrent streams would share
     it.  A replaced buffer stays alive: graphs captured on it keep its address."""
     hidden = int(layer._exl3_hidden_size)
     inter = int(layer._exl3_intermediate_local)
-    nbytes = ops.moe_scratch_bytes(hidden, inter, LNA2_MAX_TOPK)
+    nbytes = ops.moe_scratch_bytes(hidden, inter, LNA2_MAX_TOPK, rows=lna2_max_rows())
     idx = device.index if device.index is not None else torch.cuda.current_device()
     buf = _LNA2_SCRATCH.get(int(idx))
     if buf is None or buf.numel() < nbytes:

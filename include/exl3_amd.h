@@ -93,19 +93,27 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
  *     uses `bits`.  bits_mask: bit b set for every width b present (ignored
  *     when expert_bits is NULL).
  *   swiglu_limit: finite and > 0 (lna_moe_ticket.cu:552-553).
- *   scratch: >= exl3_moe_scratch_bytes(hidden, intermediate, topk) bytes, zeroed
- *     once before first use; self-resetting afterwards, and one buffer may
- *     serve layers of different shapes (its control words have fixed
- *     offsets).  One call at a time per scratch buffer.
+ *   scratch: >= exl3_moe_scratch_bytes(hidden, intermediate, topk) bytes for
+ *     m <= 16, >= exl3_moe_scratch_bytes_rows(hidden, intermediate, topk, m)
+ *     beyond; zeroed once before first use; self-resetting afterwards, and one
+ *     buffer may serve layers of different shapes (its control words have
+ *     fixed offsets).  One call at a time per scratch buffer.
+ * Rows: 1 <= m <= exl3_moe_max_rows() = 32 (the reference's lna2 takes up to
+ * LNA2_MAX_M = 24 rows, lna_moe_ticket.cu:40-51).  An expert routed by more
+ * than 16 rows of the batch runs its items in passes of 16 rows.
  * Schedule: plain launches keyed by top-k slot (gate/up, an activation launch
- * when m * topk * intermediate > 32768, down, finish), or one persistent
- * ticket-kernel launch; both give bitwise the same result.  The launches are
- * the default at every batch size.  The environment variable
- * EXL3_MOE_PHASED_MAX_ROWS, when set, picks by row count instead (0: always
- * the ticket kernel).  Every launch is on `stream`; nothing is allocated or
- * synchronised, so a call can be captured in a graph.
+ * when m * topk * intermediate > 32768, down, finish), or, up to 16 rows, one
+ * persistent ticket-kernel launch; both give bitwise the same result.  The
+ * launches are the default at every batch size.  The environment variable
+ * EXL3_MOE_PHASED_MAX_ROWS, when set, picks by row count instead up to 16 rows
+ * (0: always the ticket kernel there).  Every launch is on `stream`; nothing
+ * is allocated or synchronised, so a call can be captured in a graph.
+ * exl3_moe_scratch_bytes replaces lna2_moe_scratch_bytes (:481) and covers 16
+ * rows; exl3_moe_scratch_bytes_rows covers up to `rows` rows (the reference
+ * fixes its row capacity at build time instead).
  */
 int64_t exl3_moe_scratch_bytes(int64_t hidden, int64_t intermediate, int64_t topk);
+int64_t exl3_moe_scratch_bytes_rows(int64_t hidden, int64_t intermediate, int64_t topk, int64_t rows);
 int exl3_moe_max_rows(void);
 
 /*
@@ -167,8 +175,9 @@ int exl3_moe_decode_routed(const void* x, int x_kind, void* out, int out_kind, i
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
  * scratch is a fixed device array inside the library, one per GPU, of
  * exl3_moe_noalloc_scratch_bytes() = 128 MiB, held until the process ends; a
- * layer whose exl3_moe_scratch_bytes(hidden, intermediate, topk) exceeds it is
- * rejected (hidden 4096, intermediate 2048, top-9 needs about 126 MB).  The
+ * call whose exl3_moe_scratch_bytes_rows(hidden, intermediate, topk, m)
+ * exceeds it is rejected (hidden 4096, intermediate 2048, top-9 needs about
+ * 126 MB up to 16 rows, so larger batches of that layer are rejected).  The
  * call allocates nothing.  Its control words are zeroed by a fill kernel on
  * `stream` at the first call on each device and reset themselves afterwards.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU

@@ -2,7 +2,7 @@
 
 * 256-expert routed layer (hidden 4096, intermediate 2048, top-8, 3-bit for
   experts 0-127 and 2-bit for 128-255) at 16 rows, through both decode
-  schedules.
+  schedules, and at 24 rows (phased launches).
 * The same layer plus a 6-bit shared expert (4096 -> 2x2048 -> 4096) carried as
   a ninth slot of weight 1, at 16 rows; and two such blocks chained, the first
   block's output (RMS-normalised, fp16) feeding the second.
@@ -55,6 +55,17 @@ def test_c2_16_rows_against_oracle(c2, c2_m16, dev, path):
         got = c2.run(x, ids, w).cpu().numpy()
     mae, rel = assert_close(got, ref, what=f"C2 m=16 {path}")
     print(f"C2 m=16 {path}: max-abs {mae:.3e} rel-L2 {rel:.3e}", flush=True)
+    _no_errors(dev)
+
+
+def test_c2_24_rows_against_oracle(c2, dev):
+    """24 rows (the reference lna2's row capacity) on the phased launches."""
+    print("C2 m=24 phased vs oracle", flush=True)
+    ids, w = synth.routing(24, E, 8, seed=1024)
+    x = synth.activations(24, H, seed=1024)
+    got = c2.run(x, ids, w).cpu().numpy()
+    mae, rel = assert_close(got, c2.ref(x, ids, w), what="C2 m=24")
+    print(f"C2 m=24: max-abs {mae:.3e} rel-L2 {rel:.3e}", flush=True)
     _no_errors(dev)
 
 

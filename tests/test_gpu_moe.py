@@ -324,10 +324,10 @@ def test_argument_errors(small, dev):
     w = torch.zeros((2, 6), dtype=torch.float32, device=dev)
     kw = dict(intermediate=256, expert_bits=small.ebits, bits_mask=small.mask)
     with pytest.raises(RuntimeError):      # too many rows
-        ops.moe_decode(torch.zeros((17, 512), dtype=torch.float16, device=dev),
-                       torch.empty((17, 512), device=dev), small.tables,
-                       torch.zeros((17, 6), dtype=torch.int32, device=dev),
-                       torch.zeros((17, 6), device=dev), **kw)
+        ops.moe_decode(torch.zeros((33, 512), dtype=torch.float16, device=dev),
+                       torch.empty((33, 512), device=dev), small.tables,
+                       torch.zeros((33, 6), dtype=torch.int32, device=dev),
+                       torch.zeros((33, 6), device=dev), **kw)
     with pytest.raises(RuntimeError):      # int16 ids (int32 and int64 are accepted)
         ops.moe_decode(x, out, small.tables, ids.to(torch.int16), w, **kw)
     with pytest.raises(RuntimeError):      # non-finite limit
@@ -458,6 +458,33 @@ def test_shared_expert_as_extra_slot(dev, m):
     assert_close(got, layer.ref(x, ids9, w9), what=f"routed + shared m={m}")
 
 
+@pytest.mark.parametrize("m", [17, 24, 32])
+@pytest.mark.parametrize("profile", ["random", "hot", "R_e16", "within-row-dup", "boundary"])
+def test_rows_past_16(small, m, profile):
+    """17-32 rows run on the phased launches.  "hot" routes every row to the
+    same experts, so those groups hold all m rows and run in 16-row passes."""
+    print(f"m={m} {profile}", flush=True)
+    ids = route_ids(m, profile)
+    check(small, inputs(m, "real"), ids, route_weights(m, "normal"), f"m={m} {profile}")
+
+
+def test_rows_past_16_match_smaller_batches(small):
+    """A row's result does not depend on the batch around it: rows 0-15 of a
+    32-row batch whose every row takes the same experts (two 16-row passes per
+    group) are bitwise the 16-row batch of those rows, and rows 16-31 the
+    16-row batch of those (the item sizes are the same at both batch sizes)."""
+    import torch
+
+    ids = route_ids(32, "hot")
+    w = route_weights(32, "normal")
+    x = inputs(32, "real")
+    whole = small.run(x, ids, w)
+    lo = small.run(x[:16], ids[:16], w[:16])
+    hi = small.run(x[16:], ids[16:], w[16:])
+    torch.cuda.synchronize()
+    assert torch.equal(whole[:16], lo) and torch.equal(whole[16:], hi), "16-row passes changed a row's result"
+
+
 def test_lna2_signature_and_info(tp_slice, dev):
     """The reference plugin's calls, verbatim in shape: scratch sized by
     lna2_moe_scratch_bytes() with no arguments, lna2_moe_decode with the nine
@@ -466,7 +493,7 @@ def test_lna2_signature_and_info(tp_slice, dev):
     from dsv4_carve_amd import ops
 
     info = ops.lna2_moe_info(2)
-    assert len(info) == 14 and info[13] == 1 and info[11] == ops.lna2_moe_max_rows() == 16
+    assert len(info) == 14 and info[13] == 1 and info[11] == ops.lna2_moe_max_rows() == 32
     assert info[0] > 0 and info[1] >= info[0] and info[10] == ops.lna2_moe_scratch_bytes()
     layer = tp_slice[2]
     scratch = torch.zeros(ops.lna2_moe_scratch_bytes(), dtype=torch.uint8, device=dev)

@@ -170,7 +170,7 @@ def test_apply_experts_expert_map(dev, experts, monkeypatch):
 
 
 def test_apply_experts_large_batches_use_prefill(dev, experts, monkeypatch):
-    """Above 16 rows the routed path switches to the prefill kernel (no decline,
+    """Above 32 rows the routed path switches to the prefill kernel (no decline,
     so strict level 2 does not raise); the loop backend still serves them."""
     from dsv4_carve_amd import vllm_exl3 as V
 

@@ -136,7 +136,7 @@ def test_routed_argument_errors(dev, layer):
         _run(layer, ops.moe_decode, x, ids, w, torch.zeros(4, dtype=torch.int64))
 
 
-@pytest.mark.parametrize("rows", [3, 30])
+@pytest.mark.parametrize("rows", [3, 30, 40])
 def test_plugin_apply_with_router_tensors(dev, monkeypatch, rows):
     """apply_exl3_experts with int32 global ids, bf16 weights and an expert
     map equals the unique-expert loop (which maps on the host)."""
@@ -156,7 +156,7 @@ def test_plugin_apply_with_router_tensors(dev, monkeypatch, rows):
     ids_t = to_dev(ids, dev).to(torch.int32)
     w_t = to_dev(w, dev).to(torch.bfloat16)
     fused = V.apply_exl3_experts(x, ids_t, w_t, ex.layer)
-    assert ex.layer._exl3_last_apply == ("lna2" if rows <= 16 else "prefill")
+    assert ex.layer._exl3_last_apply == ("lna2" if rows <= V.lna2_max_rows() else "prefill")
     monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", "loop")
     loop = V.apply_exl3_experts(x, ids_t.long(), w_t, ex.layer)
     assert ex.layer._exl3_last_apply == "loop"

@@ -53,7 +53,7 @@ def _err():
 
 def test_moe_host_arithmetic_without_device():
     lib = _lib.load()
-    assert lib.exl3_moe_max_rows() == 16
+    assert lib.exl3_moe_max_rows() == 32
     a = lib.exl3_moe_scratch_bytes(4096, 2048, 8)
     b = lib.exl3_moe_scratch_bytes(4096, 256, 6)
     assert a > b > 0 and a % 256 == 0
@@ -61,6 +61,12 @@ def test_moe_host_arithmetic_without_device():
     assert lib.exl3_moe_scratch_bytes(4096, 2048, 10) == -1 and "topk" in _err()
     assert lib.exl3_moe_scratch_bytes(4096, 2048, 9) > 0
     assert lib.exl3_moe_scratch_bytes(16640, 256, 8) == -1 and "16384" in _err()
+    # up to 16 rows one size; past 16 rows the data regions grow with the row count
+    assert lib.exl3_moe_scratch_bytes_rows(4096, 2048, 8, 1) == lib.exl3_moe_scratch_bytes_rows(4096, 2048, 8, 16) == a
+    a24, a32 = lib.exl3_moe_scratch_bytes_rows(4096, 2048, 8, 24), lib.exl3_moe_scratch_bytes_rows(4096, 2048, 8, 32)
+    assert a < a24 < a32 and a32 % 256 == 0
+    assert lib.exl3_moe_scratch_bytes_rows(4096, 2048, 8, 33) == -1 and "row count" in _err()
+    assert lib.exl3_moe_scratch_bytes_rows(4096, 2048, 8, 0) == -1 and "row count" in _err()
 
 
 def _moe_call(**kw):
@@ -82,7 +88,7 @@ def _moe_call(**kw):
     ({"x_kind": 2}, "fp16 or bf16"),
     ({"out_kind": 3}, "fp16, bf16 or fp32"),
     ({"m": 0}, "row count"),
-    ({"m": 17}, "row count"),
+    ({"m": 33}, "row count"),
     ({"hidden": 500}, "multiples of 256"),
     ({"intermediate": 128}, "multiples of 256"),
     ({"n_experts": 0}, "expert count"),
