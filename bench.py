@@ -630,6 +630,10 @@ def main() -> int:
     ap.add_argument("--extra", default=",".join(EXTRA_LEGS),
                     help="comma-separated extra measurements to run: " + ", ".join(EXTRA_LEGS))
     ap.add_argument("--eager", action="store_true", help="launch the timed steps one by one (no graph)")
+    ap.add_argument("--dense-shapes", default=",".join(f"{k}x{n}" for k, n in DENSE_SHAPES),
+                    help="dense leg: comma-separated KxN shapes")
+    ap.add_argument("--dense-bits", default=",".join(str(b) for b in DENSE_BITS), help="dense leg: bit widths")
+    ap.add_argument("--dense-rows", default=",".join(str(r) for r in DENSE_ROWS), help="dense leg: row counts")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="end with one device-to-device copy of this many MiB (HBM counter calibration)")
     a = ap.parse_args()
@@ -724,10 +728,12 @@ def main() -> int:
               flush=True)
     if "dense" in legs:
         dense = {}
-        for (k, n) in DENSE_SHAPES:
-            for b in DENSE_BITS:
+        shapes = [tuple(int(v) for v in sh.split("x")) for sh in a.dense_shapes.split(",") if sh]
+        dense_rows = [int(r) for r in a.dense_rows.split(",") if r]
+        for (k, n) in shapes:
+            for b in (int(v) for v in a.dense_bits.split(",") if v):
                 key = f"{k}x{n}_K{b}"
-                dense[key] = time_dense(dev, k, n, b, DENSE_ROWS)
+                dense[key] = time_dense(dev, k, n, b, dense_rows)
                 print(f"[bench] dense {key}: {dense[key]}", file=sys.stderr, flush=True)
         extra["dense_gemv_cold"] = dense
         if not a.no_cpu:
