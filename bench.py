@@ -737,13 +737,21 @@ def main() -> int:
                 print(f"[bench] dense {key}: {dense[key]}", file=sys.stderr, flush=True)
         extra["dense_gemv_cold"] = dense
         if not a.no_cpu:
-            # the single-linear CPU reference path (4096 x 4096, 6-bit, one row)
+            # the single-linear CPU reference path (4096 x 4096, 6-bit, one row),
+            # and every dense shape and width of the sweep at one row
             from oracle import cpu_baseline as CB
             lin = synth.dense(4096, 4096, 6, seed=3)
             t = CB.time_linear(lin, 1)
             extra["dense_4096x4096_K6_cpu"] = {"us": round(t * 1e6, 1), "cores": CB.threads(),
                                                "sample": "dequant + fp32 matmul per call, median of 5 after 1 warm-up"}
             print(f"[bench] dense cpu: {extra['dense_4096x4096_K6_cpu']}", file=sys.stderr, flush=True)
+            sweep_cpu = {}
+            for (k, n) in shapes:
+                for b in DENSE_BITS:
+                    sweep_cpu[f"{k}x{n}_K{b}"] = round(CB.time_linear(synth.dense(k, n, b, seed=3), 1, reps=3) * 1e6, 1)
+            extra["dense_cpu_1row_us"] = {"us": sweep_cpu, "cores": CB.threads(),
+                                          "sample": "one row, dequant + fp32 matmul per call, median of 3 after 1 warm-up"}
+            print(f"[bench] dense cpu sweep: {extra['dense_cpu_1row_us']}", file=sys.stderr, flush=True)
 
     if "fan" in legs:
         fans = {}
@@ -764,6 +772,18 @@ def main() -> int:
         pool_ids = [synth.routing(a.rows, EXPERTS, TOPK, seed=a.rows * 1000 + i)[0] for i in range(POOL)]
         cpu = cpu_baseline(a.rows, bits, seed=1, us_ids=pool_ids)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+        key = "stack_43_layers_routed_plus_shared_rows16"
+        if key in extra and a.rows == 16:
+            # the stack on CPU: one block (this routed layer + the 6-bit shared
+            # expert, both timed) times 43
+            from oracle import cpu_baseline as CB
+            t6 = CB.time_expert(synth.expert(EXPERTS, HIDDEN, INTER, 6, seed=1), a.rows)
+            block_us = cpu["value"] + t6 * 1e6
+            extra[key]["cpu_estimate"] = {
+                "us_per_step": round(C3_LAYERS * block_us, 0), "cores": CB.threads(),
+                "sample": (f"one block timed and multiplied by {C3_LAYERS}: the routed layer's CPU baseline "
+                           f"({cpu['value']:.0f} us) plus one 6-bit shared expert at 16 rows ({t6 * 1e6:.0f} us)")}
+            print(f"[bench] stack cpu estimate: {extra[key]['cpu_estimate']}", file=sys.stderr, flush=True)
 
     if a.calib_copy_mib:
         src = torch.ones(a.calib_copy_mib << 18, dtype=torch.float32, device=dev)
