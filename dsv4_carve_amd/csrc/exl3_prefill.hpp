@@ -242,13 +242,32 @@ __device__ __forceinline__ void pf_tile(bool valid, int wave, const uint16_t* A,
     }
 }
 
-// Items: gate/up (DOWN = false) = (tile, projection, column block of I,
-// k-part); down (DOWN = true) = (tile, column block of H, k-part).  Two waves
-// per block, item 2 * blockIdx + wave each, sharing one 32 KB transpose
-// buffer (16 KB per wave leaves the LDS room for two waves per SIMD).  One
-// launch per bit width present (one width per kernel keeps the registers at
-// two waves per SIMD); items past the planned tile count or of another width
-// are skipped, and a block with none returns at once.
+// Items: gate/up (DOWN = false) = (tile, projection, k-part, column block of
+// I); down (DOWN = true) = (tile, k-part, column block of H).  The items of
+// one (tile, projection, k-part) -- a group -- read the same rows of A.  Two
+// waves per block take two neighbouring column blocks of a group, sharing one
+// 32 KB transpose buffer (16 KB per wave leaves the LDS room for two waves per
+// SIMD).
+//
+// Workgroups go to the eight XCDs in turn (block b to XCD b % 8), and each XCD
+// has its own L2.  Group g is given to XCD g % 8 as consecutive blocks of that
+// XCD's sequence, so its A rows are read into one L2 and shared there by
+// every block of the group; with eight (projection, k-part) pairs per tile,
+// each XCD also keeps the same pair across tiles, so consecutive tiles of a
+// hot expert find that pair's weight slice in its L2.  Groups go round the
+// XCDs in tile order, so the tiles of one width (a leading range of the
+// planned tiles) spread over all of them.
+//
+// One launch per bit width present (one width per kernel keeps the registers
+// at two waves per SIMD); items past the planned tile count, past the column
+// blocks or of another width are skipped, and a block with none returns at
+// once.
+__host__ __device__ inline int pf_group_blocks(int ncb) { return (ncb + 1) / 2; }
+__host__ __device__ inline int64_t pf_gemm_grid(int64_t tiles, int combos, int ncb) {
+    const int64_t groups = tiles * combos;
+    return 8 * (int64_t)pf_group_blocks(ncb) * ((groups + 7) / 8);
+}
+
 template <int BITS, int CB, bool DOWN>
 // Up to 3 bits the kernel fits two waves per SIMD (at most 256 registers);
 // the request keeps the compiler there with both step loops of pf_tile.
@@ -258,18 +277,18 @@ void pf_gemm_kernel(PfParams P) {
     const PfLayout& L = P.L;
     const int ncb = (DOWN ? P.H : P.I) / COLS;
     const int KS = DOWN ? L.ks_down : L.ks_up;
-    const int per_tile = (DOWN ? ncb : 2 * ncb) * KS;
+    const int combos = DOWN ? KS : 2 * KS;             // groups per tile
+    const int G = pf_group_blocks(ncb);
     const int wave = threadIdx.x / WAVE;
-    const int item = 2 * blockIdx.x + wave;
-    const int t = item / per_tile;
-    int rem = item - t * per_tile;
-    bool valid = t < pat<int>(P.scratch, L.meta)[PF_META_TILES];
+    const int jj = (int)(blockIdx.x >> 3);              // this block's place in its XCD's sequence
+    const int g = 8 * (jj / G) + (int)(blockIdx.x & 7);
+    const int cb = 2 * (jj % G) + wave;
+    const int t = g / combos, c = g - t * combos;
+    bool valid = cb < ncb && t < pat<int>(P.scratch, L.meta)[PF_META_TILES];
     const int e = valid ? pat<int>(P.scratch, L.tile_e)[t] : 0;
     valid = valid && (P.ebits ? (int)P.ebits[e] : P.bits) == BITS;
     if (!__syncthreads_or(valid)) return;
-    const int ks = rem % KS;
-    rem /= KS;
-    const int proj = DOWN ? 0 : rem / ncb, cb = DOWN ? rem : rem - (rem / ncb) * ncb;
+    const int proj = DOWN ? 0 : c / KS, ks = c % KS;
     const int row0 = valid ? pat<int>(P.scratch, L.tile_r0)[t] : 0;
     const int nrows = valid ? pat<int>(P.scratch, L.tile_n)[t] : 0;
     const int K = DOWN ? P.I : P.H, N = DOWN ? P.H : P.I;

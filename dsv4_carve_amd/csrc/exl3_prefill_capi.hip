@@ -316,11 +316,13 @@ static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, 
     hipLaunchKernelGGL(pf_rotate_kernel, dim3(2 * P.P * ((hidden + 511) / 512)), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
     const int64_t tiles = P.L.max_tiles;
-    if ((rc = launch_widths(P, mask, codebook, false, (int)(tiles * 2 * (intermediate / COLS) * P.L.ks_up), s)))
+    if ((rc = launch_widths(P, mask, codebook, false,
+                            (int)pf_gemm_grid(tiles, 2 * P.L.ks_up, (int)(intermediate / COLS)), s)))
         return rc;
     hipLaunchKernelGGL(pf_act_kernel, dim3(P.P * (intermediate / COLS)), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
-    if ((rc = launch_widths(P, mask, codebook, true, (int)(tiles * (hidden / COLS) * P.L.ks_down), s))) return rc;
+    if ((rc = launch_widths(P, mask, codebook, true, (int)pf_gemm_grid(tiles, P.L.ks_down, (int)(hidden / COLS)), s)))
+        return rc;
     hipLaunchKernelGGL(pf_gather_kernel, dim3((unsigned)(tokens * (hidden / COLS))), dim3(WAVE), 0, s, P);
     return check_launch();
 }

@@ -12,8 +12,8 @@ namespace prefill {
 template <>
 int launch_pf_gemm<EXL3_BITS>(const PfParams& P, int codebook, bool down, int blocks, hipStream_t stream) {
     constexpr int B = EXL3_BITS;
-    // `blocks` items, two per workgroup
-    const unsigned grid = (unsigned)((blocks + 1) / 2);
+    // `blocks` workgroups of two waves (pf_gemm_grid)
+    const unsigned grid = (unsigned)blocks;
     auto go = [&](auto cbc) {
         constexpr int C = decltype(cbc)::value;
         if (down)
