@@ -39,6 +39,7 @@ UNITS += [("exl3_moe_inst.hip", [f"-DEXL3_MOE_MASK=0x{m:03X}u", f"-DEXL3_MOE_CB=
            f"exl3_moe_m{m:03x}_c{c}.o") for m, c in MOE_UNITS]
 UNITS += [("exl3_prefill_capi.hip", [], "exl3_prefill_capi.o")]
 UNITS += [("exl3_prefill_inst.hip", [f"-DEXL3_BITS={b}"], f"exl3_pf_b{b}.o") for b in range(1, 9)]
+UNITS += [("exl3_prefill_inst.hip", ["-DEXL3_BITS=3", "-DEXL3_BITS2=2"], "exl3_pf_b32.o")]
 
 
 def _compile(unit):

@@ -268,10 +268,14 @@ __host__ __device__ inline int64_t pf_gemm_grid(int64_t tiles, int combos, int n
     return 8 * (int64_t)pf_group_blocks(ncb) * ((groups + 7) / 8);
 }
 
-template <int BITS, int CB, bool DOWN>
+// BITS2 = 0: the experts of one width, BITS.  BITS2 > 0: the experts of either
+// width BITS or BITS2 in one launch (a tile's width is the same for both waves
+// of its block), so one launch's tail is paid where two would each pay one.
+template <int BITS, int BITS2, int CB, bool DOWN>
 // Up to 3 bits the kernel fits two waves per SIMD (at most 256 registers);
 // the request keeps the compiler there with both step loops of pf_tile.
-__global__ __launch_bounds__(2 * WAVE) __attribute__((amdgpu_waves_per_eu(BITS <= 3 ? 2 : 1, BITS <= 3 ? 2 : 8)))
+__global__ __launch_bounds__(2 * WAVE)
+__attribute__((amdgpu_waves_per_eu((BITS <= 3 && BITS2 <= 3) ? 2 : 1, (BITS <= 3 && BITS2 <= 3) ? 2 : 8)))
 void pf_gemm_kernel(PfParams P) {
     __shared__ float tbuf[PF_RB * COLS];
     const PfLayout& L = P.L;
@@ -284,9 +288,10 @@ void pf_gemm_kernel(PfParams P) {
     const int g = 8 * (jj / G) + (int)(blockIdx.x & 7);
     const int cb = 2 * (jj % G) + wave;
     const int t = g / combos, c = g - t * combos;
-    bool valid = cb < ncb && t < pat<int>(P.scratch, L.meta)[PF_META_TILES];
-    const int e = valid ? pat<int>(P.scratch, L.tile_e)[t] : 0;
-    valid = valid && (P.ebits ? (int)P.ebits[e] : P.bits) == BITS;
+    const bool tile_ok = t < pat<int>(P.scratch, L.meta)[PF_META_TILES];
+    const int e = tile_ok ? pat<int>(P.scratch, L.tile_e)[t] : 0;
+    const int width = P.ebits ? (int)P.ebits[e] : P.bits;    // the same for the block's two waves
+    const bool valid = tile_ok && cb < ncb && (width == BITS || (BITS2 > 0 && width == BITS2));
     if (!__syncthreads_or(valid)) return;
     const int proj = DOWN ? 0 : c / KS, ks = c % KS;
     const int row0 = valid ? pat<int>(P.scratch, L.tile_r0)[t] : 0;
@@ -299,12 +304,18 @@ void pf_gemm_kernel(PfParams P) {
     const uint16_t* svh = reinterpret_cast<const uint16_t*>((DOWN ? P.dsv : (proj ? P.usv : P.gsv))[e]);
     float* out = DOWN ? pat<float>(P.scratch, L.D) + (size_t)ks * P.P * P.H
                       : pat<float>(P.scratch, L.GU) + ((size_t)ks * 2 + proj) * P.P * P.I;
-    pf_tile<BITS, CB>(valid, wave, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out, tbuf);
+    if (BITS2 == 0 || width == BITS)
+        pf_tile<BITS, CB>(valid, wave, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out, tbuf);
+    else
+        pf_tile<(BITS2 > 0 ? BITS2 : BITS), CB>(valid, wave, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K,
+                                                N, cb, out, tbuf);
 }
 
-// Launcher of the grouped GEMM for one bit width (exl3_prefill_inst.hip).
+// Launchers of the grouped GEMM for one bit width, and for widths 3 and 2
+// together (exl3_prefill_inst.hip).
 template <int BITS>
 int launch_pf_gemm(const PfParams& P, int codebook, bool down, int blocks, hipStream_t stream);
+int launch_pf_gemm_32(const PfParams& P, int codebook, bool down, int blocks, hipStream_t stream);
 
 }  // namespace prefill
 }  // namespace exl3

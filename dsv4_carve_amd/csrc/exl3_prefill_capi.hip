@@ -233,11 +233,18 @@ template <> int launch_pf_gemm<6>(const PfParams&, int, bool, int, hipStream_t);
 template <> int launch_pf_gemm<7>(const PfParams&, int, bool, int, hipStream_t);
 template <> int launch_pf_gemm<8>(const PfParams&, int, bool, int, hipStream_t);
 
-// Grouped GEMM over every width in `mask` (one launch each).
+// Grouped GEMM over every width in `mask`: one launch for the 3- and 2-bit
+// experts together when both are present, one launch for each other width.
 static int launch_widths(const PfParams& P, uint32_t mask, int codebook, bool down, int blocks, hipStream_t s) {
     int (*const fn[9])(const PfParams&, int, bool, int, hipStream_t) = {
         nullptr, &launch_pf_gemm<1>, &launch_pf_gemm<2>, &launch_pf_gemm<3>, &launch_pf_gemm<4>,
         &launch_pf_gemm<5>, &launch_pf_gemm<6>, &launch_pf_gemm<7>, &launch_pf_gemm<8>};
+    constexpr uint32_t W32 = (1u << 3) | (1u << 2);
+    if ((mask & W32) == W32) {
+        const int rc = launch_pf_gemm_32(P, codebook, down, blocks, s);
+        if (rc) return rc;
+        mask &= ~W32;
+    }
     for (int b = 1; b <= 8; ++b)
         if (mask & (1u << b)) {
             const int rc = fn[b](P, codebook, down, blocks, s);
