@@ -682,7 +682,10 @@ def main() -> int:
             uw, bw = time_layer(layer, dev, m, TOPK, a.steps, 3, seed=m, same_routing=True)
             sweep[str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1),
                              "frac": round(b / (u * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "bytes": int(b),
-                             "warm_us": round(uw, 2), "warm_GBps": round(bw / (uw * 1e-6) / 1e9, 1)}
+                             "warm_us": round(uw, 2), "warm_GBps": round(bw / (uw * 1e-6) / 1e9, 1),
+                             "latency_per_call": {
+                                 "cold": layer_latency(layer, dev, m, TOPK, LATENCY_ITERS, seed=m, cold=True),
+                                 "warm": layer_latency(layer, dev, m, TOPK, LATENCY_ITERS, seed=m, cold=False)}}
             print(f"[bench] sweep m={m}: {sweep[str(m)]}", file=sys.stderr, flush=True)
         extra["rows_sweep"] = sweep
     if "rows17" in legs:
