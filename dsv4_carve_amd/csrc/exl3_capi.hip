@@ -3,11 +3,14 @@
 //                              (raw variant  <- exllamav3 `reconstruct`, recipe-lna/exllamav3/exl3.py.lna:197)
 //   exl3_gemm               <- exl3_gemm        recipe-lna/exllamav3/exl3_gemm.cu.lna:336-364
 //                              (and the exl3_gemv entry, recipe-lna/lna2/bindings.cpp:135-148)
+//   exl3_had_rows           <- exllamav3_ext.had_r_128  recipe-lna/exllamav3/exl3.py.lna:190, 214
 //   exl3_gemm_scratch_bytes    scratch sizing for exl3_gemm
 //   exl3_gemm_group         <- exl3_mgemm with a broadcast A (same-input fan)
 //                              recipe-lna/vllm_exl3_exl3.py.lna:546-613
 //   exl3_gemm_group_scratch_bytes
 //   exl3_last_error            message of the last failed call on this thread
+#include <cmath>
+
 #include "exl3_dense.hpp"
 
 namespace exl3 {
@@ -46,6 +49,22 @@ int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int cod
     const DequantArgs args{trellis, k16, n16, codebook, had ? suh : nullptr, had ? svh : nullptr, out, s};
     EXL3_BITS_SWITCH(bits, return launch_dequant<B_>(args));
     return 0;
+}
+
+int exl3_had_rows(const void* x, int x_kind, void* y, int y_kind, int64_t rows, int64_t cols,
+                  const uint16_t* pre_scale, const uint16_t* post_scale, float scale, void* stream) {
+    clear_error();
+    if (!x || !y) return fail("null pointer");
+    if (x_kind < OUT_F16 || x_kind > OUT_F32 || y_kind < OUT_F16 || y_kind > OUT_F32)
+        return fail("kinds must be 0 (fp16), 1 (bf16) or 2 (fp32)");
+    if (rows < 1 || cols < 128 || cols % 128) return fail("rows must be positive and cols a positive multiple of 128");
+    if (x == y && x_kind != y_kind) return fail("in place needs the same element kind");
+    const int64_t waves = rows * ((cols / 128 + 1) / 2);
+    if (waves > 0x7fffffffLL) return fail("too many rows");
+    if (!std::isfinite(scale)) return fail("scale must be finite");
+    hipLaunchKernelGGL(had_rows_kernel<0>, dim3((unsigned)waves), dim3(64), 0, reinterpret_cast<hipStream_t>(stream), x,
+                       x_kind, y, y_kind, (int)cols, pre_scale, post_scale, scale);
+    return check_launch();
 }
 
 int64_t exl3_gemm_scratch_bytes(int64_t m, int64_t k, int64_t n) {

@@ -40,72 +40,212 @@ __global__ __launch_bounds__(64) void dequant_raw_kernel(const int16_t* __restri
 
 // ---------------------------------------------------------------- dequant (Hadamard folded)
 
-// W = diag(suh) H Wq H diag(svh) / 128, one wave per 128x128 block, in the
-// operation order of dequant_cpu (recipe-lna/lna2/bindings.cpp:80-99): row
-// transforms (* 1/sqrt(128)), then column transforms, value = ((v*norm)*su)*sv.
-constexpr int HB_LD = 129;   // padded LDS row (floats)
+// W = diag(suh) H Wq H diag(svh) / 128 in the operation order of dequant_cpu
+// (recipe-lna/lna2/bindings.cpp:80-99): row transforms (* 1/sqrt(128)), then
+// column transforms, value = ((v*norm)*su)*sv.  One workgroup of four waves
+// per 128x128 block:
+//   1. rows: lane l of every wave owns tile (l >> 3, l & 7) of the block and
+//      wave w its tile rows 4w..4w+3.  A tile row's 16 values are decoded into
+//      registers, transformed by butterflies h = 1..8 in registers and
+//      h = 16, 32, 64 with the lanes of the same tile row (lane ^ 1, 2, 4),
+//      normalised, and written to LDS as fp32.
+//   2. columns: wave w owns columns 32w..32w+31, lanes l and l ^ 32 the upper
+//      and lower 64 rows of column 32w + (l & 31): butterflies h = 1..32 in
+//      registers, h = 64 across the two lanes, then norm, su, sv, fp16.
+// The butterfly stages run in the order h = 1, 2, ..., 64 of the reference's
+// scalar loop and every butterfly is a single fp32 add or subtract of the same
+// two operands, so the result is bitwise the loop's.
+//
+// LDS position of block element (r, c), fp32, unpadded: 16-byte chunks are
+// XOR-swizzled within each aligned group of 8 by the tile column (c >> 4) & 7,
+// so the eight lanes of a tile row writing the same chunk of their own tiles,
+// and 32 lanes reading 32 consecutive columns of one row, fall on distinct
+// banks.
+__device__ __forceinline__ int hb_pos(int r, int c) {
+    return r * 128 + ((((c >> 2) ^ ((c >> 4) & 7)) << 2) | (c & 3));
+}
 
-__device__ __forceinline__ void fwht128_regs(float (&v)[128]) {
-    static_for<7>([&](auto SI) {
-        constexpr int h = 1 << decltype(SI)::value;
-        static_for<64>([&](auto JI) {
-            constexpr int j = decltype(JI)::value;
-            constexpr int i = (j / h) * 2 * h + (j % h);
-            const float a = v[i], b = v[i + h];
-            v[i] = a + b;
-            v[i + h] = a - b;
+// The value of lane (lane ^ M) within groups of 8 lanes, M = 1, 2 or 4, by
+// DPP moves (no LDS traffic): xor 1 and 2 are quad permutations, xor 4 a quad
+// reversal (xor 3) followed by the half-row mirror (xor 7).
+template <int M>
+__device__ __forceinline__ float dpp_xor(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+    else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+    else {
+        static_assert(M == 4, "xor 1, 2 or 4");
+        const int r = __builtin_amdgcn_mov_dpp(x, 0x1B, 0xF, 0xF, false);
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x141, 0xF, 0xF, false));
+    }
+}
+
+// Cross-lane butterfly of an element pair (a in the lane without the bit,
+// b in the lane with it): a + b and a - b, each one exactly rounded fp32
+// operation, as fma(+-1, own, partner).
+__device__ __forceinline__ float bfly(float own, float partner, float sgn) {
+    return __builtin_fmaf(sgn, own, partner);
+}
+
+// Phase 1 for tile rows K0..K0+3 of this lane's tile.
+template <int BITS, int CB, int K0>
+__device__ __forceinline__ void had_rows(const uint32_t* W, int kt, int nt, float* mat) {
+    const float s1 = (nt & 1) ? -1.f : 1.f, s2 = (nt & 2) ? -1.f : 1.f, s4 = (nt & 4) ? -1.f : 1.f;
+    static_for<4>([&](auto KI) {
+        constexpr int k = K0 + decltype(KI)::value;
+        float v[16];
+        static_for<16>([&](auto NI) {
+            constexpr int n = decltype(NI)::value;
+            v[n] = f16_bits_to_f32(decode_half<BITS, CB, tile_t(k, n)>(W));
         });
+#pragma unroll
+        for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int i = (j / h) * 2 * h + (j % h);
+                const float a = v[i], b = v[i + h];
+                v[i] = a + b;
+                v[i + h] = a - b;
+            }
+#pragma unroll
+        for (int n = 0; n < 16; ++n) v[n] = bfly(v[n], dpp_xor<1>(v[n]), s1);
+#pragma unroll
+        for (int n = 0; n < 16; ++n) v[n] = bfly(v[n], dpp_xor<2>(v[n]), s2);
+#pragma unroll
+        for (int n = 0; n < 16; ++n) v[n] = bfly(v[n], dpp_xor<4>(v[n]), s4);
+        const int r = 16 * kt + k;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4_t*>(mat + hb_pos(r, 16 * nt + 4 * q)) =
+                float4_t{v[4 * q] * HAD_NORM, v[4 * q + 1] * HAD_NORM, v[4 * q + 2] * HAD_NORM,
+                         v[4 * q + 3] * HAD_NORM};
     });
 }
 
 template <int BITS, int CB>
-__global__ __launch_bounds__(64) void dequant_had_kernel(const int16_t* __restrict__ trellis, int k16,
-                                                         int n16, const uint16_t* __restrict__ suh,
-                                                         const uint16_t* __restrict__ svh,
-                                                         uint16_t* __restrict__ out) {
-    __shared__ float mat[128 * HB_LD];
-    const int lane = threadIdx.x;
+__global__ __launch_bounds__(256) void dequant_had_kernel(const int16_t* __restrict__ trellis, int k16,
+                                                          int n16, const uint16_t* __restrict__ suh,
+                                                          const uint16_t* __restrict__ svh,
+                                                          uint16_t* __restrict__ out) {
+    __shared__ __align__(16) float mat[128 * 128];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int nbc = n16 / 8;
     const int br = blockIdx.x / nbc, bc = blockIdx.x - br * nbc;
     const size_t N = (size_t)n16 * 16;
     {
-        const int kt = 8 * br + (lane >> 3), nt = 8 * bc + (lane & 7);
+        const int kt = lane >> 3, nt = lane & 7;
         TileRegs<BITS> t;
         load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) +
-                               ((size_t)kt * n16 + nt) * tile_vecs<BITS>());
+                               ((size_t)(8 * br + kt) * n16 + 8 * bc + nt) * tile_vecs<BITS>());
         const uint32_t* W = t.words();
-        float* base = mat + (16 * (lane >> 3)) * HB_LD + 16 * (lane & 7);
-        static_for<16>([&](auto KI) {
-            constexpr int k = decltype(KI)::value;
-            static_for<16>([&](auto NI) {
-                constexpr int n = decltype(NI)::value;
-                base[k * HB_LD + n] = f16_bits_to_f32(decode_half<BITS, CB, tile_t(k, n)>(W));
-            });
-        });
-    }
-    __syncthreads();
-    for (int rr = lane; rr < 128; rr += 64) {
-        float v[128];
-#pragma unroll
-        for (int c = 0; c < 128; ++c) v[c] = mat[rr * HB_LD + c];
-        fwht128_regs(v);
-#pragma unroll
-        for (int c = 0; c < 128; ++c) mat[rr * HB_LD + c] = v[c] * HAD_NORM;
-    }
-    __syncthreads();
-    for (int cc = lane; cc < 128; cc += 64) {
-        float v[128];
-#pragma unroll
-        for (int r = 0; r < 128; ++r) v[r] = mat[r * HB_LD + cc];
-        fwht128_regs(v);
-        const float sv = f16_bits_to_f32(svh[128 * bc + cc]);
-#pragma unroll
-        for (int r = 0; r < 128; ++r) {
-            float x = v[r] * HAD_NORM;
-            x = x * f16_bits_to_f32(suh[128 * br + r]);
-            x = x * sv;
-            out[(size_t)(128 * br + r) * N + 128 * bc + cc] = f32_to_f16_bits(x);
+        switch (wave) {
+            case 0: had_rows<BITS, CB, 0>(W, kt, nt, mat); break;
+            case 1: had_rows<BITS, CB, 4>(W, kt, nt, mat); break;
+            case 2: had_rows<BITS, CB, 8>(W, kt, nt, mat); break;
+            default: had_rows<BITS, CB, 12>(W, kt, nt, mat); break;
         }
+    }
+    const int c = 32 * wave + (lane & 31), half = lane >> 5;
+    // this lane's 64 row scales (128 contiguous bytes), requested before the barrier
+    u32x4_t su4[8];
+    const u32x4_t* sp = reinterpret_cast<const u32x4_t*>(suh + 128 * br + 64 * half);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) su4[i] = sp[i];
+    const float sv = f16_bits_to_f32(svh[128 * bc + c]);
+    __syncthreads();
+    float v[64];
+#pragma unroll
+    for (int j = 0; j < 64; ++j) v[j] = mat[hb_pos(64 * half + j, c)];
+    __syncthreads();                               // mat is free: it becomes the fp16 output tile
+#pragma unroll
+    for (int h = 1; h < 64; h <<= 1)
+#pragma unroll
+        for (int j = 0; j < 32; ++j) {
+            const int i = (j / h) * 2 * h + (j % h);
+            const float a = v[i], b = v[i + h];
+            v[i] = a + b;
+            v[i + h] = a - b;
+        }
+    const uint32_t* su = reinterpret_cast<const uint32_t*>(su4);
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(mat);
+    const float s32 = half ? -1.f : 1.f;
+#pragma unroll
+    for (int j = 0; j < 64; ++j) {
+        float x = bfly(v[j], shfl_xor(v[j], 32), s32);
+        x = x * HAD_NORM;
+        x = x * f16_bits_to_f32((uint16_t)(su[j >> 1] >> (16 * (j & 1))));
+        x = x * sv;
+        o16[(64 * half + j) * 128 + c] = f32_to_f16_bits(x);
+    }
+    __syncthreads();
+    // 128 rows x 256 bytes, 16 bytes per lane and pass
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int id = i * 256 + (int)threadIdx.x, row = id >> 4, seg = id & 15;
+        *reinterpret_cast<u32x4_t*>(out + (size_t)(128 * br + row) * N + 128 * bc + 8 * seg) =
+            *reinterpret_cast<const u32x4_t*>(o16 + row * 128 + 8 * seg);
+    }
+}
+
+// ---------------------------------------------------------------- row Hadamard (had_r_128)
+
+// y[r][128b + i] = (H128 v / sqrt(128))[i] * scale * post[128b + i] for every
+// 128-block b of every row r, v = x[r][128b ..]; with a pre scale v is
+// half(half(x) * pre), the rounding of the GEMV path's input rotation.  Butterflies
+// in fp32, h = 1, 2, ..., 64.  One wave per (row, two blocks): lanes 0-31 and
+// 32-63 hold one block each, 4 consecutive elements per lane; a block past the
+// row (odd block count) is computed from block 2p and not stored.
+__device__ __forceinline__ void load4_kind(const void* p, int kind, size_t i, float (&v)[4], bool to_half) {
+    if (kind == OUT_F32) {
+        const float4_t f = *reinterpret_cast<const float4_t*>(reinterpret_cast<const float*>(p) + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = to_half ? f16_bits_to_f32(f32_to_f16_bits(f[e])) : f[e];
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(p) + i);
+        const uint16_t h[4] = {(uint16_t)(u.x & 0xffffu), (uint16_t)(u.x >> 16), (uint16_t)(u.y & 0xffffu),
+                               (uint16_t)(u.y >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (kind == OUT_F16) v[e] = f16_bits_to_f32(h[e]);
+            else v[e] = to_half ? f16_bits_to_f32(f32_to_f16_bits(bf16_to_f32(h[e]))) : bf16_to_f32(h[e]);
+        }
+    }
+}
+
+template <int DUMMY = 0>
+__global__ __launch_bounds__(64) void had_rows_kernel(const void* x, int x_kind, void* y, int y_kind, int cols,
+                                                      const uint16_t* pre, const uint16_t* post, float scale) {
+    const int nb = cols / 128, npair = (nb + 1) / 2;
+    const int r = blockIdx.x / npair, pb = blockIdx.x - r * npair;
+    const int lane = threadIdx.x;
+    int b = 2 * pb + (lane >> 5);
+    const bool keep = b < nb;
+    if (!keep) b = 2 * pb;
+    const int c0 = 128 * b + 4 * (lane & 31);
+    const size_t i0 = (size_t)r * cols + c0;
+    float v[4];
+    load4_kind(x, x_kind, i0, v, pre != nullptr);
+    if (pre) {
+        const uint2 u = *reinterpret_cast<const uint2*>(pre + c0);
+        const uint16_t s[4] = {(uint16_t)(u.x & 0xffffu), (uint16_t)(u.x >> 16), (uint16_t)(u.y & 0xffffu),
+                               (uint16_t)(u.y >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = f16_bits_to_f32(f32_to_f16_bits(v[e] * f16_bits_to_f32(s[e])));
+    }
+    fwht128_x4(v);
+    float sv[4] = {1.f, 1.f, 1.f, 1.f};
+    if (post) {
+        const uint2 u = *reinterpret_cast<const uint2*>(post + c0);
+        sv[0] = f16_bits_to_f32((uint16_t)(u.x & 0xffffu)); sv[1] = f16_bits_to_f32((uint16_t)(u.x >> 16));
+        sv[2] = f16_bits_to_f32((uint16_t)(u.y & 0xffffu)); sv[3] = f16_bits_to_f32((uint16_t)(u.y >> 16));
+    }
+    if (!keep) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float o = v[e] * HAD_NORM;
+        if (scale != 1.0f) o = o * scale;
+        if (post) o = o * sv[e];
+        store_out(y, i0 + e, y_kind, o);
     }
 }
 

@@ -14,7 +14,7 @@ int launch_dequant<EXL3_BITS>(const DequantArgs& a) {
         constexpr int C = decltype(cbc)::value;
         if (a.suh) {
             const int blocks = (a.k16 / 8) * (a.n16 / 8);
-            hipLaunchKernelGGL((dequant_had_kernel<B, C>), dim3(blocks), dim3(64), 0, a.stream, a.trellis,
+            hipLaunchKernelGGL((dequant_had_kernel<B, C>), dim3(blocks), dim3(256), 0, a.stream, a.trellis,
                                a.k16, a.n16, a.suh, a.svh, a.out);
         } else {
             const int tiles = a.k16 * a.n16;

@@ -112,6 +112,16 @@ def _dequant_impl(trellis, suh, svh, bits, codebook, out):
                               _ptr(out), _stream(trellis.device)))
 
 
+_LIB.define("had_rows(Tensor x, Tensor(a!) y, Tensor? pre_scale, Tensor? post_scale, float scale) -> ()")
+
+
+def _had_rows_impl(x, y, pre_scale, post_scale, scale):
+    L = _lib.load()
+    cols = x.shape[-1]
+    _lib.check(L.exl3_had_rows(_ptr(x), OUT_KIND[x.dtype], _ptr(y), OUT_KIND[y.dtype], x.numel() // cols, cols,
+                               _ptr(pre_scale), _ptr(post_scale), float(scale), _stream(x.device)))
+
+
 def _gemm_impl(a, b, c, suh, svh, codebook, scratch):
     L = _lib.load()
     m, k = a.shape
@@ -180,6 +190,7 @@ def _gemm_group_impl(a, b, c, suh, svh, codebook, scratch):
 _LIB.impl("moe_prefill", _prefill_impl, "CUDA")
 _LIB.impl("gemm_group", _gemm_group_impl, "CUDA")
 _LIB.impl("dequant", _dequant_impl, "CUDA")
+_LIB.impl("had_rows", _had_rows_impl, "CUDA")
 _LIB.impl("gemm", _gemm_impl, "CUDA")
 _LIB.impl("moe_decode", _moe_impl, "CUDA")
 
@@ -232,6 +243,20 @@ def dequant_trellis(trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor,
     return out
 
 # ------------------------------------------------------------------ dense GEMV / GEMM
+
+
+def had_r_128(x: torch.Tensor, y: torch.Tensor, pre_scale: torch.Tensor | None, post_scale: torch.Tensor | None,
+              scale: float = 1.0) -> None:
+    """exllamav3_ext.had_r_128(input, output, pre_scale, post_scale, scale): y = H128 (x * pre) / sqrt(128)
+    * scale * post per 128-block of each row (recipe-lna/exllamav3/exl3.py.lna:190, 214).  x, y fp16 / bf16 /
+    fp32 with the same shape, contiguous, last dimension a multiple of 128; y may be x."""
+    _check(x.shape == y.shape and x.is_contiguous() and y.is_contiguous(), "x and y must be contiguous, same shape")
+    _check(x.dtype in OUT_KIND and y.dtype in OUT_KIND, "x and y must be fp16, bf16 or fp32")
+    _check(x.dim() >= 1 and x.shape[-1] % 128 == 0 and x.numel() > 0, "last dimension must be a multiple of 128")
+    for t in (pre_scale, post_scale):
+        _check(t is None or (t.dtype == torch.float16 and t.is_contiguous() and t.numel() >= x.shape[-1]),
+               "scales must be contiguous fp16 covering the last dimension")
+    torch.ops.exl3_amd.had_rows(x, y, pre_scale, post_scale, float(scale))
 
 
 def gemm_scratch(device: torch.device, m: int, k: int, n: int) -> torch.Tensor:

@@ -6,8 +6,10 @@ error behaviour, so the plugin's dispatch code can switch to this package:
   * ``LinearEXL3`` / ``make_linear_exl3`` / ``execute_exl3_linear`` -- the
     exllamav3 linear (recipe-lna/exllamav3/exl3.py.lna:16-218,
     recipe-lna/vllm_exl3_exl3.py.lna:889-926).  Up to AUTO_RECONSTRUCT_THRESHOLD
-    rows run the trellis-decode GEMV kernel; more rows reconstruct the
-    Hadamard-folded fp16 weight on the GPU and run one hgemm.
+    rows run the trellis-decode GEMV kernel; more rows reconstruct the fp16
+    weight on the GPU and run one hgemm, between row-Hadamard launches below
+    FUSED_RECONSTRUCT_MIN_ROWS rows and on the Hadamard-folded weight from
+    there on.
   * ``apply_exl3_experts`` and its helpers -- routed experts
     (recipe-lna/vllm_exl3_exl3.py.lna:951-1296, 1543-1569, 1707-1779): backend
     selection by VLLM_EXL3_MOE_KERNEL, strict levels by VLLM_EXL3_MOE_STRICT,
@@ -15,8 +17,8 @@ error behaviour, so the plugin's dispatch code can switch to this package:
     scratch, and the unique-expert LinearEXL3 loop.
   * ``run_exl3_group`` and its helpers -- one fused call for the EXL3 shards
     of a module that read the same input, by LNA_EXL3_DENSE_GROUP
-    (recipe-lna/vllm_exl3_exl3.py.lna:62-802; the cross-module T1 fans are
-    not built).
+    (recipe-lna/vllm_exl3_exl3.py.lna:62-802), and the cross-module T1 fans
+    whose later members read the fused call's cached outputs.
   * ``Exl3MoEMethod`` / ``Exl3LinearMethod`` -- create_weights /
     process_weights_after_loading / apply (recipe-lna/vllm_exl3_exl3.py.lna:2045-2307,
     2310-2853), importable without vLLM.
@@ -52,7 +54,15 @@ MUL1_MULTIPLIER = 0x83DCD12D
 MUL1_MARKER_SIGNED_INT32 = -2082680531
 EXL3_SUFFIXES = ("trellis", "suh", "svh", "mcg", "mul1")
 SWIGLU_LIMIT_DEFAULT = 10.0
-AUTO_RECONSTRUCT_THRESHOLD = 144
+# Rows up to AUTO_RECONSTRUCT_THRESHOLD take the decode GEMV; more take the
+# reconstruct path.  The reference switches at 144 rows
+# (recipe-lna/exllamav3/exl3.py.lna:10); on MI355X the two paths cross at
+# 48-64 rows on the 4096x4096, 4096x1536, 1536x4096 and 4096x12288 matrices
+# (at 144 rows the GEMV takes 2.3x the reconstruct path's time on 4096x4096).
+# From FUSED_RECONSTRUCT_MIN_ROWS rows the rotations are folded into the
+# reconstructed weight (the reference's rule, exl3.py.lna:184).
+AUTO_RECONSTRUCT_THRESHOLD = 64
+FUSED_RECONSTRUCT_MIN_ROWS = 1024
 MAX_RECONSTRUCT_SLICE_N = 32768
 MOE_TABLE_KEYS = ops.MOE_TABLE_KEYS
 PREFILL_MAX_PAIRS = 65536
@@ -149,15 +159,29 @@ class LinearEXL3:
         return self.reconstruct_hgemm(x, out_dtype)
 
     def reconstruct_hgemm(self, x: torch.Tensor, out_dtype) -> torch.Tensor:
-        """Many rows: reconstruct the original-basis weight (both rotations and
-        sign vectors folded in) on the GPU, then one fp16 GEMM
-        (recipe-lna/exllamav3/exl3.py.lna:161-218, its fused-reconstruct branch)."""
+        """Many rows (recipe-lna/exllamav3/exl3.py.lna:161-218).  Below
+        FUSED_RECONSTRUCT_MIN_ROWS rows the input and output rotations run as
+        row-Hadamard launches around a GEMM on the raw codebook matrix Wq; from
+        there on both rotations and sign vectors are folded into the
+        reconstructed weight and the GEMM reads x itself.  fp16 GEMM with fp32
+        accumulation (hipBLASLt)."""
         rows = x.numel() // x.shape[-1]
         x2 = x.view(rows, self.in_features)
-        if x2.dtype != torch.float16:
-            x2 = x2.to(torch.float16)
-        w = ops.dequant_trellis(self.trellis, self.suh, self.svh, self.K, self.mcg, self.mul1)
-        y = torch.matmul(x2, w).to(out_dtype or self.default_out_dtype)
+        dtype = out_dtype or self.default_out_dtype
+        if rows >= FUSED_RECONSTRUCT_MIN_ROWS:
+            x16 = x2 if x2.dtype == torch.float16 else x2.to(torch.float16)
+            w = ops.dequant_trellis(self.trellis, self.suh, self.svh, self.K, self.mcg, self.mul1)
+            y = torch.mm(x16, w) if dtype == torch.float16 else torch.mm(x16, w, out_dtype=torch.float32).to(dtype)
+        else:
+            xh = torch.empty((rows, self.in_features), dtype=torch.float16, device=x.device)
+            ops.had_r_128(x2, xh, self.suh, None, 1.0)
+            w = ops.reconstruct_weight(self.trellis, self.codebook)
+            y32 = torch.mm(xh, w, out_dtype=torch.float32)
+            y = torch.empty((rows, self.out_features), dtype=dtype if dtype in ops.OUT_KIND else torch.float32,
+                            device=x.device)
+            ops.had_r_128(y32, y, None, self.svh, 1.0)
+            if y.dtype != dtype:
+                y = y.to(dtype)
         if self.bias is not None:
             y += self.bias
         return y.view(*x.shape[:-1], self.out_features)

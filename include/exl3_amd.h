@@ -39,6 +39,20 @@ int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int cod
                  const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream);
 
 /*
+ * Row Hadamard: for every row r and 128-block b of x [rows][cols]
+ *   y[r][128b + i] = (H128 v / sqrt(128))[i] * scale * post_scale[128b + i],
+ *   v = x[r][128b ..] * pre_scale rounded to fp16 (as the GEMV input rotation
+ *   does; x converted to fp16 first), or x itself when pre_scale is NULL.
+ * Butterflies in fp32; either scale pointer may be NULL.  Replaces
+ * exllamav3_ext.had_r_128(input, output, pre_scale, post_scale, scale) as
+ * LinearEXL3.reconstruct_hgemm calls it around the fp16 GEMM
+ * (recipe-lna/exllamav3/exl3.py.lna:186-190, 213-214).  x_kind / y_kind:
+ * 0 = fp16, 1 = bf16, 2 = fp32; cols % 128 == 0; y may be x (same kind).
+ */
+int exl3_had_rows(const void* x, int x_kind, void* y, int y_kind, int64_t rows, int64_t cols,
+                  const uint16_t* pre_scale, const uint16_t* post_scale, float scale, void* stream);
+
+/*
  * c[m][n] = had_out(had_in(a . suh) . Wq) . svh, fp32 accumulation.
  * Replaces exllamav3 `exl3_gemm` (recipe-lna/exllamav3/exl3_gemm.cu.lna:336-364,
  * limits k % 16, n % 128 at :35-37) as used by LinearEXL3.forward for rows <= 144

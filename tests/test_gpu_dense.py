@@ -41,12 +41,15 @@ def test_reconstruct_primitive_streams(ops, dev, bits):
     assert np.array_equal(got, O.reconstruct_c(tiles, bits).view(np.uint16))
 
 
-@pytest.mark.parametrize("bits", [2, 3, 4, 6, 8])
-def test_dequant_trellis_bit_exact(ops, dev, bits):
-    print(f"dequant_trellis bits={bits}", flush=True)
-    L = synth.dense(256, 384, bits, seed=bits)
-    got = ops.dequant_trellis(to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev), bits)
-    ref = O.dequant_full_c(L["trellis"], L["suh"], L["svh"], bits)
+@pytest.mark.parametrize("bits,cb", [(2, O.CB_MCG), (3, O.CB_MCG), (4, O.CB_MCG), (6, O.CB_MCG), (8, O.CB_MCG),
+                                     (1, O.CB_MCG), (5, O.CB_MCG), (7, O.CB_MCG),
+                                     (3, O.CB_3INST), (4, O.CB_3INST), (2, O.CB_MUL1), (6, O.CB_MUL1)])
+def test_dequant_trellis_bit_exact(ops, dev, bits, cb):
+    print(f"dequant_trellis bits={bits} cb={cb}", flush=True)
+    L = synth.dense(256, 384, bits, seed=bits + 10 * cb)
+    got = ops.dequant_trellis(to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev), bits,
+                              mcg=cb == O.CB_MCG, mul1=cb == O.CB_MUL1)
+    ref = O.dequant_full_c(L["trellis"], L["suh"], L["svh"], bits, cb)
     g = got.cpu().numpy()
     bad = np.argwhere(g.view(np.uint16) != ref.view(np.uint16))
     if bad.size:
@@ -185,3 +188,53 @@ def test_argument_errors(ops, dev):
     with pytest.raises(RuntimeError):
         ops.exl3_gemm(torch.zeros((1, 256), dtype=torch.float16, device=dev), tr,
                       torch.empty((1, 256), device=dev), su, None, sv, -1, True, True, 0)
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 128), (5, 384), (33, 1024)])
+def test_had_r_128_against_oracle_rotations(ops, dev, rows, cols):
+    """The row Hadamard with a pre scale (fp16 in and out) is the GEMV input
+    rotation bit for bit; with a post scale (fp32 in and out) it is the output
+    rotation bit for bit.  Odd block counts cover the dropped half-wave."""
+    import torch
+
+    print(f"had_r_128 rows={rows} cols={cols}", flush=True)
+    rng = np.random.default_rng(rows * 7 + cols)
+    x16 = rng.standard_normal((rows, cols)).astype(np.float16)
+    suh = (rng.integers(0, 2, cols) * 2 - 1).astype(np.float16)
+    svh = ((rng.integers(0, 2, cols) * 2 - 1) * rng.uniform(0.5, 2.0, cols) / 64).astype(np.float16)
+    xh = torch.empty((rows, cols), dtype=torch.float16, device=dev)
+    ops.had_r_128(to_dev(x16, dev), xh, to_dev(suh, dev), None, 1.0)
+    assert np.array_equal(xh.cpu().numpy().view(np.uint16), O.had_in_c(x16, suh).view(np.uint16))
+    c = rng.standard_normal((rows, cols)).astype(np.float32)
+    y = to_dev(c, dev)
+    ops.had_r_128(y, y, None, to_dev(svh, dev), 1.0)                  # in place
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), O.had_out_c(c, svh).view(np.uint32))
+
+
+def test_had_r_128_kinds_scale_and_errors(ops, dev):
+    """bf16 input rounds through fp16 before the pre scale; the scale argument
+    multiplies after the 1/sqrt(128); outputs in every kind agree with an fp64
+    Sylvester-Hadamard product within their rounding."""
+    import torch
+    from scipy.linalg import hadamard
+
+    rng = np.random.default_rng(3)
+    rows, cols = 4, 256
+    x = rng.standard_normal((rows, cols)).astype(np.float32)
+    suh = (rng.integers(0, 2, cols) * 2 - 1).astype(np.float16)
+    H = hadamard(128).astype(np.float64) / np.sqrt(128.0)
+    xb = torch.from_numpy(x).to(torch.bfloat16)
+    x_in = xb.float().numpy().astype(np.float16).astype(np.float64) * suh.astype(np.float64)
+    want = np.concatenate([x_in[:, b:b + 128] @ H for b in range(0, cols, 128)], axis=1) * 0.5
+    for out_dtype, tol in ((torch.float32, 1e-5), (torch.float16, 2e-3), (torch.bfloat16, 1e-2)):
+        y = torch.empty((rows, cols), dtype=out_dtype, device=dev)
+        ops.had_r_128(xb.to(dev), y, to_dev(suh, dev), None, 0.5)
+        got = y.float().cpu().numpy()
+        assert np.max(np.abs(got - want)) <= tol * max(1.0, np.max(np.abs(want))), out_dtype
+    with pytest.raises(RuntimeError):
+        ops.had_r_128(torch.zeros((2, 100), device=dev), torch.zeros((2, 100), device=dev), None, None)
+    with pytest.raises(RuntimeError):
+        ops.had_r_128(torch.zeros((2, 128), device=dev), torch.zeros((2, 256), device=dev), None, None)
+    with pytest.raises(RuntimeError):
+        ops.had_r_128(torch.zeros((2, 128), device=dev), torch.zeros((2, 128), device=dev),
+                      torch.zeros(64, dtype=torch.float16, device=dev), None)

@@ -1,6 +1,7 @@
 """GPU parity of the plugin call surface (dsv4_carve_amd.vllm_exl3) against the
-oracle: LinearEXL3.forward on both of its paths (GEMV up to 144 rows,
-reconstruct + hgemm above), Exl3LinearMethod with several output shards,
+oracle: LinearEXL3.forward on its three paths (the GEMV up to
+AUTO_RECONSTRUCT_THRESHOLD rows, row Hadamards around an hgemm on Wq up to
+1024 rows, the folded weight beyond), Exl3LinearMethod with several output shards,
 apply_exl3_experts through the routed kernel and through the LinearEXL3 loop,
 expert_map remapping, decline / strict behaviour and the full Exl3MoEMethod
 create -> load -> finalize -> apply flow.  Tolerance: max-abs 2e-2, rel-L2 1e-3
@@ -29,7 +30,7 @@ def _linear(dev, lin, **kw):
                               mcg, **kw)
 
 
-@pytest.mark.parametrize("rows", [1, 5, 16, 40, 144, 200, 520])
+@pytest.mark.parametrize("rows", [1, 5, 16, 40, 64, 65, 144, 200, 520, 1100])
 def test_linear_forward_paths(dev, rows):
     import torch
 
@@ -55,6 +56,26 @@ def test_linear_forward_3d_fp16_out_and_bias(dev):
     assert_close(y.float().cpu().numpy().reshape(6, 512), want, max_abs=2e-2 + 4e-3)
     y2 = m.forward(to_dev(x, dev).view(2, 3, 256), {"reconstruct": True}, out_dtype=torch.float32)
     assert_close(y2.cpu().numpy().reshape(6, 512), want, max_abs=2e-2 + 4e-3)
+
+
+@pytest.mark.parametrize("rows", [300, 1030])
+@pytest.mark.parametrize("x_dtype", ["float16", "bfloat16"])
+def test_linear_reconstruct_dtypes(dev, rows, x_dtype):
+    """Both reconstruct paths (row-Hadamard launches around a GEMM on Wq below
+    1024 rows, the folded weight from there) with fp16/bf16 inputs and
+    fp16/bf16/fp32 outputs."""
+    import torch
+
+    lin = synth.dense(256, 384, 3, seed=47)
+    x = synth.activations(rows, 256, seed=48 + rows)
+    xt = to_dev(x, dev).to(getattr(torch, x_dtype))
+    want = O.linear(xt.float().cpu().numpy().astype(np.float16), lin["trellis"], lin["suh"], lin["svh"], 3)
+    m = _linear(dev, lin)
+    for out_dtype, extra in ((torch.float32, 0.0), (torch.float16, 4e-3), (torch.bfloat16, 3e-2)):
+        y = m.forward(xt, {}, out_dtype=out_dtype)
+        assert y.dtype == out_dtype and tuple(y.shape) == (rows, 384)
+        assert_close(y.float().cpu().numpy(), want, max_abs=2e-2 + extra, rel=1e-3 if extra < 1e-2 else 5e-3,
+                     what=f"reconstruct rows={rows} x={x_dtype} out={out_dtype}")
 
 
 def test_execute_exl3_linear(dev):
