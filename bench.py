@@ -341,6 +341,52 @@ def time_dense(dev, k, n, bits, rows_list, steps=40):
     return res
 
 
+LINEAR_SHAPES = ((4096, 4096), (4096, 12288))
+LINEAR_ROWS = (32, 64, 144, 512, 2048)
+
+
+def time_linear(dev, k, n, bits, rows_list, steps=20):
+    """us per LinearEXL3.forward call (the plugin's dense entry: the decode
+    GEMV up to its row threshold, the reconstruct path beyond), cold over
+    > 512 MB of distinct weight copies, fp16 output."""
+    import torch
+    from dsv4_carve_amd import ops
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(k * 17 + n + bits)
+    copies = max(2, -(-(600 << 20) // (k * n * bits // 8)))
+    mcg = torch.tensor([V.MCG_MARKER_SIGNED_INT32], dtype=torch.int32, device=dev)
+    mods = []
+    for _ in range(copies):
+        tr = torch.randint(-32768, 32767, (k // 16, n // 16, 16 * bits), dtype=torch.int16, device=dev, generator=g)
+        suh = (torch.randint(0, 2, (k,), device=dev, generator=g) * 2 - 1).to(torch.float16)
+        svh = ((torch.randint(0, 2, (n,), device=dev, generator=g) * 2 - 1) / k ** 0.5).to(torch.float16)
+        mods.append(V.make_linear_exl3(tr, suh, svh, mcg))
+    res = {}
+    for rows in rows_list:
+        x = torch.randn((rows, k), device=dev, generator=g).to(torch.float16)
+        ops.prepare_gemm(dev, rows, k, n)
+        order = [i % copies for i in range(steps)]
+        for i in order[:3]:
+            mods[i].forward(x, {}, out_dtype=torch.float16)
+        torch.cuda.synchronize()
+        stream = torch.cuda.Stream()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in order:
+                mods[i].forward(x, {}, out_dtype=torch.float16)
+        us = replay_median(graph, steps)[0]
+        path = ("gemv" if rows <= V.AUTO_RECONSTRUCT_THRESHOLD else
+                "reconstruct_folded" if rows >= V.FUSED_RECONSTRUCT_MIN_ROWS else "reconstruct")
+        res[str(rows)] = {"us": round(us, 2), "path": path,
+                          "tflops": round(2.0 * rows * k * n / (us * 1e-6) / 1e12, 1)}
+        del graph
+    del mods
+    torch.cuda.empty_cache()
+    return res
+
+
 MFMA_PEAK_F16 = 2.5e15
 
 
@@ -739,6 +785,11 @@ def main() -> int:
                 dense[key] = time_dense(dev, k, n, b, dense_rows)
                 print(f"[bench] dense {key}: {dense[key]}", file=sys.stderr, flush=True)
         extra["dense_gemv_cold"] = dense
+        lin = {}
+        for (k, n) in LINEAR_SHAPES:
+            lin[f"{k}x{n}_K3"] = time_linear(dev, k, n, 3, LINEAR_ROWS)
+            print(f"[bench] linear {k}x{n}_K3: {lin[f'{k}x{n}_K3']}", file=sys.stderr, flush=True)
+        extra["dense_linear_forward"] = lin
         if not a.no_cpu:
             # the single-linear CPU reference path (4096 x 4096, 6-bit, one row),
             # and every dense shape and width of the sweep at one row
