@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(HERE, "libexl3_amd.so")
 EXPORTS = (
     "exl3_last_error",
     "exl3_dequant",
+    "exl3_dequant_nk",
     "exl3_had_rows",
     "exl3_gemm_scratch_bytes",
     "exl3_gemm",
@@ -46,6 +47,7 @@ _F = ctypes.c_float
 _SIGS = {
     "exl3_last_error": ([], ctypes.c_char_p),
     "exl3_dequant": ([_P, _L, _L, _I, _I, _P, _P, _P, _P], _I),
+    "exl3_dequant_nk": ([_P, _L, _L, _I, _I, _P, _P, _P, _P], _I),
     "exl3_had_rows": ([_P, _I, _P, _I, _L, _L, _P, _P, _F, _P], _I),
     "exl3_gemm_scratch_bytes": ([_L, _L, _L], _L),
     "exl3_gemm": ([_P, _L, _L, _P, _L, _I, _I, _P, _P, _P, _I, _P, _L, _P], _I),

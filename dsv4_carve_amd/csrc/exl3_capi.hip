@@ -3,6 +3,7 @@
 //                              (raw variant  <- exllamav3 `reconstruct`, recipe-lna/exllamav3/exl3.py.lna:197)
 //   exl3_gemm               <- exl3_gemm        recipe-lna/exllamav3/exl3_gemm.cu.lna:336-364
 //                              (and the exl3_gemv entry, recipe-lna/lna2/bindings.cpp:135-148)
+//   exl3_dequant_nk            the same weight stored [n][k], for reconstruct_hgemm's GEMM
 //   exl3_had_rows           <- exllamav3_ext.had_r_128  recipe-lna/exllamav3/exl3.py.lna:190, 214
 //   exl3_gemm_scratch_bytes    scratch sizing for exl3_gemm
 //   exl3_gemm_group         <- exl3_mgemm with a broadcast A (same-input fan)
@@ -33,11 +34,8 @@ namespace exl3 {
 
 using namespace exl3;
 
-extern "C" {
-
-int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int codebook,
-                 const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream) {
-    clear_error();
+static int dequant_impl(const int16_t* trellis, int64_t k, int64_t n, int bits, int codebook, const uint16_t* suh,
+                        const uint16_t* svh, uint16_t* out, void* stream, bool nk) {
     if (!trellis || !out) return fail("null pointer");
     if (k <= 0 || n <= 0 || k % 16 || n % 16) return fail("k and n must be positive multiples of 16");
     const bool had = suh != nullptr || svh != nullptr;
@@ -46,9 +44,23 @@ int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int cod
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const int k16 = (int)(k / 16), n16 = (int)(n / 16);
     if (codebook < CB_3INST || codebook > CB_MUL1) return fail("codebook must be 0 (3inst), 1 (mcg) or 2 (mul1)");
-    const DequantArgs args{trellis, k16, n16, codebook, had ? suh : nullptr, had ? svh : nullptr, out, s};
+    const DequantArgs args{trellis, k16, n16, codebook, had ? suh : nullptr, had ? svh : nullptr, out, s, nk};
     EXL3_BITS_SWITCH(bits, return launch_dequant<B_>(args));
     return 0;
+}
+
+extern "C" {
+
+int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int codebook,
+                 const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream) {
+    clear_error();
+    return dequant_impl(trellis, k, n, bits, codebook, suh, svh, out, stream, false);
+}
+
+int exl3_dequant_nk(const int16_t* trellis, int64_t k, int64_t n, int bits, int codebook,
+                    const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream) {
+    clear_error();
+    return dequant_impl(trellis, k, n, bits, codebook, suh, svh, out, stream, true);
 }
 
 int exl3_had_rows(const void* x, int x_kind, void* y, int y_kind, int64_t rows, int64_t cols,

@@ -12,30 +12,57 @@ namespace exl3 {
 
 // ---------------------------------------------------------------- dequant (raw)
 
-// One lane per tile; writes the 16x16 fp16 block in row-major [K][N].
-template <int BITS, int CB>
+// One lane per tile; writes the 16x16 fp16 block in row-major [K][N], or with
+// NK in row-major [N][K] (the transposed operand, which hipBLASLt's fp16 GEMM
+// reads faster).  With NK neighbouring lanes take tiles neighbouring along k,
+// so each of a lane's 16 n-rows lands next to its neighbours' in memory.
+template <int BITS, int CB, bool NK = false>
 __global__ __launch_bounds__(64) void dequant_raw_kernel(const int16_t* __restrict__ trellis,
                                                          int k16, int n16, uint16_t* __restrict__ out) {
     const int tile = blockIdx.x * 64 + threadIdx.x;
     if (tile >= k16 * n16) return;
-    const int kt = tile / n16, nt = tile - kt * n16;
+    int kt, nt;
+    if constexpr (NK) {
+        nt = tile / k16;
+        kt = tile - nt * k16;
+    } else {
+        kt = tile / n16;
+        nt = tile - kt * n16;
+    }
     TileRegs<BITS> t;
-    load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) + (size_t)tile * tile_vecs<BITS>());
+    load_tile<BITS>(t, reinterpret_cast<const u32x4_t*>(trellis) + ((size_t)kt * n16 + nt) * tile_vecs<BITS>());
     const uint32_t* W = t.words();
-    const size_t N = (size_t)n16 * 16;
-    static_for<16>([&](auto KI) {
-        constexpr int k = decltype(KI)::value;
-        u32x4_t row[2];
-        static_for<8>([&](auto PI) {
-            constexpr int p = decltype(PI)::value;
-            const uint32_t lo = decode_half<BITS, CB, tile_t(k, 2 * p)>(W);
-            const uint32_t hi = decode_half<BITS, CB, tile_t(k, 2 * p + 1)>(W);
-            row[p >> 2][p & 3] = lo | (hi << 16);
+    if constexpr (NK) {
+        const size_t K = (size_t)k16 * 16;
+        static_for<16>([&](auto NI) {
+            constexpr int n = decltype(NI)::value;
+            u32x4_t col[2];
+            static_for<8>([&](auto PI) {
+                constexpr int p = decltype(PI)::value;
+                const uint32_t lo = decode_half<BITS, CB, tile_t(2 * p, n)>(W);
+                const uint32_t hi = decode_half<BITS, CB, tile_t(2 * p + 1, n)>(W);
+                col[p >> 2][p & 3] = lo | (hi << 16);
+            });
+            u32x4_t* o = reinterpret_cast<u32x4_t*>(out + (size_t)(nt * 16 + n) * K + kt * 16);
+            o[0] = col[0];
+            o[1] = col[1];
         });
-        u32x4_t* o = reinterpret_cast<u32x4_t*>(out + (size_t)(kt * 16 + k) * N + nt * 16);
-        o[0] = row[0];
-        o[1] = row[1];
-    });
+    } else {
+        const size_t N = (size_t)n16 * 16;
+        static_for<16>([&](auto KI) {
+            constexpr int k = decltype(KI)::value;
+            u32x4_t row[2];
+            static_for<8>([&](auto PI) {
+                constexpr int p = decltype(PI)::value;
+                const uint32_t lo = decode_half<BITS, CB, tile_t(k, 2 * p)>(W);
+                const uint32_t hi = decode_half<BITS, CB, tile_t(k, 2 * p + 1)>(W);
+                row[p >> 2][p & 3] = lo | (hi << 16);
+            });
+            u32x4_t* o = reinterpret_cast<u32x4_t*>(out + (size_t)(kt * 16 + k) * N + nt * 16);
+            o[0] = row[0];
+            o[1] = row[1];
+        });
+    }
 }
 
 // ---------------------------------------------------------------- dequant (Hadamard folded)
@@ -122,7 +149,7 @@ __device__ __forceinline__ void had_rows(const uint32_t* W, int kt, int nt, floa
     });
 }
 
-template <int BITS, int CB>
+template <int BITS, int CB, bool NK = false>
 __global__ __launch_bounds__(256) void dequant_had_kernel(const int16_t* __restrict__ trellis, int k16,
                                                           int n16, const uint16_t* __restrict__ suh,
                                                           const uint16_t* __restrict__ svh,
@@ -167,8 +194,26 @@ __global__ __launch_bounds__(256) void dequant_had_kernel(const int16_t* __restr
             v[i + h] = a - b;
         }
     const uint32_t* su = reinterpret_cast<const uint32_t*>(su4);
-    uint16_t* o16 = reinterpret_cast<uint16_t*>(mat);
     const float s32 = half ? -1.f : 1.f;
+    if constexpr (NK) {
+        // this lane's 64 values are consecutive along k in output row n = 128 bc + c
+        uint32_t pk[32];
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+            float x = bfly(v[j], shfl_xor(v[j], 32), s32);
+            x = x * HAD_NORM;
+            x = x * f16_bits_to_f32((uint16_t)(su[j >> 1] >> (16 * (j & 1))));
+            x = x * sv;
+            const uint32_t h = f32_to_f16_bits(x);
+            pk[j >> 1] = (j & 1) ? (pk[j >> 1] | (h << 16)) : h;
+        }
+        const size_t K = (size_t)k16 * 16;
+        u32x4_t* o = reinterpret_cast<u32x4_t*>(out + (size_t)(128 * bc + c) * K + 128 * br + 64 * half);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = u32x4_t{pk[4 * i], pk[4 * i + 1], pk[4 * i + 2], pk[4 * i + 3]};
+        return;
+    }
+    uint16_t* o16 = reinterpret_cast<uint16_t*>(mat);
 #pragma unroll
     for (int j = 0; j < 64; ++j) {
         float x = bfly(v[j], shfl_xor(v[j], 32), s32);
@@ -684,6 +729,7 @@ inline GemvPlan gemv_fan_plan(int64_t rows, int64_t k, int64_t total_cb, int cus
 struct DequantArgs {
     const int16_t* trellis; int k16, n16; int codebook;
     const uint16_t* suh; const uint16_t* svh; uint16_t* out; hipStream_t stream;
+    bool nk;                 // write [n][k] instead of [k][n]
 };
 struct GemvArgs {
     const uint16_t* x; const int16_t* trellis; const uint16_t* suh; const uint16_t* svh;

@@ -14,12 +14,20 @@ int launch_dequant<EXL3_BITS>(const DequantArgs& a) {
         constexpr int C = decltype(cbc)::value;
         if (a.suh) {
             const int blocks = (a.k16 / 8) * (a.n16 / 8);
-            hipLaunchKernelGGL((dequant_had_kernel<B, C>), dim3(blocks), dim3(256), 0, a.stream, a.trellis,
-                               a.k16, a.n16, a.suh, a.svh, a.out);
+            if (a.nk)
+                hipLaunchKernelGGL((dequant_had_kernel<B, C, true>), dim3(blocks), dim3(256), 0, a.stream, a.trellis,
+                                   a.k16, a.n16, a.suh, a.svh, a.out);
+            else
+                hipLaunchKernelGGL((dequant_had_kernel<B, C, false>), dim3(blocks), dim3(256), 0, a.stream,
+                                   a.trellis, a.k16, a.n16, a.suh, a.svh, a.out);
         } else {
             const int tiles = a.k16 * a.n16;
-            hipLaunchKernelGGL((dequant_raw_kernel<B, C>), dim3((tiles + 63) / 64), dim3(64), 0, a.stream,
-                               a.trellis, a.k16, a.n16, a.out);
+            if (a.nk)
+                hipLaunchKernelGGL((dequant_raw_kernel<B, C, true>), dim3((tiles + 63) / 64), dim3(64), 0, a.stream,
+                                   a.trellis, a.k16, a.n16, a.out);
+            else
+                hipLaunchKernelGGL((dequant_raw_kernel<B, C, false>), dim3((tiles + 63) / 64), dim3(64), 0,
+                                   a.stream, a.trellis, a.k16, a.n16, a.out);
         }
     };
     switch (a.codebook) {

@@ -112,6 +112,17 @@ def _dequant_impl(trellis, suh, svh, bits, codebook, out):
                               _ptr(out), _stream(trellis.device)))
 
 
+_LIB.define("dequant_nk(Tensor trellis, Tensor? suh, Tensor? svh, int bits, int codebook, Tensor(a!) out) -> ()")
+
+
+def _dequant_nk_impl(trellis, suh, svh, bits, codebook, out):
+    L = _lib.load()
+    k = trellis.shape[0] * 16
+    n = trellis.shape[1] * 16
+    _lib.check(L.exl3_dequant_nk(_ptr(trellis), k, n, int(bits), int(codebook), _ptr(suh), _ptr(svh),
+                                 _ptr(out), _stream(trellis.device)))
+
+
 _LIB.define("had_rows(Tensor x, Tensor(a!) y, Tensor? pre_scale, Tensor? post_scale, float scale) -> ()")
 
 
@@ -190,6 +201,7 @@ def _gemm_group_impl(a, b, c, suh, svh, codebook, scratch):
 _LIB.impl("moe_prefill", _prefill_impl, "CUDA")
 _LIB.impl("gemm_group", _gemm_group_impl, "CUDA")
 _LIB.impl("dequant", _dequant_impl, "CUDA")
+_LIB.impl("dequant_nk", _dequant_nk_impl, "CUDA")
 _LIB.impl("had_rows", _had_rows_impl, "CUDA")
 _LIB.impl("gemm", _gemm_impl, "CUDA")
 _LIB.impl("moe_decode", _moe_impl, "CUDA")
@@ -216,6 +228,30 @@ def reconstruct_weight(trellis: torch.Tensor, codebook: int = CB_MCG) -> torch.T
     out = torch.empty((trellis.shape[0] * 16, trellis.shape[1] * 16), dtype=torch.float16,
                       device=trellis.device)
     torch.ops.exl3_amd.dequant(trellis, None, None, bits, codebook, out)
+    return out
+
+
+def reconstruct_weight_nk(trellis: torch.Tensor, codebook: int = CB_MCG) -> torch.Tensor:
+    """Raw codebook matrix stored transposed: Wq^T fp16 [out, in] (bitwise reconstruct_weight(...).t())."""
+    bits = _check_trellis(trellis)
+    out = torch.empty((trellis.shape[1] * 16, trellis.shape[0] * 16), dtype=torch.float16,
+                      device=trellis.device)
+    torch.ops.exl3_amd.dequant_nk(trellis, None, None, bits, codebook, out)
+    return out
+
+
+def dequant_trellis_nk(trellis: torch.Tensor, suh: torch.Tensor, svh: torch.Tensor, K: int,
+                       mcg: bool = True, mul1: bool = False) -> torch.Tensor:
+    """dequant_trellis stored transposed: W^T fp16 [out, in], bitwise dequant_trellis(...).t()."""
+    _check_trellis(trellis, K)
+    _check(suh.dtype == torch.float16 and svh.dtype == torch.float16, "suh and svh must be float16")
+    _check(suh.numel() >= trellis.shape[0] * 16 and svh.numel() >= trellis.shape[1] * 16,
+           "suh/svh are too short")
+    _check(trellis.shape[0] % 8 == 0 and trellis.shape[1] % 8 == 0,
+           "trellis dimensions must reconstruct whole 128-element Hadamard blocks")
+    out = torch.empty((trellis.shape[1] * 16, trellis.shape[0] * 16), dtype=torch.float16,
+                      device=trellis.device)
+    torch.ops.exl3_amd.dequant_nk(trellis, suh.contiguous(), svh.contiguous(), K, codebook_id(mcg, mul1), out)
     return out
 
 

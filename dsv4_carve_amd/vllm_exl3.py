@@ -56,12 +56,13 @@ EXL3_SUFFIXES = ("trellis", "suh", "svh", "mcg", "mul1")
 SWIGLU_LIMIT_DEFAULT = 10.0
 # Rows up to AUTO_RECONSTRUCT_THRESHOLD take the decode GEMV; more take the
 # reconstruct path.  The reference switches at 144 rows
-# (recipe-lna/exllamav3/exl3.py.lna:10); on MI355X the two paths cross at
-# 48-64 rows on the 4096x4096, 4096x1536, 1536x4096 and 4096x12288 matrices
-# (at 144 rows the GEMV takes 2.3x the reconstruct path's time on 4096x4096).
-# From FUSED_RECONSTRUCT_MIN_ROWS rows the rotations are folded into the
-# reconstructed weight (the reference's rule, exl3.py.lna:184).
-AUTO_RECONSTRUCT_THRESHOLD = 64
+# (recipe-lna/exllamav3/exl3.py.lna:10); on MI355X the GEMV is faster up to 32
+# rows (one 32-row block) and the reconstruct path from 48 rows on the
+# 4096x4096, 4096x1536, 1536x4096 and 4096x12288 matrices (at 144 rows the
+# GEMV takes 2.8x its time on 4096x4096).  From FUSED_RECONSTRUCT_MIN_ROWS
+# rows the rotations are folded into the reconstructed weight (the
+# reference's rule, exl3.py.lna:184).
+AUTO_RECONSTRUCT_THRESHOLD = 32
 FUSED_RECONSTRUCT_MIN_ROWS = 1024
 MAX_RECONSTRUCT_SLICE_N = 32768
 MOE_TABLE_KEYS = ops.MOE_TABLE_KEYS
@@ -164,19 +165,20 @@ class LinearEXL3:
         row-Hadamard launches around a GEMM on the raw codebook matrix Wq; from
         there on both rotations and sign vectors are folded into the
         reconstructed weight and the GEMM reads x itself.  fp16 GEMM with fp32
-        accumulation (hipBLASLt)."""
+        accumulation (hipBLASLt), on the weight stored [out][in], the operand
+        layout it reads fastest."""
         rows = x.numel() // x.shape[-1]
         x2 = x.view(rows, self.in_features)
         dtype = out_dtype or self.default_out_dtype
         if rows >= FUSED_RECONSTRUCT_MIN_ROWS:
             x16 = x2 if x2.dtype == torch.float16 else x2.to(torch.float16)
-            w = ops.dequant_trellis(self.trellis, self.suh, self.svh, self.K, self.mcg, self.mul1)
-            y = torch.mm(x16, w) if dtype == torch.float16 else torch.mm(x16, w, out_dtype=torch.float32).to(dtype)
+            wt = ops.dequant_trellis_nk(self.trellis, self.suh, self.svh, self.K, self.mcg, self.mul1).t()
+            y = torch.mm(x16, wt) if dtype == torch.float16 else torch.mm(x16, wt, out_dtype=torch.float32).to(dtype)
         else:
             xh = torch.empty((rows, self.in_features), dtype=torch.float16, device=x.device)
             ops.had_r_128(x2, xh, self.suh, None, 1.0)
-            w = ops.reconstruct_weight(self.trellis, self.codebook)
-            y32 = torch.mm(xh, w, out_dtype=torch.float32)
+            wt = ops.reconstruct_weight_nk(self.trellis, self.codebook).t()
+            y32 = torch.mm(xh, wt, out_dtype=torch.float32)
             y = torch.empty((rows, self.out_features), dtype=dtype if dtype in ops.OUT_KIND else torch.float32,
                             device=x.device)
             ops.had_r_128(y32, y, None, self.svh, 1.0)

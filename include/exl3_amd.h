@@ -39,6 +39,16 @@ int exl3_dequant(const int16_t* trellis, int64_t k, int64_t n, int bits, int cod
                  const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream);
 
 /*
+ * The same matrix written transposed, out[n][k] (row-major), bit for bit the
+ * values exl3_dequant writes.  No counterpart in the reference: its
+ * reconstruct writes [k][n]; LinearEXL3.reconstruct_hgemm
+ * (recipe-lna/exllamav3/exl3.py.lna:161-218) uses this layout because
+ * hipBLASLt's fp16 GEMM reads a [n][k] operand faster on MI355X.
+ */
+int exl3_dequant_nk(const int16_t* trellis, int64_t k, int64_t n, int bits, int codebook,
+                    const uint16_t* suh, const uint16_t* svh, uint16_t* out, void* stream);
+
+/*
  * Row Hadamard: for every row r and 128-block b of x [rows][cols]
  *   y[r][128b + i] = (H128 v / sqrt(128))[i] * scale * post_scale[128b + i],
  *   v = x[r][128b ..] * pre_scale rounded to fp16 (as the GEMV input rotation

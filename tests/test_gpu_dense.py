@@ -238,3 +238,19 @@ def test_had_r_128_kinds_scale_and_errors(ops, dev):
     with pytest.raises(RuntimeError):
         ops.had_r_128(torch.zeros((2, 128), device=dev), torch.zeros((2, 128), device=dev),
                       torch.zeros(64, dtype=torch.float16, device=dev), None)
+
+
+@pytest.mark.parametrize("bits,cb", [(2, O.CB_MCG), (3, O.CB_MCG), (6, O.CB_MCG), (4, O.CB_3INST),
+                                     (3, O.CB_MUL1), (8, O.CB_MCG)])
+def test_dequant_nk_is_the_transpose(ops, dev, bits, cb):
+    """The [n][k] layouts hold bitwise the transposes of the raw and the
+    Hadamard-folded matrices, which are themselves the oracle's."""
+    print(f"dequant_nk bits={bits} cb={cb}", flush=True)
+    L = synth.dense(384, 256, bits, seed=60 + bits + cb)
+    tr, su, sv = to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev)
+    raw_t = ops.reconstruct_weight_nk(tr, cb).cpu().numpy()
+    assert raw_t.shape == (256, 384)
+    assert np.array_equal(raw_t.view(np.uint16).T, O.reconstruct_c(L["trellis"], bits, cb).view(np.uint16))
+    w_t = ops.dequant_trellis_nk(tr, su, sv, bits, mcg=cb == O.CB_MCG, mul1=cb == O.CB_MUL1).cpu().numpy()
+    ref = O.dequant_full_c(L["trellis"], L["suh"], L["svh"], bits, cb)
+    assert np.array_equal(w_t.view(np.uint16).T, ref.view(np.uint16))

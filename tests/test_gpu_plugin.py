@@ -30,7 +30,7 @@ def _linear(dev, lin, **kw):
                               mcg, **kw)
 
 
-@pytest.mark.parametrize("rows", [1, 5, 16, 40, 64, 65, 144, 200, 520, 1100])
+@pytest.mark.parametrize("rows", [1, 5, 16, 32, 33, 40, 64, 144, 200, 520, 1100])
 def test_linear_forward_paths(dev, rows):
     import torch
 
