@@ -48,10 +48,12 @@ struct PfLayout {
 __host__ __device__ inline int64_t pf_al(int64_t v) { return (v + 255) / 256 * 256; }
 
 // k-splits of the gate/up (K = hidden) and down (K = intermediate) GEMMs: as
-// many as keep an even number of 64-row steps per part, up to 4 and 2.  Each
-// part writes its own fp32 output (the output Hadamard and svh are linear, so
-// they apply per part); the activation and gather kernels add the parts in
-// order, so results do not depend on scheduling.
+// many as keep an even number of 64-row steps per part, up to 2 each (on the
+// 512-token layer 2/2 measured faster than 4/2, 1/2 and 2/1: fewer parts halve
+// the partials the activation reads, more parts shorten the launches' last
+// round).  Each part writes its own fp32 output (the output Hadamard and svh
+// are linear, so they apply per part); the activation and gather kernels add
+// the parts in order, so results do not depend on scheduling.
 inline int pf_ksplit(int64_t K, int cap) {
     int ks = cap;
     while (ks > 1 && K % (2 * STEP_K * ks)) ks /= 2;
@@ -60,7 +62,7 @@ inline int pf_ksplit(int64_t K, int cap) {
 
 inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
     PfLayout L;
-    L.ks_up = pf_ksplit(H, 4);
+    L.ks_up = pf_ksplit(H, 2);
     L.ks_down = pf_ksplit(I, 2);
     L.max_tiles = E + (pairs + PF_RB - 1) / PF_RB;
     int64_t o = 0;
