@@ -40,7 +40,7 @@ constexpr int PF_META_PAIRS = 0, PF_META_ERROR = 1, PF_META_TILES = 2;
 constexpr int PF_ERR_WIDTH = 1;          // an expert width outside bits_mask was routed (it contributed nothing)
 
 struct PfLayout {
-    int64_t meta, eoff, toff, tile_e, tile_r0, tile_n, pair_slot, pos, Xh, GU, AD, D, total;
+    int64_t meta, eoff, toff, tile_e, tile_r0, tile_n, pair_slot, pair_e, pos, Xh, GU, AD, D, total;
     int64_t max_tiles;
     int ks_up, ks_down;     // k-splits: GU is [ks_up][2][pairs][I], D is [ks_down][pairs][H]
 };
@@ -73,6 +73,7 @@ inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
     L.tile_r0 = o;   o = pf_al(o + L.max_tiles * 4);
     L.tile_n = o;    o = pf_al(o + L.max_tiles * 4);
     L.pair_slot = o; o = pf_al(o + pairs * 4);
+    L.pair_e = o;    o = pf_al(o + pairs * 4);
     L.pos = o;       o = pf_al(o + pairs * 4);
     L.Xh = o;        o = pf_al(o + 2 * pairs * H * 2);
     L.GU = o;        o = pf_al(o + (int64_t)L.ks_up * 2 * pairs * I * 4);

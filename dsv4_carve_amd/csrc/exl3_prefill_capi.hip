@@ -96,6 +96,7 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     for (int e = tid; e < P.E; e += nt) cnt[e] = off[e];
     __syncthreads();
     int* pair_slot = pat<int>(P.scratch, L.pair_slot);
+    int* pair_e = pat<int>(P.scratch, L.pair_e);
     int* pos = pat<int>(P.scratch, L.pos);
     for (int s = tid; s < P.P; s += nt) {
         const int e = pf_local(P, s, &bad);
@@ -103,35 +104,54 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
         if (e >= 0) {
             p = atomicAdd(&cnt[e], 1);
             pair_slot[p] = s;
+            pair_e[p] = e;
         }
         pos[s] = p;
     }
 }
 
-// ---------------------------------------------------------------- 2. input rotation (one wave per pair, projection and 512 columns)
+// ---------------------------------------------------------------- 2. input rotation (one wave per pair and 512 columns, both projections)
 //
 // Every wave issues all of its loads before any arithmetic: one wave looping
 // over the 32 blocks of a 4096-wide row waited for each block's loads in
-// turn (50 us per layer at 512 tokens).
+// turn (50 us per layer at 512 tokens).  The pair's expert comes from the
+// plan (no route lookup), and one wave rotates the gate and the up input of
+// its columns, so the chain of dependent loads (pair -> scale pointers ->
+// x and scales) is paid once for both.
 
 __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     const PfLayout& L = P.L;
     const int nch = (P.H + 511) / 512;
-    const int p = blockIdx.x / (2 * nch);
-    const int rem = blockIdx.x - p * 2 * nch;
-    const int proj = rem / nch, ch = rem - (rem / nch) * nch;
+    const int p = blockIdx.x / nch, ch = blockIdx.x - p * nch;
     if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
-    const int lane = threadIdx.x;
     const int s = pat<int>(P.scratch, L.pair_slot)[p];
-    const int tok = s / P.topk, e = P.rt.local(s, P.E);
+    const int e = pat<int>(P.scratch, L.pair_e)[p];
+    const int tok = s / P.topk;
     const int k0 = ch * 512, nblocks = min(HAD_MAX_BLOCKS, (P.H - k0) / 128);
-    const uint16_t* suh = reinterpret_cast<const uint16_t*>((proj ? P.usu : P.gsu)[e]) + k0;
-    RowIn in;
-    had_in_load(P.x, (size_t)tok * P.H + k0, suh, nblocks, in);
-    uint32_t* dst = reinterpret_cast<uint32_t*>(pat<uint16_t>(P.scratch, L.Xh) + ((size_t)proj * P.P + p) * P.H + k0);
+    const uint16_t* gsu = reinterpret_cast<const uint16_t*>(P.gsu[e]) + k0;
+    const uint16_t* usu = reinterpret_cast<const uint16_t*>(P.usu[e]) + k0;
+    RowIn g, u;
+    had_in_load(P.x, (size_t)tok * P.H + k0, gsu, nblocks, g);
+    {
+        const int lane = threadIdx.x & (WAVE - 1);
+        gptr_t<uint32_t> sp = as_global(reinterpret_cast<const uint32_t*>(usu) + lane);
+#pragma unroll
+        for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
+            if (b < nblocks) {
+                u.x[b] = g.x[b];
+                u.s[b] = sp[64 * b];
+            }
+    }
+    const int lane = threadIdx.x;
+    uint16_t* xh = pat<uint16_t>(P.scratch, L.Xh);
+    uint32_t* dg = reinterpret_cast<uint32_t*>(xh + (size_t)p * P.H + k0);
+    uint32_t* du = reinterpret_cast<uint32_t*>(xh + ((size_t)P.P + p) * P.H + k0);
 #pragma unroll
     for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
-        if (b < nblocks) dst[64 * b + lane] = had_in_pair(in.x[b], in.s[b], P.x_kind);
+        if (b < nblocks) {
+            dg[64 * b + lane] = had_in_pair(g.x[b], g.s[b], P.x_kind);
+            du[64 * b + lane] = had_in_pair(u.x[b], u.s[b], P.x_kind);
+        }
 }
 
 // ---------------------------------------------------------------- 4. activation + down input rotation (one wave per pair and 256 columns)
@@ -142,7 +162,7 @@ __global__ __launch_bounds__(64) void pf_act_kernel(PfParams P) {
     const int p = blockIdx.x / ncb, c0 = (blockIdx.x - p * ncb) * COLS;
     if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
     const int lane = threadIdx.x;
-    const int e = P.rt.local(pat<int>(P.scratch, L.pair_slot)[p], P.E);
+    const int e = pat<int>(P.scratch, L.pair_e)[p];
     const int col = c0 + 128 * (lane >> 5) + 4 * (lane & 31);
     const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I + col;
     const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I + col;
@@ -320,7 +340,7 @@ static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, 
     int rc;
     hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(1024), 0, s, P);
     if ((rc = check_launch())) return rc;
-    hipLaunchKernelGGL(pf_rotate_kernel, dim3(2 * P.P * ((hidden + 511) / 512)), dim3(WAVE), 0, s, P);
+    hipLaunchKernelGGL(pf_rotate_kernel, dim3(P.P * ((hidden + 511) / 512)), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
     const int64_t tiles = P.L.max_tiles;
     if ((rc = launch_widths(P, mask, codebook, false,
