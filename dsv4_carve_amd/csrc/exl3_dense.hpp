@@ -92,28 +92,6 @@ __device__ __forceinline__ int hb_pos(int r, int c) {
     return r * 128 + ((((c >> 2) ^ ((c >> 4) & 7)) << 2) | (c & 3));
 }
 
-// The value of lane (lane ^ M) within groups of 8 lanes, M = 1, 2 or 4, by
-// DPP moves (no LDS traffic): xor 1 and 2 are quad permutations, xor 4 a quad
-// reversal (xor 3) followed by the half-row mirror (xor 7).
-template <int M>
-__device__ __forceinline__ float dpp_xor(float v) {
-    const int x = __builtin_bit_cast(int, v);
-    if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
-    else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
-    else {
-        static_assert(M == 4, "xor 1, 2 or 4");
-        const int r = __builtin_amdgcn_mov_dpp(x, 0x1B, 0xF, 0xF, false);
-        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x141, 0xF, 0xF, false));
-    }
-}
-
-// Cross-lane butterfly of an element pair (a in the lane without the bit,
-// b in the lane with it): a + b and a - b, each one exactly rounded fp32
-// operation, as fma(+-1, own, partner).
-__device__ __forceinline__ float bfly(float own, float partner, float sgn) {
-    return __builtin_fmaf(sgn, own, partner);
-}
-
 // Phase 1 for tile rows K0..K0+3 of this lane's tile.
 template <int BITS, int CB, int K0>
 __device__ __forceinline__ void had_rows(const uint32_t* W, int kt, int nt, float* mat) {

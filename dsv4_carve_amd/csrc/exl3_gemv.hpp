@@ -309,6 +309,29 @@ __device__ __forceinline__ float4_t sum_partials(const float* p, uint32_t voff, 
 
 // ---------------------------------------------------------------- Hadamard (wave64)
 
+// The value of lane (lane ^ M) within groups of 8 lanes, M = 1, 2 or 4, by
+// DPP moves (no LDS traffic): xor 1 and 2 are quad permutations, xor 4 a quad
+// reversal (xor 3) followed by the half-row mirror (xor 7).
+template <int M>
+__device__ __forceinline__ float dpp_xor(float v) {
+    const int x = __builtin_bit_cast(int, v);
+    if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
+    else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
+    else {
+        static_assert(M == 4, "xor 1, 2 or 4");
+        const int r = __builtin_amdgcn_mov_dpp(x, 0x1B, 0xF, 0xF, false);
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x141, 0xF, 0xF, false));
+    }
+}
+
+// Cross-lane butterfly of an element pair (a in the lane without the bit,
+// b in the lane with it): a + b and a - b, each one exactly rounded fp32
+// operation, as fma(+-1, own, partner).
+__device__ __forceinline__ float bfly(float own, float partner, float sgn) {
+    return __builtin_fmaf(sgn, own, partner);
+}
+
+
 // In-place natural-order 128-point FWHT of a block held as 2 consecutive
 // elements per lane (element 2l+e in lane l), fp32, same add/sub sequence per
 // element as the scalar loop in orders/F1-ref/exl3_dequant.cuh:136-147.

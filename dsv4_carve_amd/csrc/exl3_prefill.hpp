@@ -155,13 +155,12 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
 // One (tile, 256-column block) of C[rows, N] = A[rows, K] . Wq[K, N], rows of A
 // at A + (row0 + i) * K (fp16, already rotated), i < nrows <= 32; epilogue
 // y = (H c / sqrt(128)) * svh written as fp32 to out + (row0 + i) * N.
-// Called by both waves of a block (`wave` 0 or 1; `valid` false: no item, but
-// the wave still takes part in the block's barriers); `tbuf` (32 rows x 256
-// fp32) is shared by the two waves, which use it in turn.
+// `valid` false: no item (the wave returns).
 template <int BITS, int CB>
-__device__ __forceinline__ void pf_tile(bool valid, int wave, const uint16_t* A, int row0, int nrows,
+__device__ __forceinline__ void pf_tile(bool valid, const uint16_t* A, int row0, int nrows,
                                         const int16_t* trellis, const uint16_t* svh, int K, int k0, int nsteps,
-                                        int N, int cb, float* out, float* tbuf) {
+                                        int N, int cb, float* out) {
+    if (!valid) return;
     const int lane = threadIdx.x & (WAVE - 1);
     const int g = lane >> 4, c = lane & 15;
     const int n16 = N / 16;
@@ -204,53 +203,66 @@ __device__ __forceinline__ void pf_tile(bool valid, int wave, const uint16_t* A,
             mma_tile2<BITS, CB, TWO>(t1.words(), ac, acc);
         }
     };
-    if (valid) {
-        if (nrows > 16) steps(std::true_type{});
-        else steps(std::false_type{});
-    }
+    if (nrows > 16) steps(std::true_type{});
+    else steps(std::false_type{});
 
-    // epilogue, one wave of the block after the other: both row blocks
-    // transposed through LDS at once (the accumulators die here), then one
-    // output row per pass
-    const int col = 128 * (lane >> 5) + 4 * (lane & 31);
-    for (int w = 0; w < 2; ++w) {
-        __syncthreads();                          // tbuf is free
-        if (wave == w && valid) {
+    // Epilogue in registers.  Accumulator acc[rb][n][i] is C[16 rb + 4 g + i]
+    // [16 c + n]: a 128-column Hadamard block is 8 lanes' (c = 8 h .. 8 h + 7)
+    // 16 values, so butterflies h = 1..8 run over n in registers and
+    // h = 16, 32, 64 across lanes c ^ 1, 2, 4 -- the stage order and pairs of
+    // the row transform, so the values are bitwise those of transforming the
+    // row whole.  Each lane then stores 16 consecutive columns of its rows.
+    float sv[16];
+    {
+        const u32x4_t* sp = reinterpret_cast<const u32x4_t*>(svh + cb * COLS + 16 * c);
+        const u32x4_t s0 = sp[0], s1 = sp[1];
 #pragma unroll
-            for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float4_t* t = reinterpret_cast<float4_t*>(tbuf + (16 * rb + 4 * g + i) * COLS + 16 * c);
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        t[q] = float4_t{acc[rb][4 * q][i], acc[rb][4 * q + 1][i], acc[rb][4 * q + 2][i],
-                                        acc[rb][4 * q + 3][i]};
-                }
+        for (int q = 0; q < 4; ++q) {
+            sv[2 * q] = f16_bits_to_f32((uint16_t)(s0[q] & 0xffffu));
+            sv[2 * q + 1] = f16_bits_to_f32((uint16_t)(s0[q] >> 16));
+            sv[8 + 2 * q] = f16_bits_to_f32((uint16_t)(s1[q] & 0xffffu));
+            sv[8 + 2 * q + 1] = f16_bits_to_f32((uint16_t)(s1[q] >> 16));
         }
-        __syncthreads();
-        if (wave == w && valid) {
-            float sv[4];
+    }
+    const float s1 = (c & 1) ? -1.f : 1.f, s2 = (c & 2) ? -1.f : 1.f, s4 = (c & 4) ? -1.f : 1.f;
+    const int nrb = nrows > 16 ? 2 : 1;
+    for (int rb = 0; rb < nrb; ++rb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) sv[e] = f16_bits_to_f32(svh[cb * COLS + col + e]);
-            for (int row = 0; row < nrows; ++row) {
-                const float4_t v4 = reinterpret_cast<const float4_t*>(tbuf + row * COLS)[col / 4];
-                float v[4] = {v4[0], v4[1], v4[2], v4[3]};
-                fwht128_x4(v);
-                float4_t o;
+        for (int i = 0; i < 4; ++i) {
+            float v[16];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = v[e] * HAD_NORM * sv[e];
-                *reinterpret_cast<float4_t*>(out + (size_t)(row0 + row) * N + cb * COLS + col) = o;
+            for (int n = 0; n < 16; ++n) v[n] = rb ? acc[1][n][i] : acc[0][n][i];
+#pragma unroll
+            for (int h = 1; h < 16; h <<= 1)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int a = (j / h) * 2 * h + (j % h);
+                    const float x0 = v[a], x1 = v[a + h];
+                    v[a] = x0 + x1;
+                    v[a + h] = x0 - x1;
+                }
+#pragma unroll
+            for (int n = 0; n < 16; ++n) v[n] = bfly(v[n], dpp_xor<1>(v[n]), s1);
+#pragma unroll
+            for (int n = 0; n < 16; ++n) v[n] = bfly(v[n], dpp_xor<2>(v[n]), s2);
+#pragma unroll
+            for (int n = 0; n < 16; ++n) v[n] = bfly(v[n], dpp_xor<4>(v[n]), s4);
+            const int row = 16 * rb + 4 * g + i;
+            if (row < nrows) {
+                float4_t* o = reinterpret_cast<float4_t*>(out + (size_t)(row0 + row) * N + cb * COLS + 16 * c);
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    o[q] = float4_t{v[4 * q] * HAD_NORM * sv[4 * q], v[4 * q + 1] * HAD_NORM * sv[4 * q + 1],
+                                    v[4 * q + 2] * HAD_NORM * sv[4 * q + 2], v[4 * q + 3] * HAD_NORM * sv[4 * q + 3]};
             }
         }
-    }
 }
 
 // Items: gate/up (DOWN = false) = (tile, projection, k-part, column block of
 // I); down (DOWN = true) = (tile, k-part, column block of H).  The items of
 // one (tile, projection, k-part) -- a group -- read the same rows of A.  Two
-// waves per block take two neighbouring column blocks of a group, sharing one
-// 32 KB transpose buffer (16 KB per wave leaves the LDS room for two waves per
-// SIMD).
+// waves per block take two neighbouring column blocks of a group (the
+// epilogue needs no LDS, so the waves share nothing but their A rows in L2).
 //
 // Workgroups go to the eight XCDs in turn (block b to XCD b % 8), and each XCD
 // has its own L2.  Group g is given to XCD g % 8 as consecutive blocks of that
@@ -280,7 +292,6 @@ template <int BITS, int BITS2, int CB, bool DOWN>
 __global__ __launch_bounds__(2 * WAVE)
 __attribute__((amdgpu_waves_per_eu((BITS <= 3 && BITS2 <= 3) ? 2 : 1, (BITS <= 3 && BITS2 <= 3) ? 2 : 8)))
 void pf_gemm_kernel(PfParams P) {
-    __shared__ float tbuf[PF_RB * COLS];
     const PfLayout& L = P.L;
     const int ncb = (DOWN ? P.H : P.I) / COLS;
     const int KS = DOWN ? L.ks_down : L.ks_up;
@@ -308,10 +319,10 @@ void pf_gemm_kernel(PfParams P) {
     float* out = DOWN ? pat<float>(P.scratch, L.D) + (size_t)ks * P.P * P.H
                       : pat<float>(P.scratch, L.GU) + ((size_t)ks * 2 + proj) * P.P * P.I;
     if (BITS2 == 0 || width == BITS)
-        pf_tile<BITS, CB>(valid, wave, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out, tbuf);
+        pf_tile<BITS, CB>(valid, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out);
     else
-        pf_tile<(BITS2 > 0 ? BITS2 : BITS), CB>(valid, wave, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K,
-                                                N, cb, out, tbuf);
+        pf_tile<(BITS2 > 0 ? BITS2 : BITS), CB>(valid, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N,
+                                                cb, out);
 }
 
 // Launchers of the grouped GEMM for one bit width, and for widths 3 and 2
