@@ -225,8 +225,14 @@ __device__ __forceinline__ uint32_t ld_dev(const uint32_t* p) {
 }
 // 16-byte device-scope store (one instruction; consecutive lanes should write
 // consecutive 16-byte chunks so the write-through traffic is whole lines).
+// The compiler inserts no wait states around an asm block, so the block
+// carries its own: a store of more than 8 bytes still reads its data registers
+// in the cycle after issue, and a VALU write to them right behind it (which
+// the register allocator is free to schedule) would change what is stored.
+// Its data must not come straight from MFMA accumulators (whose wait states
+// the block cannot know); callers store LDS-loaded or VALU-computed values.
 __device__ __forceinline__ void st_dev4(float* p, float4_t v) {
-    asm volatile("global_store_dwordx4 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
+    asm volatile("global_store_dwordx4 %0, %1, off sc1\n\ts_nop 1" : : "v"(p), "v"(v) : "memory");
 }
 __device__ __forceinline__ void st_dev2(uint32_t* p, uint2 v) {
     asm volatile("global_store_dwordx2 %0, %1, off sc1" : : "v"(p), "v"(v) : "memory");
