@@ -117,7 +117,9 @@ __device__ __forceinline__ half8_t a_from_words(const u32x4_t& lo, const u32x4_t
     return __builtin_bit_cast(half8_t, d);
 }
 
-// The 64 MFMAs of one decoded tile, each B operand applied to both row blocks.
+// The 64 MFMAs of one decoded tile in the clustered order at every width (in
+// the column order the 32-row accumulators leave no registers for the shared
+// funnels and the kernel spills), each B operand applied to both row blocks.
 // Software-pipelined by one operand: row block 1's MFMA on the previous B is
 // issued halfway through decoding the next B, so no two MFMAs are adjacent
 // (back to back, the second waits for the matrix pipe).
@@ -134,13 +136,13 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
     half8_t Bprev;
     static_for<64>([&](auto II) {
         constexpr int i = decltype(II)::value;
-        constexpr int n = i / 4, r = i % 4;
+        constexpr int n = mma_n(i, true), r = mma_r(i, true);
         constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
         u32x4_t b;
         b[0] = decode_pair<BITS, CB, T0 + 0>(W);
         b[1] = decode_pair<BITS, CB, T0 + 1>(W);
         if constexpr (TWO && i > 0) {
-            constexpr int np = (i - 1) / 4, rp = (i - 1) % 4;
+            constexpr int np = mma_n(i - 1, true), rp = mma_r(i - 1, true);
             acc[1][np] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[rp], Bprev, acc[1][np], 0, 0, 0);
         }
         b[2] = decode_pair<BITS, CB, T0 + 2>(W);
