@@ -85,7 +85,7 @@ __device__ __forceinline__ uint32_t win16(const uint32_t* W) {
 
 template <int BITS, int CB, int T>
 __device__ __forceinline__ uint32_t decode_pair(const uint32_t* W) {
-    if constexpr (CB == CB_MUL1 || 16 % BITS == 0) return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
+    if constexpr (CB == CB_MUL1) return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
     else return codebook_word<CB>(win16<BITS, T>(W));
 }
 template <int BITS, int CB, int T>
