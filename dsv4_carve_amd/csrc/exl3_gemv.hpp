@@ -34,9 +34,11 @@ __device__ __forceinline__ int xa_index(int m, int s, int nsteps_cap, int kk /*0
     return ((m * nsteps_cap + s) * 4 + g) * 16 + r * 4 + q;
 }
 
-// Where the 16-bit window of element T comes from: the low or high half of
-// either a tile word (free) or one funnel shift.  When 16 % BITS == 0 two
-// windows 16 bits apart share one funnel (high half = the earlier window).
+// Where the 16-bit window of element T comes from, for the decoders that read
+// it from a register half (MUL1, and the dequant kernels' codebook_half): the
+// low or high half of either a tile word (free) or one funnel shift.  When
+// 16 % BITS == 0 two windows 16 bits apart share one funnel (high half = the
+// earlier window).
 template <int BITS, int T>
 struct WinSel {
     static constexpr int NB = 256 * BITS;
@@ -65,11 +67,11 @@ __device__ __forceinline__ uint32_t win_src(const uint32_t* W) {
 // lies inside the 32 stream bits centred on their boundary, the funnel
 // (W[I1-1]:W[I1]) >> 16; that funnel is the same expression for every window
 // crossing the boundary (about 16/BITS of them), so the compiler computes it
-// once per boundary and each window costs one extract.  Used for the widths
-// that do not divide 16, where the single 32-bit multiply saves an
-// instruction per weight.  Widths dividing 16 keep the paired funnels and the
-// 16-bit multiplies that read a window straight from a register half (no
-// isolation, fewer instructions), which latency-bound launches favour.
+// once per boundary and each window costs one extract.  With the single
+// 32-bit multiply that follows, this takes fewer issue cycles at every width
+// than a funnel per pair of windows 16 bits apart feeding two 16-bit
+// multiplies that read the window halves in place (measured at 2, 3 and 4
+// bits).
 template <int BITS, int T>
 __device__ __forceinline__ uint32_t win16(const uint32_t* W) {
     using S = WinSel<BITS, T>;
@@ -142,38 +144,22 @@ __device__ __forceinline__ void zero_acc(float4_t (&acc)[16]) {
     for (int i = 0; i < 16; ++i) acc[i] = float4_t{0.f, 0.f, 0.f, 0.f};
 }
 
-// Order of a tile's 64 MFMAs (column group n, k-group r); each accumulator
-// takes its k-groups in order either way, so the sums are bitwise the same.
-// Column order: n outer, r inner.  Clustered order: (n & 7, r, n >> 3), so the
-// MFMAs of columns n and n + 8 at one k-group, whose eight windows are
-// consecutive in the stream, run back to back and a funnel that several of
-// those windows share (the boundary funnel of the 3/5/6/7-bit extract, the
-// 4-bit funnel holding windows t and t + 4) lives only across them.  Measured:
-// column order is faster for the 2- and 3-bit decode loops (the routed layer
-// at 16 rows 1.5%); at 4 bits and above, and in kernels serving every width,
-// the column order keeps those funnels live across half the tile and the MoE
-// kernels spill 37-112 registers, which the clustered order removes.
-template <int BITS>
-constexpr bool mma_clustered() { return BITS != 2 && BITS != 3; }
-__host__ __device__ constexpr int mma_n(int i, bool clustered) {
-    return clustered ? (i >> 3) + 8 * (i & 1) : i >> 2;
-}
-__host__ __device__ constexpr int mma_r(int i, bool clustered) { return clustered ? (i >> 1) & 3 : i & 3; }
-
 // Decodes all 256 weights of the lane's tile and accumulates 64 MFMAs into acc.
 template <int BITS, int CB>
 __device__ __forceinline__ void mma_tile(const uint32_t* W, const half8_t (&A)[4], float4_t (&acc)[16]) {
-    static_for<64>([&](auto II) {
-        constexpr int i = decltype(II)::value;
-        constexpr bool CL = mma_clustered<BITS>();
-        constexpr int n = mma_n(i, CL), r = mma_r(i, CL);
-        constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
-        u32x4_t b;
-        b[0] = decode_pair<BITS, CB, T0 + 0>(W);
-        b[1] = decode_pair<BITS, CB, T0 + 1>(W);
-        b[2] = decode_pair<BITS, CB, T0 + 2>(W);
-        b[3] = decode_pair<BITS, CB, T0 + 3>(W);
-        acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], __builtin_bit_cast(half8_t, b), acc[n], 0, 0, 0);
+    static_for<16>([&](auto NI) {
+        constexpr int n = decltype(NI)::value;
+        static_for<4>([&](auto RI) {
+            constexpr int r = decltype(RI)::value;
+            constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+            u32x4_t b;
+            b[0] = decode_pair<BITS, CB, T0 + 0>(W);
+            b[1] = decode_pair<BITS, CB, T0 + 1>(W);
+            b[2] = decode_pair<BITS, CB, T0 + 2>(W);
+            b[3] = decode_pair<BITS, CB, T0 + 3>(W);
+            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], __builtin_bit_cast(half8_t, b),
+                                                            acc[n], 0, 0, 0);
+        });
     });
 }
 

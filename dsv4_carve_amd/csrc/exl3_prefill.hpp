@@ -117,9 +117,19 @@ __device__ __forceinline__ half8_t a_from_words(const u32x4_t& lo, const u32x4_t
     return __builtin_bit_cast(half8_t, d);
 }
 
-// The 64 MFMAs of one decoded tile in the clustered order at every width (in
-// the column order the 32-row accumulators leave no registers for the shared
-// funnels and the kernel spills), each B operand applied to both row blocks.
+// MFMA i of a tile: column group n and k-group r, ordered (n & 7, r, n >> 3)
+// rather than mma_tile's n-outer order, so the MFMAs of columns n and n + 8
+// at one k-group, whose eight windows are consecutive in the stream, run back
+// to back: a funnel shared by the windows that straddle one word boundary
+// then lives only across them (in the n-outer order the 32-row accumulators
+// leave no registers for those funnels and the kernel spills).  Each
+// accumulator still takes its k-groups in order, so the sums are bitwise the
+// same.
+__host__ __device__ constexpr int pf_mma_n(int i) { return (i >> 3) + 8 * (i & 1); }
+__host__ __device__ constexpr int pf_mma_r(int i) { return (i >> 1) & 3; }
+
+// The 64 MFMAs of one decoded tile in pf_mma order, each B operand applied to
+// both row blocks.
 // Software-pipelined by one operand: row block 1's MFMA on the previous B is
 // issued halfway through decoding the next B, so no two MFMAs are adjacent
 // (back to back, the second waits for the matrix pipe).
@@ -136,13 +146,13 @@ __device__ __forceinline__ void mma_tile2(const uint32_t* W, const u32x4_t (&a)[
     half8_t Bprev;
     static_for<64>([&](auto II) {
         constexpr int i = decltype(II)::value;
-        constexpr int n = mma_n(i, true), r = mma_r(i, true);
+        constexpr int n = pf_mma_n(i), r = pf_mma_r(i);
         constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
         u32x4_t b;
         b[0] = decode_pair<BITS, CB, T0 + 0>(W);
         b[1] = decode_pair<BITS, CB, T0 + 1>(W);
         if constexpr (TWO && i > 0) {
-            constexpr int np = mma_n(i - 1, true), rp = mma_r(i - 1, true);
+            constexpr int np = pf_mma_n(i - 1), rp = pf_mma_r(i - 1);
             acc[1][np] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A1[rp], Bprev, acc[1][np], 0, 0, 0);
         }
         b[2] = decode_pair<BITS, CB, T0 + 2>(W);
