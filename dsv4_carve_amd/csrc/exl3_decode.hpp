@@ -86,7 +86,8 @@ __device__ __forceinline__ uint32_t win_lo(const uint32_t* W) {
 // or high (HI=true) half of `src`, then (x & 0x8fff8fff) ^ 0x3b603b60.
 // Two ops for the multiply (a 16x16-bit multiply and v_pk_mad_u16, both reading
 // the window from its register half, so `src` needs no masking) plus the
-// masked xor (v_bitop3_b32).
+// masked xor (v_bitop3_b32).  The dequant kernels decode this way; the GEMV
+// kernels isolate each window and use codebook_word.
 template <bool HI, uint32_t MULT, uint32_t ADD>
 __device__ __forceinline__ uint32_t mcg_bits(uint32_t src) {
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));

@@ -151,9 +151,9 @@ def test_gemm_other_codebooks(ops, dev, cb):
 @pytest.mark.parametrize("bits,cb", [(1, O.CB_MCG), (5, O.CB_MCG), (7, O.CB_MCG), (8, O.CB_MCG),
                                      (5, O.CB_3INST), (6, O.CB_3INST), (2, O.CB_3INST)])
 def test_gemm_other_widths(ops, dev, bits, cb):
-    """Widths and codebooks outside the sweep: the one-multiply decode where
-    the width does not divide 16 (5, 6, 7 bits) and the paired-funnel decode
-    where it does (1, 2, 8 bits), for MCG and 3INST."""
+    """Widths and codebooks outside the sweep (1, 5, 7, 8 bits; 3INST at 2, 5
+    and 6 bits): windows inside a word, on a word's half and across a word
+    boundary occur at each of them, for MCG and 3INST."""
     import torch
 
     got, ref = _gemm_case(ops, dev, 512, 512, bits, 3, torch.float32, cb=cb)

@@ -156,8 +156,8 @@ def test_rows_random_routes(small, m, path):
 @pytest.mark.parametrize("m", [1, 4, 16])
 def test_other_widths(dev, m, path):
     """Experts at 1, 5, 6, 7 and 8 bits in one layer, through the all-width
-    kernels: the one-multiply decode (widths not dividing 16) and the
-    paired-funnel decode (1 and 8 bits) side by side."""
+    kernels: every width's window positions (inside a word, on a word's half,
+    across a word boundary) side by side in one launch."""
     print(f"moe other widths m={m} {path}", flush=True)
     layer = Layer(dev, 8, 512, 256, [5, 6, 7, 1, 8, 5, 7, 6], seed=29)
     ids, w = synth.routing(m, 8, 6, seed=300 + m)
