@@ -97,11 +97,29 @@ def replay_median(graph, steps: int) -> tuple[float, list[float]]:
     return per[len(per) // 2], per
 
 
-def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, eager=False):
+def moe_c_call(lib, entry, x, out, layer, ids, w, scratch):
+    """One routed-MoE call straight through the C ABI of `lib` (the product
+    library or its timing-only twin), with the arguments ops.moe_decode /
+    ops.moe_prefill would pass."""
+    import torch
+    from dsv4_carve_amd import _lib, ops
+
+    t = layer.tables
+    rc = getattr(lib, entry)(
+        x.data_ptr(), 0, out.data_ptr(), 2, x.shape[0], layer.hidden, layer.inter, len(layer.bits), ids.shape[1],
+        *[int(t[k].data_ptr()) for k in ops.MOE_TABLE_KEYS], ids.data_ptr(), 0, w.data_ptr(), 2, None, 0,
+        layer.ebits.data_ptr(), 0, layer.mask, ops.CB_MCG, 10.0, scratch.data_ptr(), scratch.numel(),
+        int(torch.cuda.current_stream().cuda_stream))
+    if rc < 0:
+        raise _lib.Exl3Error(lib.exl3_last_error().decode())
+
+
+def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, eager=False, lib=None):
     """Returns (us per step, mean algorithmic bytes per step).  The K steps are
     replayed from one HIP graph, the median over REPLAYS timed replays after
     the clock has settled; `eager` launches them one by one instead (for
-    counter collection, which sees every dispatch)."""
+    counter collection, which sees every dispatch).  `lib`: call that
+    library's C ABI instead of the ops (the null-decode twin)."""
     import torch
     from dsv4_carve_amd import ops, synth
 
@@ -114,6 +132,9 @@ def time_layer(layer, dev, rows, topk, steps, warmup, seed, same_routing=False, 
     scratch = ops.moe_scratch(dev, layer.hidden, layer.inter, topk, rows=rows)
 
     def launch(i):
+        if lib is not None:
+            moe_c_call(lib, "exl3_moe_decode_routed", x, out, layer, ids[i % POOL], wts[i % POOL], scratch)
+            return
         ops.moe_decode(x, out, layer.tables, ids[i % POOL], wts[i % POOL], intermediate=layer.inter,
                        expert_bits=layer.ebits, bits_mask=layer.mask, scratch=scratch)
 
@@ -300,13 +321,23 @@ def time_fan(dev, k, ns, bits, rows_list, steps=40):
     return res
 
 
-def time_dense(dev, k, n, bits, rows_list, steps=40):
+def time_dense(dev, k, n, bits, rows_list, steps=40, lib=None):
     """us per call of the trellis-decode GEMV for each row count, cold (cycling
     through > 512 MB of distinct weight copies, so no copy is still in the
     256 MB MALL when reused) and warm (one copy).  Weights are seeded on the
-    device: this measures speed only (parity is the tests' job)."""
+    device: this measures speed only (parity is the tests' job).  `lib`: call
+    that library's exl3_gemm instead of the op (the null-decode twin)."""
     import torch
-    from dsv4_carve_amd import ops
+    from dsv4_carve_amd import _lib, ops
+
+    def gemm_into(x, t, su, sv, y):
+        if lib is None:
+            return ops.gemm_into(x, t, su, sv, y)
+        scratch = ops.gemm_scratch(dev, x.shape[0], k, n)
+        if lib.exl3_gemm(x.data_ptr(), x.shape[0], k, t.data_ptr(), n, bits, ops.CB_MCG, su.data_ptr(),
+                         sv.data_ptr(), y.data_ptr(), 0, scratch.data_ptr(), scratch.numel(),
+                         int(torch.cuda.current_stream().cuda_stream)) < 0:
+            raise _lib.Exl3Error(lib.exl3_last_error().decode())
 
     g = torch.Generator(device=dev)
     g.manual_seed(k * 131 + n * 7 + bits)
@@ -325,13 +356,13 @@ def time_dense(dev, k, n, bits, rows_list, steps=40):
         out = {}
         for mode, order in (("cold", [i % copies for i in range(steps)]), ("warm", [0] * steps)):
             for i in order[:3]:
-                ops.gemm_into(x, pool[i], suh, svh, y)
+                gemm_into(x, pool[i], suh, svh, y)
             torch.cuda.synchronize()
             stream = torch.cuda.Stream()
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph, stream=stream):
                 for i in order:
-                    ops.gemm_into(x, pool[i], suh, svh, y)
+                    gemm_into(x, pool[i], suh, svh, y)
             out[mode] = replay_median(graph, steps)[0]
         nb = dense_bytes(k, n, bits, rows)
         res[str(rows)] = {"us": round(out["cold"], 2), "GBps": round(nb / (out["cold"] * 1e-6) / 1e9, 1),
@@ -390,11 +421,12 @@ def time_linear(dev, k, n, bits, rows_list, steps=20):
 MFMA_PEAK_F16 = 2.5e15
 
 
-def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True):
+def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True, lib=None):
     """Prefill-shaped layer (grouped GEMMs): us per layer over `tokens` tokens
     with Zipf(1.1) top-k routing (`zipf`; otherwise the decode benchmark's
     N(0,1)-logit routing), fresh routing each step from a pool of 4.
-    Returns (us, algorithmic flops, algorithmic bytes, mean distinct experts)."""
+    Returns (us, algorithmic flops, algorithmic bytes, mean distinct experts).
+    `lib`: call that library's C ABI instead of the ops (the null-decode twin)."""
     import torch
     from dsv4_carve_amd import ops, synth
 
@@ -408,6 +440,9 @@ def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True):
     scratch = ops.moe_prefill_scratch(dev, tokens, layer.hidden, layer.inter, topk, n_exp)
 
     def launch(i):
+        if lib is not None:
+            moe_c_call(lib, "exl3_moe_prefill_routed", x, out, layer, ids[i % 4], wts[i % 4], scratch)
+            return
         ops.moe_prefill(x, out, layer.tables, ids[i % 4], wts[i % 4], intermediate=layer.inter,
                         expert_bits=layer.ebits, bits_mask=layer.mask, scratch=scratch)
 
@@ -572,43 +607,54 @@ def time_decode_ceiling(dev, iters: int = 512, reps: int = 5) -> dict:
     single-wave workgroups per SIMD, per bit width.  Returns the decoded
     weights per second (median of `reps` timed launches after one warm-up),
     the shader clock the loop ran at, and the SIMD cycles it spends per 64
-    weights (one weight per lane)."""
+    weights (one weight per lane).  `split` takes the loop apart at the same
+    residency, shorter runs: the decode alone, the MFMAs alone, and the whole
+    loop at four waves per SIMD."""
     import ctypes
 
     import torch
     from dsv4_carve_amd import build as B
 
     lib = ctypes.CDLL(B.PROBE_LIB)
-    lib.exl3_probe_decode.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
-                                      ctypes.c_void_p, ctypes.c_void_p]
-    lib.exl3_probe_decode.restype = ctypes.c_int
+    lib.exl3_probe_decode_mode.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.exl3_probe_decode_mode.restype = ctypes.c_int
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     simds = 4 * cus
-    blocks = 2 * simds
     g = torch.Generator().manual_seed(11)
     words = torch.randint(0, 2 ** 31 - 1, (64 * 8 * 6,), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
-    sink = torch.empty(blocks * 64, dtype=torch.float32, device=dev)
-    clk = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    sink = torch.empty(4 * simds * 64, dtype=torch.float32, device=dev)
+    clk = torch.zeros(2 * 4 * simds, dtype=torch.int64, device=dev)
     stream = int(torch.cuda.current_stream(dev).cuda_stream)
-    res = {}
-    for bits in (2, 3, 4, 6):
+
+    def run(bits, mode, waves, n_iter, n_reps):
+        blocks = waves * simds
         times = []
-        for _ in range(reps + 1):
+        for _ in range(n_reps + 1):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
-            assert lib.exl3_probe_decode(bits, blocks, iters, words.data_ptr(), sink.data_ptr(), clk.data_ptr(),
-                                         stream) == 0
+            assert lib.exl3_probe_decode_mode(bits, mode, blocks, n_iter, words.data_ptr(), sink.data_ptr(),
+                                              clk.data_ptr(), stream) == 0
             b.record()
             torch.cuda.synchronize()
             times.append(a.elapsed_time(b) * 1e-3)
-        t = sorted(times[1:])[reps // 2]
-        c = clk.view(blocks, 2).double().sum(0).tolist()
+        t = sorted(times[1:])[n_reps // 2]
+        c = clk[:2 * blocks].view(blocks, 2).double().sum(0).tolist()
         ghz = c[0] / c[1] * 0.1                      # reference ticks at 100 MHz
-        weights = blocks * iters * 16384.0
-        res[f"K{bits}"] = {"Gweights_per_s": round(weights / t / 1e9, 1), "clock_GHz": round(ghz, 3),
-                           "simd_cycles_per_64_weights": round(t * ghz * 1e9 * simds / (weights / 64.0), 2)}
+        weights = blocks * n_iter * 16384.0
+        return {"Gweights_per_s": round(weights / t / 1e9, 1), "clock_GHz": round(ghz, 3),
+                "simd_cycles_per_64_weights": round(t * ghz * 1e9 * simds / (weights / 64.0), 2)}
+
+    res = {f"K{bits}": run(bits, 0, 2, iters, reps) for bits in (2, 3, 4, 6)}
+    split = {}
+    for bits in (2, 3, 4, 6):
+        split[f"K{bits}"] = {
+            "decode_only": run(bits, 1, 2, iters // 4, 3)["simd_cycles_per_64_weights"],
+            "mfma_only": run(bits, 2, 2, iters // 4, 3)["simd_cycles_per_64_weights"],
+            "full_4_waves_per_simd": run(bits, 0, 4, iters // 4, 3)["simd_cycles_per_64_weights"]}
     del words, sink, clk
-    return {"workgroups": blocks, "iters": iters, "codebook": "MCG", **res}
+    return {"workgroups": 2 * simds, "iters": iters, "codebook": "MCG", **res,
+            "split_simd_cycles_per_64_weights": split}
 
 
 def decode_floor_us(rate: dict, rows: int, bits: list[int], hidden: int, inter: int, topk: int, seed: int) -> float:
@@ -662,7 +708,7 @@ def cpu_baseline(rows: int, bits: list[int], seed: int, us_ids: np.ndarray) -> d
     }
 
 
-EXTRA_LEGS = ("ceiling", "sweep", "rows17", "tp8", "prefill", "stack", "dense", "fan", "glue")
+EXTRA_LEGS = ("ceiling", "null", "sweep", "rows17", "tp8", "prefill", "stack", "dense", "fan", "glue")
 
 
 def main() -> int:
@@ -721,6 +767,26 @@ def main() -> int:
                                               "measured": round(us, 1)}
         extra["decode_ceiling"] = dc
         print(f"[bench] decode ceiling: {dc}", file=sys.stderr, flush=True)
+    if "null" in legs:
+        # The same workloads on the timing-only twin library (each decoded
+        # weight replaced by a loaded tile word): the skeleton of loads, MFMAs,
+        # stores and launches the decode runs on, measured, not argued.
+        from dsv4_carve_amd import _lib, build as B
+
+        twin = _lib.load_twin(B.NULL_LIB)
+        nl = {}
+        for m in (1, a.rows):
+            u_null, _ = time_layer(layer, dev, m, TOPK, a.steps, 3, seed=m, lib=twin)
+            u_real = us if m == a.rows else time_layer(layer, dev, m, TOPK, a.steps, 3, seed=m)[0]
+            nl[f"layer_rows{m}"] = {"null_decode_us": round(u_null, 2), "with_decode_us": round(u_real, 2)}
+        up_null = time_prefill(layer, dev, 512, TOPK, 10, 2, seed=4242, lib=twin)[0]
+        up_real = time_prefill(layer, dev, 512, TOPK, 10, 2, seed=4242)[0]
+        nl["prefill_512_tokens"] = {"null_decode_us": round(up_null, 1), "with_decode_us": round(up_real, 1)}
+        dn = time_dense(dev, 4096, 4096, 6, [1], lib=twin)["1"]["us"]
+        dr = time_dense(dev, 4096, 4096, 6, [1])["1"]["us"]
+        nl["dense_4096x4096_K6_rows1"] = {"null_decode_us": dn, "with_decode_us": dr}
+        extra["null_decode"] = {"library": "libexl3_null.so (EXL3_NULL_DECODE=1)", **nl}
+        print(f"[bench] null decode: {extra['null_decode']}", file=sys.stderr, flush=True)
     if "sweep" in legs:
         sweep = {}
         for m in (1, 2, 4, 8, 16):
@@ -754,7 +820,11 @@ def main() -> int:
             tp[f"K{kb}"] = {}
             for m in (1, 2, 4, 8, 16):
                 u, b = time_layer(tl, dev, m, 6, 40, 3, seed=100 + m)
-                tp[f"K{kb}"][str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1)}
+                # per call, the reference's method (recipe-lna/lna2/bench_lna.py:26-60):
+                # a > 512 MB flush before every call, 40 calls, p50 / p95
+                cold = layer_latency(tl, dev, m, 6, LATENCY_ITERS, seed=100 + m, cold=True)
+                tp[f"K{kb}"][str(m)] = {"us": round(u, 2), "GBps": round(b / (u * 1e-6) / 1e9, 1),
+                                        "per_call_cold": cold}
                 print(f"[bench] tp8 slice K{kb} m={m}: {tp[f'K{kb}'][str(m)]}", file=sys.stderr, flush=True)
             del tl
             torch.cuda.empty_cache()

@@ -30,6 +30,7 @@ EXPORTS = (
     "exl3_moe_decode_routed",
     "exl3_moe_noalloc_scratch_bytes",
     "exl3_moe_decode_noalloc",
+    "exl3_moe_noalloc_error",
     "exl3_moe_info",
     "exl3_moe_prefill_scratch_bytes",
     "exl3_moe_prefill",
@@ -69,6 +70,7 @@ _SIGS = {
                                  _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                  _P, _I, _P, _I, _P, _L,
                                  _P, _I, _I, _I, _F, _P], _I),
+    "exl3_moe_noalloc_error": ([_I, _P], _I),
     "exl3_moe_info": ([ctypes.POINTER(ctypes.c_int64), _I], _I),
     "exl3_moe_prefill_scratch_bytes": ([_L, _L, _L, _L, _L], _L),
     "exl3_moe_prefill": ([_P, _I, _P, _I, _L, _L, _L, _L, _L,
@@ -101,6 +103,20 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
             fn.restype = res
         _lib = lib
         return lib
+
+
+def load_twin(path: str) -> ctypes.CDLL:
+    """A library with this C ABI built another way (the benchmark's timing-only
+    null-decode build), typed from the same signature table; not cached, and
+    never the library the ops call."""
+    if not os.path.isfile(path):
+        raise ImportError(f"{path} is not built; run `python -m dsv4_carve_amd.build`")
+    lib = ctypes.CDLL(path)
+    for name, (args, res) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    return lib
 
 
 def check(rc: int) -> int:

@@ -13,9 +13,15 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libexl3_amd.so")
-# The HBM read-ceiling probe the benchmark times beside the decode kernels
-# (not part of the decode path's ABI, so a library of its own).
+# The HBM read-ceiling and decode-rate probes the benchmark times beside the
+# decode kernels (not part of the decode path's ABI, so a library of its own).
 PROBE_LIB = os.path.join(HERE, "libexl3_probe.so")
+# Timing-only twin of libexl3_amd.so built with EXL3_NULL_DECODE=1: the same
+# kernels with each decoded weight replaced by a loaded tile word, so the
+# benchmark can time the loads, MFMAs, stores and launches without the decode
+# (its outputs are meaningless; nothing but the benchmark loads it).
+NULL_LIB = os.path.join(HERE, "libexl3_null.so")
+NULL_DIR = os.path.join(OUT_DIR, "null")
 ARCH = os.environ.get("EXL3_OFFLOAD_ARCH", "gfx950")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -44,7 +50,7 @@ UNITS += [("exl3_prefill_inst.hip", ["-DEXL3_BITS=3", "-DEXL3_BITS2=2"], "exl3_p
 
 def _compile(unit):
     src, defs, obj = unit
-    out = os.path.join(OUT_DIR, obj)
+    out = obj if os.path.isabs(obj) else os.path.join(OUT_DIR, obj)
     cmd = [HIPCC, *COMMON, *defs, "-c", os.path.join(CSRC, src), "-o", out]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "packed-fp32-ops"
@@ -54,18 +60,26 @@ def _compile(unit):
     return out
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> str:
-    os.makedirs(OUT_DIR, exist_ok=True)
-    units = [u for u in UNITS if os.path.isfile(os.path.join(CSRC, u[0]))]
-    jobs = jobs or min(8, os.cpu_count() or 1)
-    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, units))
-    tmp = LIB + ".tmp"
+def _link(objs, lib):
+    tmp = lib + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
-        raise RuntimeError("link failed:\n" + r.stderr)
-    os.replace(tmp, LIB)
+        raise RuntimeError(f"link of {lib} failed:\n" + r.stderr)
+    os.replace(tmp, lib)
+
+
+def build(jobs: int | None = None, verbose: bool = True, null: bool = True) -> str:
+    os.makedirs(OUT_DIR, exist_ok=True)
+    os.makedirs(NULL_DIR, exist_ok=True)
+    units = [u for u in UNITS if os.path.isfile(os.path.join(CSRC, u[0]))]
+    null_units = [(src, [*defs, "-DEXL3_NULL_DECODE=1"], os.path.join(NULL_DIR, obj)) for src, defs, obj in units]
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, units + (null_units if null else [])))
+    _link(objs[:len(units)], LIB)
+    if null:
+        _link(objs[len(units):], NULL_LIB)
     tmp = PROBE_LIB + ".tmp"
     cmd = [HIPCC, *COMMON, "-shared", "-o", tmp, os.path.join(CSRC, "exl3_probe.hip")]
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -73,12 +87,14 @@ def build(jobs: int | None = None, verbose: bool = True) -> str:
         raise RuntimeError("probe build failed:\n" + r.stderr)
     os.replace(tmp, PROBE_LIB)
     if verbose:
-        print(f"built {LIB} from {len(objs)} objects, and {PROBE_LIB}", file=sys.stderr)
+        print(f"built {LIB} from {len(units)} objects, {PROBE_LIB}" + (f" and {NULL_LIB}" if null else ""),
+              file=sys.stderr)
     return LIB
 
 
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--no-null", action="store_true", help="skip the timing-only null-decode library")
     a = ap.parse_args()
-    build(a.jobs)
+    build(a.jobs, null=not a.no_null)

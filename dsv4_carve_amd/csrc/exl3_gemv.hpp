@@ -85,9 +85,19 @@ __device__ __forceinline__ uint32_t win16(const uint32_t* W) {
     }
 }
 
+// EXL3_NULL_DECODE=1 builds a timing-only library (libexl3_null.so): every
+// decoded B operand is replaced by a word of the loaded tile (a register move
+// at most), so its kernels keep the loads, MFMAs, stores and launches of the
+// real ones without the decode.  Their outputs are meaningless; the product
+// library is always built with 0.
+#ifndef EXL3_NULL_DECODE
+#define EXL3_NULL_DECODE 0
+#endif
+
 template <int BITS, int CB, int T>
 __device__ __forceinline__ uint32_t decode_pair(const uint32_t* W) {
-    if constexpr (CB == CB_MUL1) return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
+    if constexpr (EXL3_NULL_DECODE) return W[T % (8 * BITS)];
+    else if constexpr (CB == CB_MUL1) return codebook_pair<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
     else return codebook_word<CB>(win16<BITS, T>(W));
 }
 template <int BITS, int CB, int T>

@@ -6,6 +6,7 @@
 //   exl3_moe_max_rows       <- lna2_moe_max_rows       :484
 //   exl3_moe_info           <- lna2_moe_info           :494-505
 //   exl3_moe_decode_noalloc    (no counterpart: the routed decode on a fixed scratch)
+//   exl3_moe_noalloc_error     (no counterpart: that fixed scratch's error word)
 #include <math.h>
 #include <stddef.h>
 #include <stdlib.h>
@@ -263,6 +264,11 @@ __global__ __launch_bounds__(256) void zero_fill_kernel(uint4* p, int64_t n) {
         p[i] = make_uint4(0u, 0u, 0u, 0u);
 }
 
+// Clears one 32-bit word (the error word; the words around it keep their values).
+__global__ __launch_bounds__(64) void clear_word_kernel(int* p) {
+    if (threadIdx.x == 0) *p = 0;
+}
+
 // This device's fixed scratch.  On the first call on a device its control
 // words (the fixed region at the head of every layout) are zeroed by a fill
 // kernel on `stream`, ahead of the layer's launches.  A fill recorded into a
@@ -319,6 +325,33 @@ int exl3_moe_decode_noalloc(const void* x, int x_kind, void* out, int out_kind, 
                            gate_suh, gate_svh, up_trellis, up_suh, up_svh, down_trellis, down_suh, down_svh, rt,
                            expert_bits, bits, bits_mask, codebook, swiglu_limit, scratch, NOALLOC_SCRATCH_BYTES,
                            stream);
+}
+
+int exl3_moe_noalloc_error(int clear, void* stream) {
+    clear_error();
+    if (clear < 0 || clear > 2) return fail("clear must be 0 (read), 1 (clear the bits) or 2 (reset every control word)");
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone)
+        return fail("the error word is read with a stream synchronisation: not inside a graph capture");
+    char* scratch = nullptr;
+    if (int rc = fixed_scratch_for(st, &scratch)) return rc;
+    int* word = reinterpret_cast<int*>(scratch + exl3_moe_error_offset());
+    int value = 0;
+    if (hipMemcpyAsync(&value, word, sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+        return fail("cannot read the fixed scratch's error word");
+    if (clear == 2) {
+        // every counter, flag and the epoch back to zero, as at the first call
+        const int64_t ctrl_bytes = layout(COLS, COLS, 1).PA;
+        hipLaunchKernelGGL(zero_fill_kernel, dim3(256), dim3(256), 0, st, reinterpret_cast<uint4*>(scratch),
+                           ctrl_bytes / 16);
+        if (int rc = check_launch()) return rc;
+    } else if (clear == 1 && value) {
+        hipLaunchKernelGGL(clear_word_kernel, dim3(1), dim3(64), 0, st, word);
+        if (int rc = check_launch()) return rc;
+    }
+    return value;
 }
 
 }  // extern "C"

@@ -16,6 +16,12 @@
 // W weights cannot finish in less than W / rate, whatever the memory system
 // delivers.  The tile words are made opaque to the compiler every iteration,
 // so each iteration decodes and multiplies all 256 weights of the lane's tile.
+// Three modes split the loop's cost: the decode and the MFMAs together (the
+// loop the kernels run), the decode alone (each decoded B operand is handed
+// to an empty asm statement, which forces its computation and emits no
+// instruction), and the MFMAs alone (the B operands are the tile words
+// themselves, register moves at most).  The launch's block count sets the
+// waves per SIMD.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -44,7 +50,42 @@ __global__ __launch_bounds__(PROBE_THREADS) void probe_read_kernel(const u32x4_t
     sink[tid] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
-template <int BITS>
+enum ProbeMode : int { PROBE_FULL = 0, PROBE_DECODE_ONLY = 1, PROBE_MFMA_ONLY = 2 };
+
+// The decode kernels' mma_tile with the decode or the MFMA taken out (MODE).
+template <int BITS, int MODE>
+__device__ __forceinline__ void probe_tile(const uint32_t* W, const exl3::half8_t (&A)[4], exl3::float4_t (&acc)[16]) {
+    using namespace exl3;
+    if constexpr (MODE == PROBE_FULL) {
+        mma_tile<BITS, CB_MCG>(W, A, acc);
+    } else {
+        static_for<16>([&](auto NI) {
+            constexpr int n = decltype(NI)::value;
+            static_for<4>([&](auto RI) {
+                constexpr int r = decltype(RI)::value;
+                constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+                u32x4_t b;
+                if constexpr (MODE == PROBE_DECODE_ONLY) {
+                    b[0] = decode_pair<BITS, CB_MCG, T0 + 0>(W);
+                    b[1] = decode_pair<BITS, CB_MCG, T0 + 1>(W);
+                    b[2] = decode_pair<BITS, CB_MCG, T0 + 2>(W);
+                    b[3] = decode_pair<BITS, CB_MCG, T0 + 3>(W);
+                    asm volatile("" : : "v"(b));
+                } else {
+                    constexpr int NW = 8 * BITS;
+                    b[0] = W[(T0 + 0) % NW];
+                    b[1] = W[(T0 + 1) % NW];
+                    b[2] = W[(T0 + 2) % NW];
+                    b[3] = W[(T0 + 3) % NW];
+                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], __builtin_bit_cast(half8_t, b), acc[n],
+                                                                    0, 0, 0);
+                }
+            });
+        });
+    }
+}
+
+template <int BITS, int MODE>
 __global__ __launch_bounds__(64, 2) void probe_decode_kernel(const uint32_t* __restrict__ words, int iters,
                                                             float* __restrict__ sink, uint64_t* __restrict__ clk) {
     using namespace exl3;
@@ -63,7 +104,7 @@ __global__ __launch_bounds__(64, 2) void probe_decode_kernel(const uint32_t* __r
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
         for (int i = 0; i < 8 * BITS; ++i) asm volatile("" : "+v"(W[i]));
-        mma_tile<BITS, CB_MCG>(W, A, acc);
+        probe_tile<BITS, MODE>(W, A, acc);
     }
     const uint64_t c1 = __builtin_amdgcn_s_memtime(), t1 = __builtin_amdgcn_s_memrealtime();
     float sum = 0.f;
@@ -74,6 +115,27 @@ __global__ __launch_bounds__(64, 2) void probe_decode_kernel(const uint32_t* __r
         clk[2 * blockIdx.x] = c1 - c0;
         clk[2 * blockIdx.x + 1] = t1 - t0;
     }
+}
+
+template <int BITS>
+static int launch_probe_decode(int mode, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                               hipStream_t st) {
+    switch (mode) {
+        case PROBE_FULL:
+            hipLaunchKernelGGL((probe_decode_kernel<BITS, PROBE_FULL>), dim3(blocks), dim3(64), 0, st, words, iters,
+                               sink, clk);
+            break;
+        case PROBE_DECODE_ONLY:
+            hipLaunchKernelGGL((probe_decode_kernel<BITS, PROBE_DECODE_ONLY>), dim3(blocks), dim3(64), 0, st, words,
+                               iters, sink, clk);
+            break;
+        case PROBE_MFMA_ONLY:
+            hipLaunchKernelGGL((probe_decode_kernel<BITS, PROBE_MFMA_ONLY>), dim3(blocks), dim3(64), 0, st, words,
+                               iters, sink, clk);
+            break;
+        default: return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 extern "C" {
@@ -91,23 +153,29 @@ int exl3_probe_read(const void* buf, int64_t bytes, uint32_t* sink, int blocks, 
 int exl3_probe_threads(void) { return PROBE_THREADS; }
 
 // Launches `blocks` single-wave workgroups of the decode-rate probe at `bits`
-// (2, 3, 4 or 6; MCG codebook), each decoding 16384 weights per iteration for
-// `iters` iterations.  words: 64 * 8 * bits uint32 of tile data (any values);
-// sink: blocks * 64 floats; clk: 2 * blocks uint64 (per workgroup the shader
-// clock cycles and the 100 MHz reference ticks of its loop, which give the
-// clock the loop ran at).  Returns 0, or -1 on a bad argument or launch error.
-int exl3_probe_decode(int bits, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
-                      void* stream) {
+// (2, 3, 4 or 6; MCG codebook) in `mode` (0 decode + MFMA, 1 decode only, 2
+// MFMA only), each covering 16384 weights per iteration for `iters`
+// iterations.  words: 64 * 8 * bits uint32 of tile data (any values); sink:
+// blocks * 64 floats; clk: 2 * blocks uint64 (per workgroup the shader clock
+// cycles and the 100 MHz reference ticks of its loop, which give the clock the
+// loop ran at).  Returns 0, or -1 on a bad argument or launch error.
+int exl3_probe_decode_mode(int bits, int mode, int blocks, int iters, const uint32_t* words, float* sink,
+                           uint64_t* clk, void* stream) {
     if (!words || !sink || !clk || blocks < 1 || iters < 1) return -1;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     switch (bits) {
-        case 2: hipLaunchKernelGGL(probe_decode_kernel<2>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
-        case 3: hipLaunchKernelGGL(probe_decode_kernel<3>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
-        case 4: hipLaunchKernelGGL(probe_decode_kernel<4>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
-        case 6: hipLaunchKernelGGL(probe_decode_kernel<6>, dim3(blocks), dim3(64), 0, st, words, iters, sink, clk); break;
+        case 2: return launch_probe_decode<2>(mode, blocks, iters, words, sink, clk, st);
+        case 3: return launch_probe_decode<3>(mode, blocks, iters, words, sink, clk, st);
+        case 4: return launch_probe_decode<4>(mode, blocks, iters, words, sink, clk, st);
+        case 6: return launch_probe_decode<6>(mode, blocks, iters, words, sink, clk, st);
         default: return -1;
     }
-    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// The decode kernels' loop (mode 0) at `bits`.
+int exl3_probe_decode(int bits, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                      void* stream) {
+    return exl3_probe_decode_mode(bits, PROBE_FULL, blocks, iters, words, sink, clk, stream);
 }
 
 }  // extern "C"

@@ -57,11 +57,14 @@ class _ScratchPool:
     The kernels' counters must be zero before the first launch and are left
     zero by every launch (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296 is the
     same contract), so a buffer is zeroed exactly once, when it is created.
-    A buffer that a larger one replaces is kept alive until the process ends:
-    a graph captured while it was current keeps launching on its address."""
+    A buffer that a larger one replaces is freed (after the device finished
+    the work queued on it), unless a graph was captured while it was current:
+    such a graph keeps launching on its address, so that buffer is kept alive
+    until the process ends."""
 
     def __init__(self):
         self._bufs: dict[tuple[int, str], torch.Tensor] = {}
+        self._captured: set[tuple[int, str]] = set()
         self._retired: list[torch.Tensor] = []
         self._lock = threading.Lock()
 
@@ -70,15 +73,24 @@ class _ScratchPool:
         key = (int(idx), purpose)
         with self._lock:
             buf = self._bufs.get(key)
+            capturing = torch.cuda.is_current_stream_capturing()
             if buf is None or buf.numel() < nbytes:
-                if torch.cuda.is_current_stream_capturing():
+                if capturing:
                     raise RuntimeError(
                         f"exl3 {purpose} scratch was not prewarmed for device {idx} "
                         f"(need {nbytes} bytes during graph capture)")
                 if buf is not None:
-                    self._retired.append(buf)
+                    if key in self._captured:
+                        self._retired.append(buf)
+                        self._captured.discard(key)
+                    elif buf.is_cuda:
+                        torch.cuda.synchronize(buf.device)
+                    del self._bufs[key]
+                    del buf
                 buf = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
+            if capturing:
+                self._captured.add(key)
             return buf
 
     def current(self, device: torch.device, purpose: str) -> torch.Tensor | None:
@@ -472,7 +484,12 @@ def moe_scratch_bytes(hidden: int, intermediate: int, topk: int, rows: int = 16)
 
 
 def moe_scratch(device: torch.device, hidden: int, intermediate: int, topk: int, rows: int = 16) -> torch.Tensor:
-    """The shared per-device MoE scratch (zeroed once, self-resetting afterwards)."""
+    """The shared per-device MoE scratch (zeroed once, self-resetting afterwards).
+    Up to 16 rows share one size; a call of more rows sizes it once for
+    moe_max_rows(), so batches growing past 16 rows allocate one more buffer,
+    not one per row count."""
+    if rows > 16:
+        rows = moe_max_rows()
     return SCRATCH.get(device, "moe", moe_scratch_bytes(hidden, intermediate, topk, rows))
 
 

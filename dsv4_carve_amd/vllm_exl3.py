@@ -768,43 +768,38 @@ def _validate_lna_pointer_contract(inners, hidden: int, intermediate: int) -> No
                 raise RuntimeError(f"expert {e} {name}: codebook differs from the layer's")
 
 
-_LNA2_SCRATCH: dict[int, torch.Tensor] = {}
-_LNA2_SCRATCH_RETIRED: list[torch.Tensor] = []
 LNA2_MAX_TOPK = 9            # routed top-k plus a shared expert appended as one more slot
 
 
 def _lna2_scratch_for(layer, device: torch.device) -> torch.Tensor:
-    """The shared routed-MoE scratch of this device, zeroed once on creation and
+    """The shared routed-MoE decode scratch of this device (ops.SCRATCH's "moe"
+    buffer, the one ops.moe_decode uses), zeroed once on creation and
     self-resetting after (recipe-lna/vllm_exl3_exl3.py.lna:1276-1296).  Sized
     for the largest top-k and row count the decode kernels take, so a route
     with a shared-expert slot or a batch of up to lna2_max_rows() rows never
-    needs a bigger buffer at apply time (which capture forbids).
+    needs a bigger buffer at apply time (which capture forbids), and every
+    layer of the model shares it: layers of other shapes need no more.
     One launch at a time per device: launches on concurrent streams would share
-    it.  A replaced buffer stays alive: graphs captured on it keep its address."""
+    it."""
     hidden = int(layer._exl3_hidden_size)
     inter = int(layer._exl3_intermediate_local)
     nbytes = ops.moe_scratch_bytes(hidden, inter, LNA2_MAX_TOPK, rows=lna2_max_rows())
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    buf = _LNA2_SCRATCH.get(int(idx))
-    if buf is None or buf.numel() < nbytes:
-        if torch.cuda.is_current_stream_capturing():
+    if torch.cuda.is_current_stream_capturing():
+        buf = ops.SCRATCH.current(device, "moe")
+        if buf is None or buf.numel() < nbytes:
             raise RuntimeError("LNA2 scratch was not prewarmed for this device")
-        if buf is not None:
-            _LNA2_SCRATCH_RETIRED.append(buf)
-        buf = torch.zeros(nbytes, dtype=torch.uint8, device=device)
-        _LNA2_SCRATCH[int(idx)] = buf
-    return buf
+    return ops.SCRATCH.get(device, "moe", nbytes)
 
 
 def lna2_scratch_bytes_resident() -> int:
-    return sum(int(b.numel()) for b in _LNA2_SCRATCH.values()) + \
-        sum(int(b.numel()) for b in _LNA2_SCRATCH_RETIRED)
+    """Bytes of every shared scratch buffer the library holds (decode, prefill
+    and dense, on every device, with the ones a captured graph keeps alive)."""
+    return ops.SCRATCH.resident_bytes()
 
 
 def lna2_scratch_error(device: torch.device, clear: bool = True) -> int:
     """Error word of this device's routed-MoE scratch (ops.ERR_* bits, 0 = none)."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    buf = _LNA2_SCRATCH.get(int(idx))
+    buf = ops.SCRATCH.current(device, "moe")
     return 0 if buf is None else ops.moe_error(buf, clear)
 
 
@@ -895,8 +890,9 @@ def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
     kw = dict(intermediate=inter, expert_bits=layer._exl3_bits_table, bits_mask=layer._exl3_bits_mask,
               codebook=layer._exl3_codebook, swiglu_limit=float(limit), expert_map=expert_map)
     if rows <= lna2_max_rows():
-        ops.moe_decode(x_in, out, ptrs, route_ids, route_w, scratch=_lna2_scratch_for(layer, x2d.device), **kw)
-        _MOE_CALLS["lna2"] += 1
+        def run(dst):
+            ops.moe_decode(x_in, dst, ptrs, route_ids, route_w, scratch=_lna2_scratch_for(layer, x2d.device), **kw)
+        kind = "lna2"
     else:
         # many rows: the grouped-GEMM prefill path (the reference falls back to
         # exllamav3's fused exl3_moe here, vllm_exl3_exl3.py.lna:1597-1704).
@@ -909,11 +905,71 @@ def _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit):
             if not _FAT_CHUNK_LOGGED:
                 logger.info("EXL3 prefill token slicing ACTIVE (tokens=%d, slice=%d)", rows, chunk)
                 _FAT_CHUNK_LOGGED = True
-        for s0 in range(0, rows, chunk):
-            s1 = min(rows, s0 + chunk)
-            ops.moe_prefill(x_in[s0:s1], out[s0:s1], ptrs, route_ids[s0:s1], route_w[s0:s1], **kw)
-        _MOE_CALLS["prefill"] += 1
+
+        def run(dst):
+            for s0 in range(0, rows, chunk):
+                s1 = min(rows, s0 + chunk)
+                ops.moe_prefill(x_in[s0:s1], dst[s0:s1], ptrs, route_ids[s0:s1], route_w[s0:s1], **kw)
+        kind = "prefill"
+    run(out)
+    _MOE_CALLS[kind] += 1
+    _native_selfcheck(layer, kind, run, out, x_in, ids, weights, inners, expert_map, limit)
     return out
+
+
+# ---------------------------------------------------------------- live self-check
+#
+# LNA_EXL3_NATIVE_SELFCHECK=N (the reference's switch,
+# recipe-lna/vllm_exl3_exl3.py.lna:1508-1539): the first N eager calls of the
+# routed kernels on each layer are checked on the live weights against the
+# LinearEXL3 loop, for a bitwise repeat (the same call again into a second
+# buffer) and for finite values.  Eager only: the loop allocates and the
+# check synchronises, neither of which a graph capture allows.  A failure is
+# logged; with LNA_EXL3_NATIVE_STRICT=1 it raises Exl3SelfCheckError, which
+# apply_exl3_experts passes to the caller instead of falling back.
+
+SELFCHECK_REL_L2 = 2e-3          # the reference's bar against the loop (:1532)
+
+
+class Exl3SelfCheckError(RuntimeError):
+    """The routed kernel disagreed with the loop, was not bitwise repeatable
+    or produced non-finite values, under LNA_EXL3_NATIVE_STRICT=1."""
+
+
+def native_selfcheck_calls() -> int:
+    try:
+        return max(0, int(os.environ.get("LNA_EXL3_NATIVE_SELFCHECK", "0") or 0))
+    except ValueError:
+        return 0
+
+
+def _native_selfcheck(layer, kind, run, out, x_in, ids, weights, inners, expert_map, limit) -> None:
+    n_chk = native_selfcheck_calls()
+    if n_chk <= 0 or torch.cuda.is_current_stream_capturing():
+        return
+    done = int(getattr(layer, "_exl3_lna_selfcheck_done", 0))
+    if done >= n_chk:
+        return
+    layer._exl3_lna_selfcheck_done = done + 1
+    ref = apply_exl3_python_loop(x_in, ids, weights, inners, expert_map, limit)
+    repeat = torch.empty_like(out)
+    run(repeat)
+    torch.cuda.synchronize(out.device)
+    got = out.float()
+    rel = float(((got - ref).norm() / (ref.norm() + 1e-6)).item())
+    bitwise = bool(torch.equal(out, repeat))
+    finite = bool(torch.isfinite(got).all().item())
+    record = {"call": done + 1, "kernel": kind, "rows": int(x_in.shape[0]), "rel_l2": rel, "bitwise": bitwise,
+              "finite": finite, "ok": rel <= SELFCHECK_REL_L2 and bitwise and finite}
+    layer._exl3_lna_selfcheck = [*getattr(layer, "_exl3_lna_selfcheck", []), record]
+    logger.info("EXL3 native selfcheck %s call=%d kernel=%s m=%d rel=%.3g bitwise=%s finite=%s",
+                getattr(layer, "prefix", "?"), done + 1, kind, record["rows"], rel, bitwise, finite)
+    if not record["ok"]:
+        msg = (f"EXL3 native selfcheck failed on {getattr(layer, 'prefix', '?')} call {done + 1} ({kind}, "
+               f"m={record['rows']}): rel={rel:.3g} (bar {SELFCHECK_REL_L2}) bitwise={bitwise} finite={finite}")
+        if os.environ.get("LNA_EXL3_NATIVE_STRICT", "0") == "1":
+            raise Exl3SelfCheckError(msg)
+        logger.warning(msg)
 
 
 def apply_exl3_experts(x, topk_ids, topk_weights, layer, *, limit: float = SWIGLU_LIMIT_DEFAULT,
@@ -939,7 +995,7 @@ def apply_exl3_experts(x, topk_ids, topk_weights, layer, *, limit: float = SWIGL
         try:
             res = _apply_lna2_moe(x2d, ids, weights, layer, inners, expert_map, limit)
         except Exception as exc:
-            if moe_kernel_strict():
+            if moe_kernel_strict() or isinstance(exc, Exl3SelfCheckError):
                 raise
             res = None
             layer._exl3_lna2_error = repr(exc)
@@ -1386,14 +1442,19 @@ class Exl3LinearMethod:
 
     @staticmethod
     def _prewarm(layer) -> None:
+        """Reserve the shared scratch of every call this module can make before
+        any graph capture: each shard's GEMV for every row count it takes (up
+        to AUTO_RECONSTRUCT_THRESHOLD rows, whatever LNA_EXL3_PREWARM_ROWS
+        says: a capture at a row count without an earlier eager call would
+        otherwise need a larger buffer), and the fused group at its row counts
+        (up to DENSE_GROUP_MAX_ROWS)."""
         lins = [lin for lin in layer._exl3_linears if lin is not None]
         if not lins or lins[0].trellis.device.type != "cuda":
             return
         dev = lins[0].trellis.device
         try:
-            for rows in sorted(set(_dense_prewarm_rows()) | {DENSE_GROUP_MAX_ROWS}):
-                for lin in lins:
-                    ops.prepare_gemm(dev, rows, int(lin.in_features), int(lin.out_features))
+            for lin in lins:
+                ops.prepare_gemm(dev, AUTO_RECONSTRUCT_THRESHOLD, int(lin.in_features), int(lin.out_features))
             prewarm_exl3_dense_group(layer)
         except Exception as exc:
             logger.warning("EXL3 prewarm skipped for %s: %s", getattr(layer, "prefix", "?"), exc)

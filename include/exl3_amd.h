@@ -220,6 +220,19 @@ int exl3_moe_decode_noalloc(const void* x, int x_kind, void* out, int out_kind, 
                             float swiglu_limit, void* stream);
 
 /*
+ * The error word of this device's fixed scratch (the ERR bits of
+ * exl3_moe_decode_noalloc's calls: 1 = an expert of a width outside bits_mask
+ * was routed and contributed zero, 2 = a bounded wait gave up), read after
+ * the work queued on `stream`.  No counterpart in the reference; it serves
+ * the same callers as exl3_moe_decode_noalloc, which cannot see the fixed
+ * array's address.  clear: 0 reads only; 1 also clears the bits; 2 also
+ * resets every control word to zero, as at the first call (recovery after a
+ * call that did not complete).  Synchronises `stream`, so it is refused inside
+ * a graph capture; allocates nothing.  Returns the word (>= 0) or < 0.
+ */
+int exl3_moe_noalloc_error(int clear, void* stream);
+
+/*
  * Routed-MoE layer for many tokens (prefill), same mathematics as
  * exl3_moe_decode: tokens are routed by expert on the device and each expert's
  * weights are decoded once per 32 routed rows, feeding fp16 MFMA with fp32

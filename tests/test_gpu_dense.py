@@ -85,13 +85,23 @@ def test_gemm_small(ops, dev, bits, rows):
     assert_close(got, ref, what=f"K{bits} rows={rows}")
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4, 6])
 @pytest.mark.parametrize("k,n", [(4096, 4096), (4096, 1536), (1536, 4096), (4096, 12288)])
-def test_gemm_baseline_shapes(ops, dev, k, n):
+def test_gemm_baseline_shapes(ops, dev, k, n, bits):
+    """The dense sweep at its full sizes, every combination: each shape and
+    width at 1, 2, 4, 8 and 16 rows against the oracle (the weight is
+    reconstructed once per shape and width)."""
     import torch
 
-    for bits, rows in ((6, 1), (2, 16), (3, 4), (4, 8)):
-        got, ref = _gemm_case(ops, dev, k, n, bits, rows, torch.float32, seed=k + n)
-        assert_close(got, ref, what=f"{k}x{n} K{bits} rows={rows}")
+    L = synth.dense(k, n, bits, seed=k + n + bits)
+    tr, su, sv = to_dev(L["trellis"], dev), to_dev(L["suh"], dev), to_dev(L["svh"], dev)
+    w = O.reconstruct_fast(L["trellis"], bits, O.CB_MCG)
+    for rows in (1, 2, 4, 8, 16):
+        print(f"gemm {k}x{n} K{bits} rows={rows}", flush=True)
+        x = synth.activations(rows, k, seed=k + n + rows)
+        y = ops.gemm(to_dev(x, dev), tr, su, sv, O.CB_MCG, torch.float32)
+        ref = O.linear(x, L["trellis"], L["suh"], L["svh"], bits, O.CB_MCG, w=w)
+        assert_close(y.cpu().numpy(), ref, what=f"{k}x{n} K{bits} rows={rows}")
 
 
 def test_gemm_c0_config(ops, dev):

@@ -266,7 +266,10 @@ def test_linear_method_prewarms_groups_and_captures(dev):
     """LNA_EXL3_DENSE_GROUP=1: after process_weights_after_loading the
     module's shards run as one fused call, the scratch is reserved for every
     decode row count (no prepare_gemm by hand), and a graph captured at each
-    row count 1..16 replays to the oracle's result."""
+    row count 1..16 replays to the oracle's result; so do graphs at 24 and 32
+    rows, where the group declines and each shard takes the GEMV (which runs
+    up to AUTO_RECONSTRUCT_THRESHOLD rows), with no scratch grown by the
+    capture."""
     import torch
     from dsv4_carve_amd import ops, vllm_exl3 as V
 
@@ -276,7 +279,7 @@ def test_linear_method_prewarms_groups_and_captures(dev):
                                           [512, 512], 4, seed=1200)
         assert V.dense_group_stats()["prewarm_groups"] == 1
         before = ops.SCRATCH.resident_bytes()
-        for rows in range(1, 17):
+        for rows in [*range(1, 17), 24, V.AUTO_RECONSTRUCT_THRESHOLD]:
             x16 = synth.activations(rows, 1024, seed=1300 + rows)
             x = to_dev(x16.astype(np.float32), dev)          # fp32 in and out: no output cast on the bar
             static_out = None

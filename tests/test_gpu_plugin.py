@@ -246,6 +246,47 @@ def test_apply_experts_declines_bad_geometry(dev, experts, monkeypatch):
         V.apply_exl3_experts(xf, to_dev(ids.astype(np.int64), dev), to_dev(w, dev), experts.layer)
 
 
+def test_native_selfcheck(dev, experts, monkeypatch):
+    """LNA_EXL3_NATIVE_SELFCHECK=2: the first two eager calls (decode, then
+    prefill) are checked on the live weights against the loop, for a bitwise
+    repeat and finite values; the third is not.  A loop that disagrees fails
+    the check: raised under LNA_EXL3_NATIVE_STRICT=1 (not swallowed into a
+    fallback), logged otherwise with the kernel's output returned."""
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", "lna2")
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "0")
+    monkeypatch.setenv("LNA_EXL3_NATIVE_SELFCHECK", "2")
+    monkeypatch.setenv("LNA_EXL3_NATIVE_STRICT", "1")
+    layer = experts.layer
+    layer._exl3_lna_selfcheck_done, layer._exl3_lna_selfcheck = 0, []
+    try:
+        for m in (5, 40, 7):
+            print(f"selfcheck m={m}", flush=True)
+            ids, w = synth.routing(m, 12, 6, seed=300 + m)
+            x = synth.activations(m, 512, seed=301 + m)
+            y = V.apply_exl3_experts(to_dev(x, dev), to_dev(ids.astype(np.int64), dev), to_dev(w, dev), layer)
+            assert_close(y.float().cpu().numpy(), experts.ref(x, ids, w), max_abs=2e-2 + 8e-3)
+        recs = layer._exl3_lna_selfcheck
+        assert [r["kernel"] for r in recs] == ["lna2", "prefill"] and [r["rows"] for r in recs] == [5, 40]
+        assert all(r["ok"] and r["bitwise"] and r["finite"] and r["rel_l2"] < 1e-3 for r in recs), recs
+
+        loop = V.apply_exl3_python_loop
+        monkeypatch.setattr(V, "apply_exl3_python_loop", lambda *a, **k: loop(*a, **k) * 1.01)
+        ids, w = synth.routing(4, 12, 6, seed=310)
+        args = (to_dev(synth.activations(4, 512, seed=311), dev), to_dev(ids.astype(np.int64), dev),
+                to_dev(w, dev), layer)
+        layer._exl3_lna_selfcheck_done = 0
+        with pytest.raises(V.Exl3SelfCheckError, match="rel="):
+            V.apply_exl3_experts(*args)
+        monkeypatch.setenv("LNA_EXL3_NATIVE_STRICT", "0")
+        layer._exl3_lna_selfcheck_done = 0
+        V.apply_exl3_experts(*args)
+        assert layer._exl3_last_apply == "lna2" and not layer._exl3_lna_selfcheck[-1]["ok"]
+    finally:
+        del layer._exl3_lna_selfcheck_done, layer._exl3_lna_selfcheck
+
+
 def test_stale_pointer_tables_decline(dev, monkeypatch):
     from dsv4_carve_amd import vllm_exl3 as V
 

@@ -490,3 +490,26 @@ def test_wo_a_loader_keeps_this_ranks_slice():
     meth.process_weights_after_loading(layer)
     (lin,) = layer._exl3_linears
     assert lin.in_features == 256 and lin.out_features == 128 and int(lin.trellis.float().mean()) == 3
+
+
+def test_scratch_pool_frees_replaced_buffers_unless_captured(monkeypatch):
+    """A buffer that a larger one replaces is freed, except one that was
+    current during a graph capture (a captured graph keeps its address)."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    pool = ops._ScratchPool()
+    cpu = torch.device("cpu", 0)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    a = pool.get(cpu, "moe", 1000)
+    assert pool.get(cpu, "moe", 500) is a                  # large enough: reused
+    b = pool.get(cpu, "moe", 4000)
+    assert b is not a and pool.resident_bytes() == 4000     # `a` is no longer held by the pool
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: True)
+    assert pool.get(cpu, "moe", 100) is b                  # a capture used `b`
+    with pytest.raises(RuntimeError, match="not prewarmed"):
+        pool.get(cpu, "moe", 8000)
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: False)
+    c = pool.get(cpu, "moe", 8000)
+    assert pool.resident_bytes() == 8000 + 4000             # `b` retired, kept alive
+    assert pool.get(cpu, "moe", 16000) is not c and pool.resident_bytes() == 16000 + 4000

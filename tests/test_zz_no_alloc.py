@@ -66,3 +66,40 @@ def test_noalloc_rejects_oversized_layer(dev):
                                    *([tab.data_ptr()] * 9), ids.data_ptr(), 0, w.data_ptr(), 2, None, 0,
                                    None, 2, 0, ops.CB_MCG, 10.0, int(torch.cuda.current_stream().cuda_stream))
     assert rc < 0 and b"128 MiB" in L.exl3_last_error()
+
+
+def test_noalloc_error_word(dev):
+    """The fixed scratch's error word through exl3_moe_noalloc_error: a call
+    whose bits_mask lacks a routed expert's width reports ERR_WIDTH (those
+    experts contribute zero, every launch completes); clearing resets it; a
+    full reset of the control words leaves the next call correct."""
+    import torch
+    from dsv4_carve_amd import _lib, ops
+
+    L = _lib.load()
+    stream = int(torch.cuda.current_stream().cuda_stream)
+    bits = [3, 2, 5, 3, 2, 5, 3, 2]                  # experts 2 and 5 are 5-bit
+    layer = Layer(dev, 8, 512, 256, bits, seed=41)
+    m, topk = 6, 4
+    ids, w = synth.routing(m, 8, topk, seed=42)
+    x16 = synth.activations(m, 512, seed=43)
+    keep = np.where(np.isin(ids, [2, 5]), 0.0, w).astype(np.float32)
+    assert (keep != w).any(), "the route must reach a 5-bit expert"
+    x, idd, wd = to_dev(x16, dev), to_dev(ids, dev), to_dev(w, dev)
+    out = torch.empty((m, 512), dtype=torch.float32, device=dev)
+    _lib.check(L.exl3_moe_noalloc_error(2, stream))             # start from zeroed control words
+    lacking = (1 << 2) | (1 << 3)                                # the launch covers 2 and 3 bits only
+    layer_mask, layer.mask = layer.mask, lacking
+    print("noalloc error word: unlisted 5-bit experts", flush=True)
+    _call(L.exl3_moe_decode_noalloc, layer, x, idd, wd, out, [])
+    layer.mask = layer_mask
+    assert _lib.check(L.exl3_moe_noalloc_error(0, stream)) == ops.ERR_WIDTH
+    assert_close(out.cpu().numpy(), layer.ref(x16, ids, keep), what="noalloc: unlisted width dropped")
+    assert _lib.check(L.exl3_moe_noalloc_error(1, stream)) == ops.ERR_WIDTH   # read, then clear
+    assert _lib.check(L.exl3_moe_noalloc_error(0, stream)) == 0
+    print("noalloc error word: full mask after a reset", flush=True)
+    _lib.check(L.exl3_moe_noalloc_error(2, stream))
+    _call(L.exl3_moe_decode_noalloc, layer, x, idd, wd, out, [])
+    assert _lib.check(L.exl3_moe_noalloc_error(0, stream)) == 0
+    assert_close(out.cpu().numpy(), layer.ref(x16, ids, w), what="noalloc: full mask after the reset")
+    assert L.exl3_moe_noalloc_error(3, stream) < 0
