@@ -48,9 +48,20 @@ UNITS += [("exl3_prefill_inst.hip", [f"-DEXL3_BITS={b}"], f"exl3_pf_b{b}.o") for
 UNITS += [("exl3_prefill_inst.hip", ["-DEXL3_BITS=3", "-DEXL3_BITS2=2"], "exl3_pf_b32.o")]
 
 
-def _compile(unit):
+def _stale(src: str, out: str) -> bool:
+    """True unless `out` is newer than the unit's source and every header."""
+    if not os.path.isfile(out):
+        return True
+    t = os.path.getmtime(out)
+    deps = [os.path.join(CSRC, src)] + [os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hpp")]
+    return any(os.path.getmtime(d) > t for d in deps)
+
+
+def _compile(unit, incremental=False):
     src, defs, obj = unit
     out = obj if os.path.isabs(obj) else os.path.join(OUT_DIR, obj)
+    if incremental and not _stale(src, out):
+        return out
     cmd = [HIPCC, *COMMON, *defs, "-c", os.path.join(CSRC, src), "-o", out]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "packed-fp32-ops"
@@ -69,14 +80,14 @@ def _link(objs, lib):
     os.replace(tmp, lib)
 
 
-def build(jobs: int | None = None, verbose: bool = True, null: bool = True) -> str:
+def build(jobs: int | None = None, verbose: bool = True, null: bool = True, incremental: bool = False) -> str:
     os.makedirs(OUT_DIR, exist_ok=True)
     os.makedirs(NULL_DIR, exist_ok=True)
     units = [u for u in UNITS if os.path.isfile(os.path.join(CSRC, u[0]))]
     null_units = [(src, [*defs, "-DEXL3_NULL_DECODE=1"], os.path.join(NULL_DIR, obj)) for src, defs, obj in units]
     jobs = jobs or min(8, os.cpu_count() or 1)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, units + (null_units if null else [])))
+        objs = list(ex.map(lambda u: _compile(u, incremental), units + (null_units if null else [])))
     _link(objs[:len(units)], LIB)
     if null:
         _link(objs[len(units):], NULL_LIB)
@@ -96,5 +107,7 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--no-null", action="store_true", help="skip the timing-only null-decode library")
+    ap.add_argument("--incremental", action="store_true",
+                    help="recompile only units older than their sources (development; build() always compiles all)")
     a = ap.parse_args()
-    build(a.jobs, null=not a.no_null)
+    build(a.jobs, null=not a.no_null, incremental=a.incremental)
