@@ -657,6 +657,58 @@ def time_decode_ceiling(dev, iters: int = 512, reps: int = 5) -> dict:
             "split_simd_cycles_per_64_weights": split}
 
 
+ISA_OPS = ("v_and_b32", "v_xor_b32", "v_lshrrev_b32", "v_bitop3_b32", "v_mul_lo_u16", "v_add_u32",
+           "v_bfe_u32", "v_alignbit_b32", "v_perm_b32", "v_mul_lo_u32", "v_lshlrev_b32", "v_add3_u32")
+
+
+def time_isa_rates(dev, iters: int = 2048) -> dict:
+    """Issue rates of the decode's VALU instruction kinds (csrc/exl3_probe.hip
+    probe_isa_kernel): each kind alone in a loop of eight independent chains,
+    four-wave workgroups (a wave per SIMD of a CU) at 1, 2 and 4 waves per
+    SIMD.  Returns SIMD cycles per wave64 instruction two ways: from the
+    launch's event time at the loop's shader clock (median of three after one
+    warm-up), and from each wave's own loop cycles divided by the waves
+    sharing its SIMD."""
+    import ctypes
+
+    import torch
+    from dsv4_carve_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_LIB)
+    lib.exl3_probe_isa.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                   ctypes.c_void_p]
+    lib.exl3_probe_isa.restype = ctypes.c_int
+    assert int(lib.exl3_probe_isa_ops()) == len(ISA_OPS)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    simds = 4 * cus
+    sink = torch.empty(4 * simds * 64, dtype=torch.int32, device=dev)
+    clk = torch.zeros(2 * 4 * simds, dtype=torch.int64, device=dev)
+    stream = int(torch.cuda.current_stream(dev).cuda_stream)
+    out = {}
+    for op, name in enumerate(ISA_OPS):
+        per = {}
+        for waves in (1, 2, 4):
+            blocks = waves * cus
+            nw = 4 * blocks
+            ev, own = [], []
+            for _ in range(4):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                assert lib.exl3_probe_isa(op, blocks, iters, sink.data_ptr(), clk.data_ptr(), stream) == 0
+                b.record()
+                torch.cuda.synchronize()
+                t = a.elapsed_time(b) * 1e-3
+                c = clk[:2 * nw].view(nw, 2).double()
+                ghz = c[:, 0].sum().item() / c[:, 1].sum().item() * 0.1      # reference ticks at 100 MHz
+                ev.append(t * ghz * 1e9 * simds / (nw * iters * 64.0))
+                own.append(c[:, 0].mean().item() / (waves * iters * 64.0))
+            per[f"{waves}_waves_per_simd"] = {"event": round(sorted(ev[1:])[1], 2),
+                                              "per_wave_loop": round(sorted(own[1:])[1], 2)}
+        out[name] = per
+    del sink, clk
+    return {"unit": "SIMD cycles per wave64 instruction", "chains_per_lane": 8, "iters": iters, **out}
+
+
 def decode_floor_us(rate: dict, rows: int, bits: list[int], hidden: int, inter: int, topk: int, seed: int) -> float:
     """Lower bound on one routed layer's time from the decode rate alone: the
     mean, over the headline's routing pool, of each distinct expert's
@@ -767,6 +819,8 @@ def main() -> int:
                                               "measured": round(us, 1)}
         extra["decode_ceiling"] = dc
         print(f"[bench] decode ceiling: {dc}", file=sys.stderr, flush=True)
+        extra["isa_issue_rates"] = time_isa_rates(dev)
+        print(f"[bench] instruction issue rates: {extra['isa_issue_rates']}", file=sys.stderr, flush=True)
     if "null" in legs:
         # The same workloads on the timing-only twin library (each decoded
         # weight replaced by a loaded tile word): the skeleton of loads, MFMAs,

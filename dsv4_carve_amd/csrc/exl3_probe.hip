@@ -22,6 +22,11 @@
 // instruction), and the MFMAs alone (the B operands are the tile words
 // themselves, register moves at most).  The launch's block count sets the
 // waves per SIMD.
+//
+// 3. Instruction issue rates.  One VALU instruction of the decode's kinds in a
+// loop: eight independent chains per lane, 64 instructions per iteration, in
+// four-wave workgroups (one wave per SIMD of a CU), so a launch of n * CUs
+// workgroups puts n waves on each SIMD.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -138,6 +143,60 @@ static int launch_probe_decode(int mode, int blocks, int iters, const uint32_t* 
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// The instruction kinds of the issue-rate probe (exl3_probe_isa's `op`).
+enum ProbeIsaOp : int {
+    ISA_AND = 0, ISA_XOR, ISA_LSHRREV, ISA_BITOP3, ISA_MUL_LO_U16, ISA_ADD_U32,
+    ISA_BFE, ISA_ALIGNBIT, ISA_PERM, ISA_MUL_LO_U32, ISA_LSHLREV, ISA_ADD3,
+    ISA_OPS
+};
+
+template <int OP>
+__device__ __forceinline__ void isa_op(uint32_t& x, uint32_t k) {
+    if constexpr (OP == ISA_AND) asm volatile("v_and_b32 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_XOR) asm volatile("v_xor_b32 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_LSHRREV) asm volatile("v_lshrrev_b32 %0, 3, %0" : "+v"(x));
+    else if constexpr (OP == ISA_BITOP3) asm volatile("v_bitop3_b32 %0, %0, %1, %0 bitop3:0x6c" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MUL_LO_U16) asm volatile("v_mul_lo_u16 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_ADD_U32) asm volatile("v_add_u32 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_BFE) asm volatile("v_bfe_u32 %0, %0, 3, 16" : "+v"(x));
+    else if constexpr (OP == ISA_ALIGNBIT) asm volatile("v_alignbit_b32 %0, %0, %1, 16" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_PERM) asm volatile("v_perm_b32 %0, %0, %1, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MUL_LO_U32) asm volatile("v_mul_lo_u32 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_LSHLREV) asm volatile("v_lshlrev_b32 %0, 3, %0" : "+v"(x));
+    else asm volatile("v_add3_u32 %0, %0, %1, %1" : "+v"(x) : "v"(k));
+}
+
+template <int OP>
+__global__ __launch_bounds__(256) void probe_isa_kernel(int iters, uint32_t* __restrict__ sink,
+                                                        uint64_t* __restrict__ clk) {
+    const int lane = threadIdx.x & 63, wave = (int)(blockIdx.x * 4 + threadIdx.x / 64);
+    uint32_t x[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = (uint32_t)lane * 2654435761u + (uint32_t)i;
+    const uint32_t k = 0x8fff8fffu ^ (uint32_t)wave;
+    const uint64_t c0 = __builtin_amdgcn_s_memtime(), t0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int r = 0; r < 8; ++r)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) isa_op<OP>(x[i], k);
+    }
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), t1 = __builtin_amdgcn_s_memrealtime();
+    uint32_t v = 0u;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v ^= x[i];
+    sink[wave * 64 + lane] = v;
+    if (lane == 0) {
+        clk[2 * wave] = c1 - c0;
+        clk[2 * wave + 1] = t1 - t0;
+    }
+}
+
+template <int OP>
+static void launch_isa(int blocks, int iters, uint32_t* sink, uint64_t* clk, hipStream_t st) {
+    hipLaunchKernelGGL((probe_isa_kernel<OP>), dim3(blocks), dim3(256), 0, st, iters, sink, clk);
+}
+
 extern "C" {
 
 // Launches the probe over bytes (a multiple of 16) at buf; sink holds one
@@ -171,6 +230,35 @@ int exl3_probe_decode_mode(int bits, int mode, int blocks, int iters, const uint
         default: return -1;
     }
 }
+
+// Instruction issue-rate probe: `blocks` four-wave workgroups, each wave
+// running `iters` iterations of 64 instructions of kind `op` (0 v_and_b32, 1
+// v_xor_b32, 2 v_lshrrev_b32, 3 v_bitop3_b32, 4 v_mul_lo_u16, 5 v_add_u32, 6
+// v_bfe_u32, 7 v_alignbit_b32, 8 v_perm_b32, 9 v_mul_lo_u32, 10 v_lshlrev_b32,
+// 11 v_add3_u32).  sink: blocks * 256 uint32; clk: 2 * 4 * blocks uint64, per
+// wave as exl3_probe_decode_mode's per workgroup.  Returns 0, or -1 on a bad
+// argument or launch error.
+int exl3_probe_isa(int op, int blocks, int iters, uint32_t* sink, uint64_t* clk, void* stream) {
+    if (!sink || !clk || blocks < 1 || iters < 1 || op < 0 || op >= ISA_OPS) return -1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    switch (op) {
+        case ISA_AND: launch_isa<ISA_AND>(blocks, iters, sink, clk, st); break;
+        case ISA_XOR: launch_isa<ISA_XOR>(blocks, iters, sink, clk, st); break;
+        case ISA_LSHRREV: launch_isa<ISA_LSHRREV>(blocks, iters, sink, clk, st); break;
+        case ISA_BITOP3: launch_isa<ISA_BITOP3>(blocks, iters, sink, clk, st); break;
+        case ISA_MUL_LO_U16: launch_isa<ISA_MUL_LO_U16>(blocks, iters, sink, clk, st); break;
+        case ISA_ADD_U32: launch_isa<ISA_ADD_U32>(blocks, iters, sink, clk, st); break;
+        case ISA_BFE: launch_isa<ISA_BFE>(blocks, iters, sink, clk, st); break;
+        case ISA_ALIGNBIT: launch_isa<ISA_ALIGNBIT>(blocks, iters, sink, clk, st); break;
+        case ISA_PERM: launch_isa<ISA_PERM>(blocks, iters, sink, clk, st); break;
+        case ISA_MUL_LO_U32: launch_isa<ISA_MUL_LO_U32>(blocks, iters, sink, clk, st); break;
+        case ISA_LSHLREV: launch_isa<ISA_LSHLREV>(blocks, iters, sink, clk, st); break;
+        default: launch_isa<ISA_ADD3>(blocks, iters, sink, clk, st); break;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+int exl3_probe_isa_ops(void) { return ISA_OPS; }
 
 // The decode kernels' loop (mode 0) at `bits`.
 int exl3_probe_decode(int bits, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
