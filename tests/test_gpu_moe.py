@@ -282,8 +282,11 @@ def test_dtypes(small, dev, out_dtype, x_dtype):
     got = small.run(xt, ids, w, out_dtype=getattr(torch, out_dtype)).float().cpu().numpy()
     x16 = xt.float().cpu().numpy().astype(np.float16)        # the kernel's bf16 -> fp16 rounding
     ref = small.ref(x16, ids, w)
-    tol = 6e-3 if "bfloat16" in (out_dtype,) else 2e-3
-    assert rel_l2(got, ref) <= tol
+    # a 16-bit output adds its own rounding (half an ulp: 2^-11 fp16, 2^-9 bf16
+    # relative), the slack of the prefill dtype test on the same layer
+    slack = 4e-3 if out_dtype == "bfloat16" else 1e-3
+    assert_close(got, ref, max_abs=2e-2 + 8 * slack, rel=2e-3 if out_dtype == "float16" else 6e-3,
+                 what=f"{x_dtype}->{out_dtype}")
 
 
 def test_bitwise_repeat_and_scratch_reuse(small):
@@ -301,7 +304,7 @@ def test_bitwise_repeat_and_scratch_reuse(small):
             outs[m] = o
     ids, w = synth.routing(16, 16, 6, seed=516)
     ref = small.ref(inputs(16, "real"), ids, w)
-    assert rel_l2(outs[16].cpu().numpy(), ref) < 1e-3
+    assert_close(outs[16].cpu().numpy(), ref, what="m=16 after the alternating calls")
 
 
 def test_transposed_ids_changes_output(small):
