@@ -7,8 +7,8 @@
   a ninth slot of weight 1, at 16 rows; and two such blocks chained, the first
   block's output (RMS-normalised, fp16) feeding the second.
 * The prefill path on the 256-expert layer at 512 tokens with Zipf(1.1)
-  routing: a fixed sample of 32 tokens, half of them routed to the hottest
-  expert (whose rows span many 32-row tiles), checked against the oracle.
+  routing, every token checked against the oracle (the hottest expert's rows
+  span many 32-row tiles).
 
 Bars: max-abs 2e-2 and rel-L2 1e-3 on the raw outputs (no rescaling), and the
 kernels' error word must stay zero."""
@@ -131,7 +131,7 @@ def test_chained_blocks_16_rows(blocks, dev):
 def test_prefill_512_tokens_zipf(c2, dev):
     from tests.test_gpu_prefill import run_prefill
 
-    print("prefill 512 tokens Zipf(1.1) vs oracle (32-token sample)", flush=True)
+    print("prefill 512 tokens Zipf(1.1) vs oracle (every token)", flush=True)
     T = 512
     ids, w = synth.zipf_routing(T, E, 8, seed=4512)
     x = synth.activations(T, H, seed=4512)
@@ -140,12 +140,8 @@ def test_prefill_512_tokens_zipf(c2, dev):
     hot = int(np.argmax(counts))
     hot_rows = np.flatnonzero((ids == hot).any(axis=1))
     assert len(hot_rows) > 64, "the hottest expert should span several 32-row tiles"
-    rng = np.random.default_rng(4513)
-    pick = np.unique(np.concatenate([
-        hot_rows[np.linspace(0, len(hot_rows) - 1, 16).astype(int)],
-        rng.choice(np.setdiff1d(np.arange(T), hot_rows), 16, replace=False)]))
-    ref = c2.ref(x[pick], ids[pick], w[pick])
-    mae, rel = assert_close(got[pick], ref, what="prefill 512 tokens")
-    print(f"prefill 512: hot expert {hot} on {len(hot_rows)} tokens; sample max-abs {mae:.3e} rel-L2 {rel:.3e}",
-          flush=True)
+    ref = c2.ref(x, ids, w)
+    mae, rel = assert_close(got, ref, what="prefill 512 tokens")
+    print(f"prefill 512: hot expert {hot} on {len(hot_rows)} tokens, {int((counts > 0).sum())} experts; "
+          f"max-abs {mae:.3e} rel-L2 {rel:.3e}", flush=True)
     _no_errors(dev)
