@@ -4,8 +4,8 @@ from __future__ import annotations
 
 import numpy as np
 
-# BASELINE fp tolerance for layer outputs vs an fp32 (here float64) matmul on the
-# oracle-dequantized weights: max-abs-err 2e-2 and rel-L2 1e-3.
+# The floating-point bar for layer outputs against an fp32 (here float64)
+# matmul on the oracle-dequantized weights: max-abs-err 2e-2 and rel-L2 1e-3.
 MAX_ABS = 2e-2
 REL_L2 = 1e-3
 
