@@ -349,7 +349,7 @@ def c2(dev):
     return Layer(dev, 256, 4096, 2048, synth.mixed_bits(256), seed=2)
 
 
-@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 8])
 def test_c2_against_oracle(c2, m):
     print(f"c2 m={m}", flush=True)
     ids, w = synth.routing(m, 256, 8, seed=1000 + m)
