@@ -462,6 +462,24 @@ def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True, lib=N
     return us, flops, nbytes, distinct
 
 
+def prefill_decoded_weights(layer, tokens: int, topk: int, seed: int, tile_rows: int = 32) -> tuple[float, float]:
+    """Weights the prefill GEMMs decode per layer on time_prefill's routing
+    pool (each expert's gate, up and down once per tile of up to `tile_rows`
+    routed rows), and the minimum (each active expert once), means over the
+    pool."""
+    from dsv4_carve_amd import synth
+
+    n_exp = len(layer.bits)
+    per = 3.0 * layer.hidden * layer.inter
+    dec, low = [], []
+    for i in range(4):
+        ids = synth.zipf_routing(tokens, n_exp, topk, seed=seed + i)[0].reshape(-1)
+        cnt = np.bincount(ids[(ids >= 0) & (ids < n_exp)], minlength=n_exp)
+        dec.append(float(np.ceil(cnt / tile_rows).sum()) * per)
+        low.append(float((cnt > 0).sum()) * per)
+    return float(np.mean(dec)), float(np.mean(low))
+
+
 C3_LAYERS = 43
 
 
@@ -891,6 +909,9 @@ def main() -> int:
             "tflops": round(fl / (usp * 1e-6) / 1e12, 2), "mfma_frac_fp16": round(fl / (usp * 1e-6) / MFMA_PEAK_F16, 4),
             "GBps": round(bp / (usp * 1e-6) / 1e9, 1), "hbm_frac": round(bp / (usp * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
             "distinct_experts": dist, "algorithmic_gflop": round(fl / 1e9, 1), "bytes": int(bp)}
+        dw, dmin = prefill_decoded_weights(layer, 512, TOPK, seed=4242)
+        extra["prefill_512_tokens_zipf1.1"]["decoded_gweights"] = round(dw / 1e9, 2)
+        extra["prefill_512_tokens_zipf1.1"]["decoded_gweights_min"] = round(dmin / 1e9, 2)
         print(f"[bench] prefill 512 tokens: {extra['prefill_512_tokens_zipf1.1']}", file=sys.stderr, flush=True)
     if "stack" in legs:
         us3, b3 = time_stack(dev, 16, 4, 1)
