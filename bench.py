@@ -627,7 +627,8 @@ def time_decode_ceiling(dev, iters: int = 512, reps: int = 5) -> dict:
     the shader clock the loop ran at, and the SIMD cycles it spends per 64
     weights (one weight per lane).  `split` takes the loop apart at the same
     residency, shorter runs: the decode alone, the MFMAs alone, and the whole
-    loop at four waves per SIMD."""
+    loop at four waves per SIMD, with its accumulators in AGPRs, and with each
+    weight's addends summed on the VALU so half the MFMAs run."""
     import ctypes
 
     import torch
@@ -669,14 +670,76 @@ def time_decode_ceiling(dev, iters: int = 512, reps: int = 5) -> dict:
         split[f"K{bits}"] = {
             "decode_only": run(bits, 1, 2, iters // 4, 3)["simd_cycles_per_64_weights"],
             "mfma_only": run(bits, 2, 2, iters // 4, 3)["simd_cycles_per_64_weights"],
-            "full_4_waves_per_simd": run(bits, 0, 4, iters // 4, 3)["simd_cycles_per_64_weights"]}
+            "full_4_waves_per_simd": run(bits, 0, 4, iters // 4, 3)["simd_cycles_per_64_weights"],
+            "full_agpr_acc": run(bits, 3, 2, iters // 4, 3)["simd_cycles_per_64_weights"],
+            "full_agpr_acc_4_waves_per_simd": run(bits, 3, 4, iters // 4, 3)["simd_cycles_per_64_weights"],
+            "addends_summed_half_mfmas": run(bits, 4, 2, iters // 4, 3)["simd_cycles_per_64_weights"]}
     del words, sink, clk
     return {"workgroups": 2 * simds, "iters": iters, "codebook": "MCG", **res,
             "split_simd_cycles_per_64_weights": split}
 
 
+ROWS_CFG = ((1, 1), (2, 1), (2, 2), (3, 2), (4, 2), (4, 4), (6, 4), (8, 4))
+
+
+def time_row_blocks(dev, iters: int = 256, reps: int = 3) -> dict:
+    """The grouped GEMM's inner loop with each decoded B operand applied to
+    RB 16-row blocks, each lane decoding 16/D of its tile's columns
+    (csrc/exl3_probe.hip probe_rows_kernel; single-wave workgroups, two per
+    SIMD).  Returns SIMD cycles per decoded weight (per 64 weights, one per
+    lane) and per weight-row (divided by 16 RB) for each (RB, D) at 2 and 3
+    bits."""
+    import ctypes
+
+    import torch
+    from dsv4_carve_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_LIB)
+    lib.exl3_probe_rows.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                    ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.exl3_probe_rows.restype = ctypes.c_int
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    simds = 4 * cus
+    blocks = 2 * simds
+    g = torch.Generator().manual_seed(11)
+    words = torch.randint(0, 2 ** 31 - 1, (64 * 8 * 3,), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
+    sink = torch.empty(blocks * 64, dtype=torch.float32, device=dev)
+    clk = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    stream = int(torch.cuda.current_stream(dev).cuda_stream)
+    out = {}
+    for bits in (2, 3):
+        for cfg, (rb, d) in enumerate(ROWS_CFG):
+            times = []
+            for _ in range(reps + 1):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                assert lib.exl3_probe_rows(bits, cfg, blocks, iters, words.data_ptr(), sink.data_ptr(),
+                                           clk.data_ptr(), stream) == 0
+                b.record()
+                torch.cuda.synchronize()
+                times.append(a.elapsed_time(b) * 1e-3)
+            t = sorted(times[1:])[reps // 2]
+            c = clk[:2 * blocks].view(blocks, 2).double().sum(0).tolist()
+            ghz = c[0] / c[1] * 0.1
+            weights = blocks * iters * 16384.0 / d
+            cyc = t * ghz * 1e9 * simds / (weights / 64.0)
+            out[f"K{bits}_rb{rb}_d{d}"] = {"per_64_weights": round(cyc, 2), "per_64_weight_rows": round(cyc / (16 * rb), 3)}
+    del words, sink, clk
+    return {"unit": "SIMD cycles", "iters": iters, **out}
+
+
 ISA_OPS = ("v_and_b32", "v_xor_b32", "v_lshrrev_b32", "v_bitop3_b32", "v_mul_lo_u16", "v_add_u32",
-           "v_bfe_u32", "v_alignbit_b32", "v_perm_b32", "v_mul_lo_u32", "v_lshlrev_b32", "v_add3_u32")
+           "v_bfe_u32", "v_alignbit_b32", "v_perm_b32", "v_mul_lo_u32", "v_lshlrev_b32", "v_add3_u32",
+           "v_mad_u32_u16", "v_mad_u32_u16 op_sel hi", "v_pk_mad_u16", "v_pk_mul_lo_u16",
+           "v_mad_u16 op_sel hi", "v_mul_u32_u24", "v_mul_hi_u32_u24", "v_mad_u32_u24", "v_mul_hi_u32",
+           "v_lshl_or_b32", "v_and_or_b32", "v_bfi_b32", "v_alignbyte_b32", "v_xad_u32", "v_or3_b32",
+           "v_lshl_add_u32", "v_lshrrev_b32 vgpr shift", "v_lshlrev_b32 vgpr shift", "v_dot2_u32_u16",
+           "v_pk_lshrrev_b16", "v_mul_lo_u16_sdwa dst hi", "v_mul_u32_u24_sdwa src hi",
+           "v_lshrrev_b32_sdwa shift hi", "v_and_b32_sdwa src lo", "v_pk_add_f16", "v_add_f16", "v_fma_f32",
+           "v_cvt_f32_u32",
+           "seq mul_lo_u32+and", "seq mul_lo_u32+and+xor", "seq mul_lo_u32+bitop3", "seq bfe+mul_lo_u32+bitop3",
+           "seq lshrrev+and+mul_lo_u32+bitop3", "seq lshrrev+mul_lo_u32+bitop3", "seq and+mul_lo_u32+bitop3",
+           "seq perm+and", "seq bfe+mul_lo_u32+bitop3 interleaved")
 
 
 def time_isa_rates(dev, iters: int = 2048) -> dict:
@@ -839,6 +902,8 @@ def main() -> int:
         print(f"[bench] decode ceiling: {dc}", file=sys.stderr, flush=True)
         extra["isa_issue_rates"] = time_isa_rates(dev)
         print(f"[bench] instruction issue rates: {extra['isa_issue_rates']}", file=sys.stderr, flush=True)
+        extra["row_block_rates"] = time_row_blocks(dev)
+        print(f"[bench] row-block rates: {extra['row_block_rates']}", file=sys.stderr, flush=True)
     if "null" in legs:
         # The same workloads on the timing-only twin library (each decoded
         # weight replaced by a loaded tile word): the skeleton of loads, MFMAs,

@@ -20,8 +20,11 @@
 // loop the kernels run), the decode alone (each decoded B operand is handed
 // to an empty asm statement, which forces its computation and emits no
 // instruction), and the MFMAs alone (the B operands are the tile words
-// themselves, register moves at most).  The launch's block count sets the
-// waves per SIMD.
+// themselves, register moves at most).  A fourth runs the whole loop with the
+// MFMA accumulators in the accumulation registers (AGPRs) instead of VGPRs,
+// and a fifth sums each weight's two addends on the VALU so an MFMA takes
+// eight weights per lane (half the MFMAs, no duplicated activations).
+// The launch's block count sets the waves per SIMD.
 //
 // 3. Instruction issue rates.  One VALU instruction of the decode's kinds in a
 // loop: eight independent chains per lane, 64 instructions per iteration, in
@@ -55,14 +58,41 @@ __global__ __launch_bounds__(PROBE_THREADS) void probe_read_kernel(const u32x4_t
     sink[tid] = acc[0] ^ acc[1] ^ acc[2] ^ acc[3];
 }
 
-enum ProbeMode : int { PROBE_FULL = 0, PROBE_DECODE_ONLY = 1, PROBE_MFMA_ONLY = 2 };
+enum ProbeMode : int {
+    PROBE_FULL = 0, PROBE_DECODE_ONLY = 1, PROBE_MFMA_ONLY = 2, PROBE_FULL_AGPR = 3, PROBE_NO_DUP = 4
+};
 
 // The decode kernels' mma_tile with the decode or the MFMA taken out (MODE).
 template <int BITS, int MODE>
 __device__ __forceinline__ void probe_tile(const uint32_t* W, const exl3::half8_t (&A)[4], exl3::float4_t (&acc)[16]) {
     using namespace exl3;
-    if constexpr (MODE == PROBE_FULL) {
+    if constexpr (MODE == PROBE_FULL || MODE == PROBE_FULL_AGPR) {
         mma_tile<BITS, CB_MCG>(W, A, acc);
+    } else if constexpr (MODE == PROBE_NO_DUP) {
+        // Each weight's two fp16 addends summed on the VALU (one packed add per
+        // two weights, after two byte permutes gather their low and high
+        // addends), so one MFMA takes eight weights per lane instead of four:
+        // half the MFMAs, A not duplicated (the probe reuses A[0..1] as the
+        // eight distinct activations).
+        typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+        static_for<16>([&](auto NI) {
+            constexpr int n = decltype(NI)::value;
+            static_for<2>([&](auto RI) {
+                constexpr int r2 = decltype(RI)::value;
+                u32x4_t b;
+                static_for<4>([&](auto JI) {
+                    constexpr int j = decltype(JI)::value;
+                    constexpr int r = 2 * r2 + j / 2, q0 = 2 * (j & 1);
+                    constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3) + q0;
+                    const uint32_t xa = decode_pair<BITS, CB_MCG, T0>(W);
+                    const uint32_t xb = decode_pair<BITS, CB_MCG, T0 + 1>(W);
+                    const h2_t lo = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(xb, xa, 0x01000504u));
+                    const h2_t hi = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(xb, xa, 0x03020706u));
+                    b[j] = __builtin_bit_cast(uint32_t, lo + hi);
+                });
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r2], __builtin_bit_cast(half8_t, b), acc[n], 0, 0, 0);
+            });
+        });
     } else {
         static_for<16>([&](auto NI) {
             constexpr int n = decltype(NI)::value;
@@ -94,6 +124,9 @@ template <int BITS, int MODE>
 __global__ __launch_bounds__(64, 2) void probe_decode_kernel(const uint32_t* __restrict__ words, int iters,
                                                             float* __restrict__ sink, uint64_t* __restrict__ clk) {
     using namespace exl3;
+    // PROBE_FULL_AGPR: an (empty) asm statement that clobbers an accumulation
+    // register makes the compiler keep the MFMA accumulators there
+    if constexpr (MODE == PROBE_FULL_AGPR) asm volatile("" ::: "a0");
     const int lane = threadIdx.x;
     uint32_t W[8 * BITS];
 #pragma unroll
@@ -138,15 +171,132 @@ static int launch_probe_decode(int mode, int blocks, int iters, const uint32_t* 
             hipLaunchKernelGGL((probe_decode_kernel<BITS, PROBE_MFMA_ONLY>), dim3(blocks), dim3(64), 0, st, words,
                                iters, sink, clk);
             break;
+        case PROBE_FULL_AGPR:
+            hipLaunchKernelGGL((probe_decode_kernel<BITS, PROBE_FULL_AGPR>), dim3(blocks), dim3(64), 0, st, words,
+                               iters, sink, clk);
+            break;
+        case PROBE_NO_DUP:
+            hipLaunchKernelGGL((probe_decode_kernel<BITS, PROBE_NO_DUP>), dim3(blocks), dim3(64), 0, st, words,
+                               iters, sink, clk);
+            break;
         default: return -1;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Row-block probe: the grouped GEMM's inner loop with each decoded B operand
+// applied to RB row blocks (16 rows each), the lane decoding the 16 / D
+// columns n = D m + p of its tile (D = 1: all 16).  A lane whose tile words are
+// rotated by p 32-element blocks (p * BITS words) finds those columns' windows
+// at the positions of p = 0, so the positions stay compile-time for any p; the
+// probe's words are opaque, so it decodes the p = 0 set.  MFMAs run in the
+// (n & 7, r, n >> 3) order of the GEMM, row block 0's right after its B is
+// decoded and row block b's (b > 0) on the previous B after the b-th of its
+// four windows, so no two MFMAs are adjacent.  One A operand per k-group
+// serves every row block (timing only).  Rates are per decoded weight.
+template <int BITS, int RB, int D>
+__device__ __forceinline__ void probe_rows_tile(const uint32_t* W, const exl3::half8_t (&A)[4],
+                                                exl3::float4_t (&acc)[RB][16 / D]) {
+    using namespace exl3;
+    constexpr int NA = 8 / D;                    // values of n & 7 per lane
+    half8_t Bprev;
+    static_for<NA * 8>([&](auto II) {
+        constexpr int i = decltype(II)::value;
+        constexpr int n = D * (i / 8) + 8 * (i & 1), r = (i >> 1) & 3;
+        constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+        u32x4_t b;
+        static_for<4>([&](auto QI) {
+            constexpr int q = decltype(QI)::value;
+            b[q] = decode_pair<BITS, CB_MCG, T0 + q>(W);
+            if constexpr (i > 0 && q + 1 < RB && q < 3) {
+                constexpr int np = D * ((i - 1) / 8) + 8 * ((i - 1) & 1), rp = ((i - 1) >> 1) & 3;
+                acc[q + 1][np / D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rp], Bprev, acc[q + 1][np / D], 0, 0, 0);
+            }
+        });
+        if constexpr (i > 0 && RB > 4) {
+            constexpr int np = D * ((i - 1) / 8) + 8 * ((i - 1) & 1), rp = ((i - 1) >> 1) & 3;
+            static_for<RB - 4>([&](auto BI) {
+                constexpr int bb = 4 + decltype(BI)::value;
+                acc[bb][np / D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rp], Bprev, acc[bb][np / D], 0, 0, 0);
+            });
+        }
+        const half8_t B = __builtin_bit_cast(half8_t, b);
+        acc[0][n / D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[r], B, acc[0][n / D], 0, 0, 0);
+        Bprev = B;
+    });
+    constexpr int nl = D * ((NA * 8 - 1) / 8) + 8, rl = 3;
+    static_for<RB - 1>([&](auto BI) {
+        constexpr int bb = 1 + decltype(BI)::value;
+        acc[bb][nl / D] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[rl], Bprev, acc[bb][nl / D], 0, 0, 0);
+    });
+}
+
+template <int BITS, int RB, int D>
+__global__ __launch_bounds__(64, 2) void probe_rows_kernel(const uint32_t* __restrict__ words, int iters,
+                                                          float* __restrict__ sink, uint64_t* __restrict__ clk) {
+    using namespace exl3;
+    const int lane = threadIdx.x;
+    uint32_t W[8 * BITS];
+#pragma unroll
+    for (int i = 0; i < 8 * BITS; ++i) W[i] = words[lane * 8 * BITS + i];
+    half8_t A[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) A[r][j] = (_Float16)((float)((lane + 3 * r + j) & 7) * 0.125f - 0.4375f);
+    float4_t acc[RB][16 / D];
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int i = 0; i < 16 / D; ++i) acc[b][i] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const uint64_t c0 = __builtin_amdgcn_s_memtime(), t0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 8 * BITS; ++i) asm volatile("" : "+v"(W[i]));
+        probe_rows_tile<BITS, RB, D>(W, A, acc);
+    }
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), t1 = __builtin_amdgcn_s_memrealtime();
+    float sum = 0.f;
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+        for (int i = 0; i < 16 / D; ++i) sum += acc[b][i][0] + acc[b][i][1] + acc[b][i][2] + acc[b][i][3];
+    sink[blockIdx.x * 64 + lane] = sum;
+    if (lane == 0) {
+        clk[2 * blockIdx.x] = c1 - c0;
+        clk[2 * blockIdx.x + 1] = t1 - t0;
+    }
+}
+
+// (row blocks, column divisor) pairs of the row-block probe, by index
+constexpr int PROBE_ROWS_CFG[][2] = {{1, 1}, {2, 1}, {2, 2}, {3, 2}, {4, 2}, {4, 4}, {6, 4}, {8, 4}};
+constexpr int PROBE_ROWS_N = 8;
+
+template <int BITS, int C>
+static void launch_probe_rows(int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                              hipStream_t st) {
+    hipLaunchKernelGGL((probe_rows_kernel<BITS, PROBE_ROWS_CFG[C][0], PROBE_ROWS_CFG[C][1]>), dim3(blocks), dim3(64),
+                       0, st, words, iters, sink, clk);
+}
+template <int BITS, int... C>
+static void probe_rows_dispatch(int cfg, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                                hipStream_t st, std::integer_sequence<int, C...>) {
+    ((cfg == C ? launch_probe_rows<BITS, C>(blocks, iters, words, sink, clk, st) : void()), ...);
 }
 
 // The instruction kinds of the issue-rate probe (exl3_probe_isa's `op`).
 enum ProbeIsaOp : int {
     ISA_AND = 0, ISA_XOR, ISA_LSHRREV, ISA_BITOP3, ISA_MUL_LO_U16, ISA_ADD_U32,
     ISA_BFE, ISA_ALIGNBIT, ISA_PERM, ISA_MUL_LO_U32, ISA_LSHLREV, ISA_ADD3,
+    // candidates for other decode sequences
+    ISA_MAD_U32_U16, ISA_MAD_U32_U16_HI, ISA_PK_MAD_U16, ISA_PK_MUL_LO_U16, ISA_MAD_U16_HI,
+    ISA_MUL_U32_U24, ISA_MUL_HI_U32_U24, ISA_MAD_U32_U24, ISA_MUL_HI_U32, ISA_LSHL_OR, ISA_AND_OR,
+    ISA_BFI, ISA_ALIGNBYTE, ISA_XAD, ISA_OR3, ISA_LSHL_ADD, ISA_LSHRREV_V, ISA_LSHLREV_V,
+    ISA_DOT2_U32_U16, ISA_PK_LSHRREV_B16, ISA_MUL_LO_U16_SDWA_HI, ISA_MUL_U32_U24_SDWA_W1,
+    ISA_LSHRREV_SDWA, ISA_AND_SDWA_W0, ISA_PK_ADD_F16, ISA_ADD_F16, ISA_FMA_F32, ISA_CVT_F32_U32,
+    // instruction sequences, one per call (the rate is per sequence)
+    SEQ_MUL_AND, SEQ_MUL_AND2, SEQ_MUL_BITOP3, SEQ_BFE_MUL_BITOP3, SEQ_LSHR_AND_MUL_BITOP3,
+    SEQ_LSHR_MUL_BITOP3, SEQ_AND_MUL_BITOP3, SEQ_PERM_AND, SEQ_BFE_MUL_BITOP3_IL,
     ISA_OPS
 };
 
@@ -163,7 +313,84 @@ __device__ __forceinline__ void isa_op(uint32_t& x, uint32_t k) {
     else if constexpr (OP == ISA_PERM) asm volatile("v_perm_b32 %0, %0, %1, %1" : "+v"(x) : "v"(k));
     else if constexpr (OP == ISA_MUL_LO_U32) asm volatile("v_mul_lo_u32 %0, %0, %1" : "+v"(x) : "v"(k));
     else if constexpr (OP == ISA_LSHLREV) asm volatile("v_lshlrev_b32 %0, 3, %0" : "+v"(x));
-    else asm volatile("v_add3_u32 %0, %0, %1, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_ADD3) asm volatile("v_add3_u32 %0, %0, %1, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MAD_U32_U16) asm volatile("v_mad_u32_u16 %0, %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MAD_U32_U16_HI)
+        asm volatile("v_mad_u32_u16 %0, %0, %1, %0 op_sel:[1,0,0,0]" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_PK_MAD_U16) asm volatile("v_pk_mad_u16 %0, %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_PK_MUL_LO_U16) asm volatile("v_pk_mul_lo_u16 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MAD_U16_HI)
+        asm volatile("v_mad_u16 %0, %0, %1, %0 op_sel:[0,0,1,1]" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MUL_U32_U24) asm volatile("v_mul_u32_u24 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MUL_HI_U32_U24) asm volatile("v_mul_hi_u32_u24 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MAD_U32_U24) asm volatile("v_mad_u32_u24 %0, %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MUL_HI_U32) asm volatile("v_mul_hi_u32 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_LSHL_OR) asm volatile("v_lshl_or_b32 %0, %0, 3, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_AND_OR) asm volatile("v_and_or_b32 %0, %0, %1, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_BFI) asm volatile("v_bfi_b32 %0, %1, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_ALIGNBYTE) asm volatile("v_alignbyte_b32 %0, %0, %1, 2" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_XAD) asm volatile("v_xad_u32 %0, %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_OR3) asm volatile("v_or3_b32 %0, %0, %1, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_LSHL_ADD) asm volatile("v_lshl_add_u32 %0, %0, 3, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_LSHRREV_V) asm volatile("v_lshrrev_b32 %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_LSHLREV_V) asm volatile("v_lshlrev_b32 %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_DOT2_U32_U16) asm volatile("v_dot2_u32_u16 %0, %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_PK_LSHRREV_B16) asm volatile("v_pk_lshrrev_b16 %0, 3, %0" : "+v"(x));
+    else if constexpr (OP == ISA_MUL_LO_U16_SDWA_HI)
+        asm volatile("v_mul_lo_u16_sdwa %0, %0, %1 dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:WORD_0 "
+                     "src1_sel:WORD_0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_MUL_U32_U24_SDWA_W1)
+        asm volatile("v_mul_u32_u24_sdwa %0, %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1 "
+                     "src1_sel:DWORD" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_LSHRREV_SDWA)
+        asm volatile("v_lshrrev_b32_sdwa %0, %1, %0 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD "
+                     "src1_sel:WORD_1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_AND_SDWA_W0)
+        asm volatile("v_and_b32_sdwa %0, %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_0 "
+                     "src1_sel:DWORD" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_PK_ADD_F16) asm volatile("v_pk_add_f16 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_ADD_F16) asm volatile("v_add_f16 %0, %0, %1" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_FMA_F32) asm volatile("v_fma_f32 %0, %0, %1, %0" : "+v"(x) : "v"(k));
+    else if constexpr (OP == ISA_CVT_F32_U32) asm volatile("v_cvt_f32_u32 %0, %0" : "+v"(x));
+    else static_assert(OP < SEQ_MUL_AND, "sequences run through isa_seq");
+}
+
+// One instruction sequence on each of eight independent chains, stage by
+// stage (all eight chains' first instruction, then their second, ...), so a
+// chain's next instruction issues eight instructions after its previous one.
+#define EXL3_R8(F) F(0) F(1) F(2) F(3) F(4) F(5) F(6) F(7)
+#define EXL3_MUL(i) "v_mul_lo_u32 %" #i ", %" #i ", %8\n\t"
+#define EXL3_AND(i) "v_and_b32 %" #i ", %" #i ", %8\n\t"
+#define EXL3_ANDC(i) "v_and_b32 %" #i ", 0xffff, %" #i "\n\t"
+#define EXL3_XOR(i) "v_xor_b32 %" #i ", %" #i ", %8\n\t"
+#define EXL3_BITOP3(i) "v_bitop3_b32 %" #i ", %" #i ", %8, %" #i " bitop3:0x6c\n\t"
+#define EXL3_BFE(i) "v_bfe_u32 %" #i ", %" #i ", 3, 16\n\t"
+#define EXL3_LSHR3(i) "v_lshrrev_b32 %" #i ", 3, %" #i "\n\t"
+#define EXL3_LSHR16(i) "v_lshrrev_b32 %" #i ", 16, %" #i "\n\t"
+#define EXL3_PERM(i) "v_perm_b32 %" #i ", %" #i ", %8, %8\n\t"
+#define EXL3_SEQ_ASM(BODY)                                                                   \
+    asm volatile(BODY : "+v"(x[0]), "+v"(x[1]), "+v"(x[2]), "+v"(x[3]), "+v"(x[4]), "+v"(x[5]), \
+                 "+v"(x[6]), "+v"(x[7]) : "v"(k))
+
+template <int OP>
+__device__ __forceinline__ void isa_seq(uint32_t (&x)[8], uint32_t k) {
+    if constexpr (OP == SEQ_MUL_AND) EXL3_SEQ_ASM(EXL3_R8(EXL3_MUL) EXL3_R8(EXL3_AND));
+    else if constexpr (OP == SEQ_MUL_AND2) EXL3_SEQ_ASM(EXL3_R8(EXL3_MUL) EXL3_R8(EXL3_AND) EXL3_R8(EXL3_XOR));
+    else if constexpr (OP == SEQ_MUL_BITOP3) EXL3_SEQ_ASM(EXL3_R8(EXL3_MUL) EXL3_R8(EXL3_BITOP3));
+    else if constexpr (OP == SEQ_BFE_MUL_BITOP3)
+        EXL3_SEQ_ASM(EXL3_R8(EXL3_BFE) EXL3_R8(EXL3_MUL) EXL3_R8(EXL3_BITOP3));
+    else if constexpr (OP == SEQ_LSHR_AND_MUL_BITOP3)
+        EXL3_SEQ_ASM(EXL3_R8(EXL3_LSHR3) EXL3_R8(EXL3_ANDC) EXL3_R8(EXL3_MUL) EXL3_R8(EXL3_BITOP3));
+    else if constexpr (OP == SEQ_LSHR_MUL_BITOP3)
+        EXL3_SEQ_ASM(EXL3_R8(EXL3_LSHR16) EXL3_R8(EXL3_MUL) EXL3_R8(EXL3_BITOP3));
+    else if constexpr (OP == SEQ_AND_MUL_BITOP3)
+        EXL3_SEQ_ASM(EXL3_R8(EXL3_ANDC) EXL3_R8(EXL3_MUL) EXL3_R8(EXL3_BITOP3));
+    else if constexpr (OP == SEQ_PERM_AND) EXL3_SEQ_ASM(EXL3_R8(EXL3_PERM) EXL3_R8(EXL3_AND));
+    else  // software-pipelined: round j extracts chain j, multiplies chain j-3, masks chain j-6
+        EXL3_SEQ_ASM(EXL3_BFE(0) EXL3_MUL(5) EXL3_BITOP3(2) EXL3_BFE(1) EXL3_MUL(6) EXL3_BITOP3(3)
+                     EXL3_BFE(2) EXL3_MUL(7) EXL3_BITOP3(4) EXL3_BFE(3) EXL3_MUL(0) EXL3_BITOP3(5)
+                     EXL3_BFE(4) EXL3_MUL(1) EXL3_BITOP3(6) EXL3_BFE(5) EXL3_MUL(2) EXL3_BITOP3(7)
+                     EXL3_BFE(6) EXL3_MUL(3) EXL3_BITOP3(0) EXL3_BFE(7) EXL3_MUL(4) EXL3_BITOP3(1));
 }
 
 template <int OP>
@@ -177,9 +404,14 @@ __global__ __launch_bounds__(256) void probe_isa_kernel(int iters, uint32_t* __r
     const uint64_t c0 = __builtin_amdgcn_s_memtime(), t0 = __builtin_amdgcn_s_memrealtime();
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
-        for (int r = 0; r < 8; ++r)
+        for (int r = 0; r < 8; ++r) {
+            if constexpr (OP >= SEQ_MUL_AND) {
+                isa_seq<OP>(x, k);
+            } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) isa_op<OP>(x[i], k);
+                for (int i = 0; i < 8; ++i) isa_op<OP>(x[i], k);
+            }
+        }
     }
     const uint64_t c1 = __builtin_amdgcn_s_memtime(), t1 = __builtin_amdgcn_s_memrealtime();
     uint32_t v = 0u;
@@ -195,6 +427,12 @@ __global__ __launch_bounds__(256) void probe_isa_kernel(int iters, uint32_t* __r
 template <int OP>
 static void launch_isa(int blocks, int iters, uint32_t* sink, uint64_t* clk, hipStream_t st) {
     hipLaunchKernelGGL((probe_isa_kernel<OP>), dim3(blocks), dim3(256), 0, st, iters, sink, clk);
+}
+
+template <int... OPS>
+static void isa_dispatch(int op, int blocks, int iters, uint32_t* sink, uint64_t* clk, hipStream_t st,
+                         std::integer_sequence<int, OPS...>) {
+    ((op == OPS ? launch_isa<OPS>(blocks, iters, sink, clk, st) : void()), ...);
 }
 
 extern "C" {
@@ -213,7 +451,8 @@ int exl3_probe_threads(void) { return PROBE_THREADS; }
 
 // Launches `blocks` single-wave workgroups of the decode-rate probe at `bits`
 // (2, 3, 4 or 6; MCG codebook) in `mode` (0 decode + MFMA, 1 decode only, 2
-// MFMA only), each covering 16384 weights per iteration for `iters`
+// MFMA only, 3 decode + MFMA with the accumulators in AGPRs, 4 decode + the
+// addends summed on the VALU + half the MFMAs), each covering 16384 weights per iteration for `iters`
 // iterations.  words: 64 * 8 * bits uint32 of tile data (any values); sink:
 // blocks * 64 floats; clk: 2 * blocks uint64 (per workgroup the shader clock
 // cycles and the 100 MHz reference ticks of its loop, which give the clock the
@@ -232,33 +471,37 @@ int exl3_probe_decode_mode(int bits, int mode, int blocks, int iters, const uint
 }
 
 // Instruction issue-rate probe: `blocks` four-wave workgroups, each wave
-// running `iters` iterations of 64 instructions of kind `op` (0 v_and_b32, 1
-// v_xor_b32, 2 v_lshrrev_b32, 3 v_bitop3_b32, 4 v_mul_lo_u16, 5 v_add_u32, 6
-// v_bfe_u32, 7 v_alignbit_b32, 8 v_perm_b32, 9 v_mul_lo_u32, 10 v_lshlrev_b32,
-// 11 v_add3_u32).  sink: blocks * 256 uint32; clk: 2 * 4 * blocks uint64, per
+// running `iters` iterations of 64 instructions of kind `op` (ProbeIsaOp order:
+// 0 v_and_b32 ... 11 v_add3_u32, then the candidates from 12 v_mad_u32_u16).
+// sink: blocks * 256 uint32; clk: 2 * 4 * blocks uint64, per
 // wave as exl3_probe_decode_mode's per workgroup.  Returns 0, or -1 on a bad
 // argument or launch error.
 int exl3_probe_isa(int op, int blocks, int iters, uint32_t* sink, uint64_t* clk, void* stream) {
     if (!sink || !clk || blocks < 1 || iters < 1 || op < 0 || op >= ISA_OPS) return -1;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    switch (op) {
-        case ISA_AND: launch_isa<ISA_AND>(blocks, iters, sink, clk, st); break;
-        case ISA_XOR: launch_isa<ISA_XOR>(blocks, iters, sink, clk, st); break;
-        case ISA_LSHRREV: launch_isa<ISA_LSHRREV>(blocks, iters, sink, clk, st); break;
-        case ISA_BITOP3: launch_isa<ISA_BITOP3>(blocks, iters, sink, clk, st); break;
-        case ISA_MUL_LO_U16: launch_isa<ISA_MUL_LO_U16>(blocks, iters, sink, clk, st); break;
-        case ISA_ADD_U32: launch_isa<ISA_ADD_U32>(blocks, iters, sink, clk, st); break;
-        case ISA_BFE: launch_isa<ISA_BFE>(blocks, iters, sink, clk, st); break;
-        case ISA_ALIGNBIT: launch_isa<ISA_ALIGNBIT>(blocks, iters, sink, clk, st); break;
-        case ISA_PERM: launch_isa<ISA_PERM>(blocks, iters, sink, clk, st); break;
-        case ISA_MUL_LO_U32: launch_isa<ISA_MUL_LO_U32>(blocks, iters, sink, clk, st); break;
-        case ISA_LSHLREV: launch_isa<ISA_LSHLREV>(blocks, iters, sink, clk, st); break;
-        default: launch_isa<ISA_ADD3>(blocks, iters, sink, clk, st); break;
-    }
+    isa_dispatch(op, blocks, iters, sink, clk, st, std::make_integer_sequence<int, ISA_OPS>{});
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 int exl3_probe_isa_ops(void) { return ISA_OPS; }
+
+// Launches `blocks` single-wave workgroups of the row-block probe at `bits`
+// (2 or 3; MCG) for configuration `cfg` (0-7: (row blocks, column divisor) =
+// (1,1) (2,1) (2,2) (3,2) (4,2) (4,4) (6,4) (8,4)), each iteration decoding
+// 64 * 256 / divisor weights; buffers and clocks as exl3_probe_decode_mode.
+// Returns 0, or -1 on a bad argument or launch error.
+int exl3_probe_rows(int bits, int cfg, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                    void* stream) {
+    if (!words || !sink || !clk || blocks < 1 || iters < 1 || cfg < 0 || cfg >= PROBE_ROWS_N) return -1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (bits == 2)
+        probe_rows_dispatch<2>(cfg, blocks, iters, words, sink, clk, st, std::make_integer_sequence<int, PROBE_ROWS_N>{});
+    else if (bits == 3)
+        probe_rows_dispatch<3>(cfg, blocks, iters, words, sink, clk, st, std::make_integer_sequence<int, PROBE_ROWS_N>{});
+    else
+        return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 // The decode kernels' loop (mode 0) at `bits`.
 int exl3_probe_decode(int bits, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
