@@ -462,11 +462,21 @@ def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True, lib=N
     return us, flops, nbytes, distinct
 
 
-def prefill_decoded_weights(layer, tokens: int, topk: int, seed: int, tile_rows: int = 32) -> tuple[float, float]:
+def prefill_tiles(c: int) -> int:
+    """Tiles the prefill GEMMs run for an expert with c routed rows
+    (csrc/exl3_prefill_capi.hip pf_plan_kernel): one narrow tile of up to 32
+    rows, or above 32 rows wide tiles of up to 64 rows with a last part of at
+    most 32 rows in a narrow tile.  Each tile decodes the expert once."""
+    if c <= 32:
+        return 1 if c > 0 else 0
+    full, rem = divmod(c, 64)
+    return full + (1 if rem > 0 else 0)
+
+
+def prefill_decoded_weights(layer, tokens: int, topk: int, seed: int) -> tuple[float, float]:
     """Weights the prefill GEMMs decode per layer on time_prefill's routing
-    pool (each expert's gate, up and down once per tile of up to `tile_rows`
-    routed rows), and the minimum (each active expert once), means over the
-    pool."""
+    pool (each expert's gate, up and down once per tile, prefill_tiles), and
+    the minimum (each active expert once), means over the pool."""
     from dsv4_carve_amd import synth
 
     n_exp = len(layer.bits)
@@ -475,7 +485,7 @@ def prefill_decoded_weights(layer, tokens: int, topk: int, seed: int, tile_rows:
     for i in range(4):
         ids = synth.zipf_routing(tokens, n_exp, topk, seed=seed + i)[0].reshape(-1)
         cnt = np.bincount(ids[(ids >= 0) & (ids < n_exp)], minlength=n_exp)
-        dec.append(float(np.ceil(cnt / tile_rows).sum()) * per)
+        dec.append(float(sum(prefill_tiles(int(c)) for c in cnt)) * per)
         low.append(float((cnt > 0).sum()) * per)
     return float(np.mean(dec)), float(np.mean(low))
 

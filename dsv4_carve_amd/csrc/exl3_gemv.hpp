@@ -336,17 +336,21 @@ __device__ __forceinline__ float4_t sum_partials(const float* p, uint32_t voff, 
 
 // ---------------------------------------------------------------- Hadamard (wave64)
 
-// The value of lane (lane ^ M) within groups of 8 lanes, M = 1, 2 or 4, by
+// The value of lane (lane ^ M) within rows of 16 lanes, M = 1, 2, 4 or 8, by
 // DPP moves (no LDS traffic): xor 1 and 2 are quad permutations, xor 4 a quad
-// reversal (xor 3) followed by the half-row mirror (xor 7).
+// reversal (xor 3) followed by the half-row mirror (xor 7), xor 8 the row
+// mirror (xor 15) followed by the half-row mirror.
 template <int M>
 __device__ __forceinline__ float dpp_xor(float v) {
     const int x = __builtin_bit_cast(int, v);
     if constexpr (M == 1) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0xB1, 0xF, 0xF, false));
     else if constexpr (M == 2) return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(x, 0x4E, 0xF, 0xF, false));
-    else {
-        static_assert(M == 4, "xor 1, 2 or 4");
+    else if constexpr (M == 4) {
         const int r = __builtin_amdgcn_mov_dpp(x, 0x1B, 0xF, 0xF, false);
+        return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x141, 0xF, 0xF, false));
+    } else {
+        static_assert(M == 8, "xor 1, 2, 4 or 8");
+        const int r = __builtin_amdgcn_mov_dpp(x, 0x140, 0xF, 0xF, false);
         return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(r, 0x141, 0xF, 0xF, false));
     }
 }

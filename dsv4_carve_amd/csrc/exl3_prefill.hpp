@@ -4,12 +4,16 @@
 //
 // Launch sequence (one stream, no host synchronisation, no persistent state):
 //   1. plan:     route (token, slot) pairs by expert (counting sort in LDS),
-//                cut each expert's rows into tiles of PF_RB rows.
+//                cut each expert's rows into tiles: narrow tiles of up to
+//                PF_RB rows for an expert with at most PF_RB rows (and for a
+//                remainder of at most PF_RB), wide tiles of up to PF_RB_WIDE
+//                rows otherwise.
 //   2. rotate:   Xh[proj][pair] = half(H (half(x[token] * suh[e])) / sqrt(128))
 //                for the gate and up projections.
-//   3. gemm:     gate/up tiles: decode each 64x256 weight step once per tile
-//                and feed it to the MFMAs of both 16-row blocks; epilogue
-//                output Hadamard + svh -> fp32 [pair][I].
+//   3. gemm:     gate/up tiles: decode each weight step once per tile and
+//                feed it to the MFMAs of every 16-row block (two in a narrow
+//                tile, four in a wide one); epilogue output Hadamard + svh ->
+//                fp32 [pair][I].
 //   4. act:      half(silu(min(g, L)) * clamp(u, -L, L)), x down_suh, input
 //                Hadamard -> fp16 down input [pair][I].
 //   5. gemm:     down tiles, same kernel -> fp32 [pair][H].
@@ -29,7 +33,9 @@
 namespace exl3 {
 namespace prefill {
 
-constexpr int PF_RB = 32;                 // rows per tile (two MFMA row blocks)
+constexpr int PF_RB = 32;                 // rows per narrow tile (two MFMA row blocks)
+constexpr int PF_RB_WIDE = 64;            // rows per wide tile (four MFMA row blocks)
+constexpr int PF_A_PAD_ROWS = 16;         // rows after each A buffer that a wide tile may read
 constexpr int PF_MAX_EXPERTS = 2048;
 constexpr int PF_MAX_TOPK = 9;
 constexpr int PF_MAX_PAIRS = 65536;
@@ -40,12 +46,21 @@ constexpr int PF_META_PAIRS = 0, PF_META_ERROR = 1, PF_META_TILES = 2;
 constexpr int PF_ERR_WIDTH = 1;          // an expert width outside bits_mask was routed (it contributed nothing)
 
 struct PfLayout {
-    int64_t meta, eoff, toff, tile_e, tile_r0, tile_n, pair_slot, pair_e, pos, Xh, GU, AD, D, total;
+    int64_t meta, eoff, toff, tile_e, tile_r0, tile_n, tile_w, pair_slot, pair_e, pos, Xh, GU, AD, D, total;
     int64_t max_tiles;
     int ks_up, ks_down;     // k-splits: GU is [ks_up][2][pairs][I], D is [ks_down][pairs][H]
 };
 
 __host__ __device__ inline int64_t pf_al(int64_t v) { return (v + 255) / 256 * 256; }
+
+// Tile-table entries of an expert with c routed rows: one narrow tile up to
+// PF_RB rows; above that two per wide tile of up to PF_RB_WIDE rows, and one
+// for a last part of at most PF_RB rows.  Never more than ceil(c / PF_RB).
+__host__ __device__ inline int pf_tile_entries(int c) {
+    if (c <= PF_RB) return c > 0 ? 1 : 0;
+    const int full = c / PF_RB_WIDE, rem = c - full * PF_RB_WIDE;
+    return 2 * full + (rem > PF_RB ? 2 : rem > 0 ? 1 : 0);
+}
 
 // k-splits of the gate/up (K = hidden) and down (K = intermediate) GEMMs: as
 // many as keep an even number of 64-row steps per part, up to 2 each (on the
@@ -64,6 +79,8 @@ inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
     PfLayout L;
     L.ks_up = pf_ksplit(H, 2);
     L.ks_down = pf_ksplit(I, 2);
+    // An expert with c rows has at most ceil(c / PF_RB) tile entries (a wide
+    // tile is two entries, one per half of the column blocks).
     L.max_tiles = E + (pairs + PF_RB - 1) / PF_RB;
     int64_t o = 0;
     L.meta = o;      o = pf_al(o + 64);
@@ -72,12 +89,15 @@ inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
     L.tile_e = o;    o = pf_al(o + L.max_tiles * 4);
     L.tile_r0 = o;   o = pf_al(o + L.max_tiles * 4);
     L.tile_n = o;    o = pf_al(o + L.max_tiles * 4);
+    L.tile_w = o;    o = pf_al(o + L.max_tiles * 4);
     L.pair_slot = o; o = pf_al(o + pairs * 4);
     L.pair_e = o;    o = pf_al(o + pairs * 4);
     L.pos = o;       o = pf_al(o + pairs * 4);
-    L.Xh = o;        o = pf_al(o + 2 * pairs * H * 2);
+    // A wide tile's last row block may read up to 15 rows past its last row
+    // (pf_tile_wide): the A buffers end with that many rows of padding.
+    L.Xh = o;        o = pf_al(o + (2 * pairs + PF_A_PAD_ROWS) * H * 2);
     L.GU = o;        o = pf_al(o + (int64_t)L.ks_up * 2 * pairs * I * 4);
-    L.AD = o;        o = pf_al(o + pairs * I * 2);
+    L.AD = o;        o = pf_al(o + (pairs + PF_A_PAD_ROWS) * I * 2);
     L.D = o;         o = pf_al(o + (int64_t)L.ks_down * pairs * H * 4);
     L.total = o;
     return L;
@@ -270,6 +290,250 @@ __device__ __forceinline__ void pf_tile(bool valid, const uint16_t* A, int row0,
         }
 }
 
+// ---------------------------------------------------------------- 3/5b. wide tiles
+//
+// An expert with more than PF_RB routed rows is cut into tiles of PF_RB_WIDE
+// rows (a remainder of at most PF_RB rows goes to a narrow tile), so its
+// weights are decoded once per 64 rows instead of once per 32.  A wide tile is
+// two entries of the tile table, one per half of the column blocks, so a
+// group's blocks are the same count as a narrow tile's: the two waves of a
+// block share one 256-column block, 128 columns (8 n-tiles) each, and each
+// wave applies every decoded B operand to four 16-row blocks.
+//
+// Lane c of a wave holds n-tile c >> 1 and the eight columns n = 2m + p of it,
+// p = c & 1 (MFMA column c is tile column 2m + p of n-tile c >> 1).  By the
+// tile permutation (tile_t), column 2m + 1's windows sit 32 elements after
+// column 2m's, so a lane of parity 1 loads its tile rotated by one 32-element
+// block (BITS words) and decodes the windows of the even columns at their
+// compile-time positions; the stream is circular, so each rotated window holds
+// the bits of the window it stands for.
+//
+// Accumulator acc[rb][m][i] is C[16 rb + 4 g + i][16 (c >> 1) + 2 m + (c & 1)].
+// Each accumulator takes the same k-groups in the same order as a narrow
+// tile's, with the same MFMA operands, and the epilogue pairs the same
+// elements in the same stage order, so every row's output is bitwise what a
+// narrow tile gives.
+
+// N consecutive words at byte offset voff + soff of a buffer, in loads of at
+// most four words (4-byte alignment suffices).  Constant offsets go into the
+// uniform soff, so every load of a tile shares the lane's one voff.
+template <int N>
+__device__ __forceinline__ void load_words(uint32_t* dst, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    if constexpr (N >= 4) {
+        const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+        dst[0] = v[0]; dst[1] = v[1]; dst[2] = v[2]; dst[3] = v[3];
+        if constexpr (N > 4) load_words<N - 4>(dst + 4, r, voff, soff + 16);
+    } else if constexpr (N == 3) {
+        typedef uint32_t u32x3_t __attribute__((ext_vector_type(3)));
+        const u32x3_t v = __builtin_bit_cast(u32x3_t, __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 0));
+        dst[0] = v[0]; dst[1] = v[1]; dst[2] = v[2];
+    } else if constexpr (N == 2) {
+        const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+        dst[0] = v.x; dst[1] = v.y;
+    } else {
+        dst[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+    }
+}
+
+// The words of a lane's tile that its columns' windows read, rotated by p (0
+// or 1) blocks of BITS words (buffer block b is stream block (b + p) & 7).
+// The even columns' windows lie in the even blocks of the rotated stream and
+// reach at most 16 - BITS bits back, into the last word of the block before:
+// 4 (BITS + 1) of the 8 BITS words.  The other words are never written or
+// read, so they take no registers.
+template <int BITS>
+struct WideTile {
+    uint32_t w[8 * BITS];
+};
+
+// vrot: byte offset of the lane's rotated tile (its first word plus p blocks),
+// vlast: of the word before rotated block 0; soff: the step's byte offset.
+template <int BITS>
+__device__ __forceinline__ void load_tile_rot(WideTile<BITS>& d, __amdgpu_buffer_rsrc_t r, uint32_t vrot,
+                                              uint32_t vlast, uint32_t soff) {
+    load_words<BITS>(d.w, r, vrot, soff);
+    load_words<1>(d.w + 8 * BITS - 1, r, vlast, soff);
+#pragma unroll
+    for (int b = 2; b < 8; b += 2) load_words<BITS + 1>(d.w + b * BITS - 1, r, vrot, soff + 4 * (b * BITS - 1));
+}
+
+// The MFMAs of one decoded wide-tile step: k-group r outer (the four row
+// blocks' A operands of one k-group live at a time), then the lane's columns
+// in pairs n, n + 8 whose eight windows are consecutive in the stream.  Row
+// block 0's MFMA follows its B; blocks 1-3 take the previous B between the
+// next B's window decodes, and the k-group's last B after its own.
+template <int BITS, int CB>
+__device__ __forceinline__ void mma_tile_wide(const uint32_t* W, const u32x4_t (&a)[4][2], float4_t (&acc)[4][8]) {
+    static_for<4>([&](auto RI) {
+        constexpr int r = decltype(RI)::value;
+        // keeps each k-group's operand builds and decodes within the k-group,
+        // so no more than one k-group's A operands are live
+        __builtin_amdgcn_sched_barrier(0);
+        half8_t Ar[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) Ar[rb] = a_from_words(a[rb][0], a[rb][1], r);
+        half8_t Bprev;
+        static_for<8>([&](auto II) {
+            constexpr int i = decltype(II)::value;
+            constexpr int n = 2 * (i >> 1) + 8 * (i & 1), m = n / 2;
+            constexpr int ip = i > 0 ? i - 1 : 0;
+            constexpr int mp = (2 * (ip >> 1) + 8 * (ip & 1)) / 2;
+            constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3);
+            u32x4_t b;
+            static_for<4>([&](auto QI) {
+                constexpr int q = decltype(QI)::value;
+                b[q] = decode_pair<BITS, CB, T0 + q>(W);
+                if constexpr (i > 0 && q < 3)
+                    acc[q + 1][mp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ar[q + 1], Bprev, acc[q + 1][mp], 0, 0, 0);
+            });
+            const half8_t B = __builtin_bit_cast(half8_t, b);
+            acc[0][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ar[0], B, acc[0][m], 0, 0, 0);
+            Bprev = B;
+        });
+        static_for<3>([&](auto BI) {
+            constexpr int rb = 1 + decltype(BI)::value;
+            acc[rb][7] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ar[rb], Bprev, acc[rb][7], 0, 0, 0);
+        });
+    });
+}
+
+// One (wide tile, 128-column block c128) of C[rows, N] = A[rows, K] . Wq[K, N]:
+// as pf_tile, for nrows <= 64 rows of A from row0.
+// A wave-uniform pointer in scalar registers.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+template <int BITS, int CB>
+__device__ __forceinline__ void pf_tile_wide(bool valid, const uint16_t* A, int row0, int nrows,
+                                             const int16_t* trellis, const uint16_t* svh, int K, int k0, int nsteps,
+                                             int N, int c128, float* out) {
+    if (!valid) return;
+    // every argument is the same across the wave; in scalar registers, the
+    // buffer resources below need no per-lane handling
+    A = uniform_ptr(A);
+    trellis = uniform_ptr(trellis);
+    svh = uniform_ptr(svh);
+    out = uniform_ptr(out);
+    row0 = __builtin_amdgcn_readfirstlane(row0);
+    nrows = __builtin_amdgcn_readfirstlane(nrows);
+    k0 = __builtin_amdgcn_readfirstlane(k0);
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int g = lane >> 4, c = lane & 15, j = c >> 1, p = c & 1;
+    const int n16 = N / 16;
+    const int nt = 8 * c128 + j;                      // N is a multiple of 256, c128 < N / 128
+    constexpr int TW = 8 * BITS;                      // words per tile
+    // one matrix's trellis is below 2 GiB, so byte offsets fit 32 bits
+    const __amdgpu_buffer_rsrc_t trsrc = dev_rsrc(trellis);
+    const uint32_t vtile = ((uint32_t)(k0 / 16 + g) * (uint32_t)n16 + (uint32_t)nt) * (uint32_t)(TW * 4);
+    const uint32_t vrot = vtile + 4 * p * BITS, vlast = vtile + 4 * (p ? BITS - 1 : TW - 1);
+    const uint32_t tstep = 4u * 4u * (uint32_t)n16 * TW;   // bytes between steps
+    // A rows of this lane: 16 rb + c, k-slice g of each step.  A row block
+    // wholly past nrows re-reads block 0; in the last block that holds rows,
+    // lanes past nrows read up to 15 rows beyond the tile's last row (other
+    // pairs' rows, or the padding rows that end each A buffer).  Their
+    // accumulator rows are never stored.  So one lane offset serves every row
+    // block, the block's offset going in the uniform part.
+    const __amdgpu_buffer_rsrc_t arsrc = dev_rsrc(A + (size_t)row0 * K + k0);
+    const uint32_t avo = ((uint32_t)c * (uint32_t)K + 16u * g) * 2u;
+    uint32_t arb[4];                                   // byte offset of each row block's rows
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) arb[rb] = 16 * rb < nrows ? 32u * (uint32_t)K * rb : 0u;
+
+    float4_t acc[4][8];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int m = 0; m < 8; ++m) acc[rb][m] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    WideTile<BITS> t0, t1;
+    u32x4_t ac[4][2];
+    auto load_a = [&](int s) {
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            ac[rb][0] = __builtin_bit_cast(u32x4_t, ld_dev4_buf<CPOL_PLAIN>(arsrc, avo, (uint32_t)s * 128u + arb[rb]));
+            ac[rb][1] =
+                __builtin_bit_cast(u32x4_t, ld_dev4_buf<CPOL_PLAIN>(arsrc, avo, (uint32_t)s * 128u + arb[rb] + 16u));
+        }
+    };
+    // nsteps is even; the step's A loads go out before the next step's tile
+    load_tile_rot<BITS>(t0, trsrc, vrot, vlast, 0u);
+    for (int s = 0; s < nsteps; s += 2) {
+        load_a(s);
+        load_tile_rot<BITS>(t1, trsrc, vrot, vlast, (uint32_t)(s + 1) * tstep);
+        mma_tile_wide<BITS, CB>(t0.w, ac, acc);
+        load_a(s + 1);
+        // the last iteration reloads its own step (a valid address, unused)
+        load_tile_rot<BITS>(t0, trsrc, vrot, vlast, (uint32_t)min(s + 2, nsteps - 1) * tstep);
+        mma_tile_wide<BITS, CB>(t1.w, ac, acc);
+    }
+
+    // Epilogue in registers.  The 128 columns of the wave are one Hadamard
+    // block, column 16 j + 2 m + p: stage h = 1 pairs lanes c, c ^ 1; h = 2, 4,
+    // 8 run over m in registers; h = 16, 32, 64 pair lanes c ^ 2, 4, 8.  Then
+    // each lane swaps half its values with lane c ^ 1 so that it stores eight
+    // consecutive columns, 16 j + 8 p .. + 7, of each of its rows.
+    float sv[8];
+    {
+        const u32x4_t* sp = reinterpret_cast<const u32x4_t*>(svh + (size_t)16 * nt);
+        const u32x4_t s0 = sp[0], s1 = sp[1];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            sv[m] = f16_bits_to_f32((uint16_t)(p ? s0[m] >> 16 : s0[m] & 0xffffu));
+            sv[4 + m] = f16_bits_to_f32((uint16_t)(p ? s1[m] >> 16 : s1[m] & 0xffffu));
+        }
+    }
+    const float sg1 = (c & 1) ? -1.f : 1.f, sg2 = (c & 2) ? -1.f : 1.f;
+    const float sg4 = (c & 4) ? -1.f : 1.f, sg8 = (c & 8) ? -1.f : 1.f;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        if (16 * rb >= nrows) break;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float v[8];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) v[m] = acc[rb][m][i];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) v[m] = bfly(v[m], dpp_xor<1>(v[m]), sg1);
+#pragma unroll
+            for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int a = (q / h) * 2 * h + (q % h);
+                    const float x0 = v[a], x1 = v[a + h];
+                    v[a] = x0 + x1;
+                    v[a + h] = x0 - x1;
+                }
+#pragma unroll
+            for (int m = 0; m < 8; ++m) v[m] = bfly(v[m], dpp_xor<2>(v[m]), sg2);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) v[m] = bfly(v[m], dpp_xor<4>(v[m]), sg4);
+#pragma unroll
+            for (int m = 0; m < 8; ++m) v[m] = bfly(v[m], dpp_xor<8>(v[m]), sg8);
+            float y[8], o[8];
+#pragma unroll
+            for (int m = 0; m < 8; ++m) y[m] = v[m] * HAD_NORM * sv[m];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                // parity 0 keeps columns 2q (own) and 2q + 1 (partner's y[q]);
+                // parity 1 keeps 8 + 2q (partner's y[4 + q]) and 9 + 2q (own)
+                const float r = dpp_xor<1>(p ? y[q] : y[4 + q]);
+                o[2 * q] = p ? r : y[q];
+                o[2 * q + 1] = p ? y[4 + q] : r;
+            }
+            const int row = 16 * rb + 4 * g + i;
+            if (row < nrows) {
+                float4_t* dst = reinterpret_cast<float4_t*>(out + (size_t)(row0 + row) * N + 128 * c128 + 16 * j + 8 * p);
+                dst[0] = float4_t{o[0], o[1], o[2], o[3]};
+                dst[1] = float4_t{o[4], o[5], o[6], o[7]};
+            }
+        }
+    }
+}
+
 // Items: gate/up (DOWN = false) = (tile, projection, k-part, column block of
 // I); down (DOWN = true) = (tile, k-part, column block of H).  The items of
 // one (tile, projection, k-part) -- a group -- read the same rows of A.  Two
@@ -316,8 +580,11 @@ void pf_gemm_kernel(PfParams P) {
     const int t = g / combos, c = g - t * combos;
     const bool tile_ok = t < pat<int>(P.scratch, L.meta)[PF_META_TILES];
     const int e = tile_ok ? pat<int>(P.scratch, L.tile_e)[t] : 0;
+    // wide tile entry: its half of the column blocks, both waves on one block
+    const int half = tile_ok ? pat<int>(P.scratch, L.tile_w)[t] : -1;
+    const int cbx = half < 0 ? cb : half * G + (jj % G);      // 256-column block
     const int width = P.ebits ? (int)P.ebits[e] : P.bits;    // the same for the block's two waves
-    const bool valid = tile_ok && cb < ncb && (width == BITS || (BITS2 > 0 && width == BITS2));
+    const bool valid = tile_ok && cbx < ncb && (width == BITS || (BITS2 > 0 && width == BITS2));
     if (!__syncthreads_or(valid)) return;
     const int proj = DOWN ? 0 : c / KS, ks = c % KS;
     const int row0 = valid ? pat<int>(P.scratch, L.tile_r0)[t] : 0;
@@ -330,11 +597,19 @@ void pf_gemm_kernel(PfParams P) {
     const uint16_t* svh = reinterpret_cast<const uint16_t*>((DOWN ? P.dsv : (proj ? P.usv : P.gsv))[e]);
     float* out = DOWN ? pat<float>(P.scratch, L.D) + (size_t)ks * P.P * P.H
                       : pat<float>(P.scratch, L.GU) + ((size_t)ks * 2 + proj) * P.P * P.I;
-    if (BITS2 == 0 || width == BITS)
+    constexpr int B2 = BITS2 > 0 ? BITS2 : BITS;
+    if (half >= 0) {
+        if (BITS2 == 0 || width == BITS)
+            pf_tile_wide<BITS, CB>(valid, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N,
+                                   2 * cbx + wave, out);
+        else
+            pf_tile_wide<B2, CB>(valid, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, 2 * cbx + wave,
+                                 out);
+    } else if (BITS2 == 0 || width == BITS) {
         pf_tile<BITS, CB>(valid, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out);
-    else
-        pf_tile<(BITS2 > 0 ? BITS2 : BITS), CB>(valid, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N,
-                                                cb, out);
+    } else {
+        pf_tile<B2, CB>(valid, A, row0, nrows, tr, svh, K, ks * kpart, kpart / STEP_K, N, cb, out);
+    }
 }
 
 // Launchers of the grouped GEMM for one bit width, and for widths 3 and 2

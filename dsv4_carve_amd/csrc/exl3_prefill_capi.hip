@@ -62,7 +62,7 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     __syncthreads();
     for (int e = tid; e < P.E; e += nt) {
         off[e] = cnt[e];
-        tof[e] = (cnt[e] + PF_RB - 1) / PF_RB;
+        tof[e] = pf_tile_entries(cnt[e]);
     }
     __syncthreads();
     wave0_scan(off, P.E, &totals[0]);
@@ -73,14 +73,33 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     int* tile_e = pat<int>(P.scratch, L.tile_e);
     int* tile_r0 = pat<int>(P.scratch, L.tile_r0);
     int* tile_n = pat<int>(P.scratch, L.tile_n);
+    int* tile_w = pat<int>(P.scratch, L.tile_w);
     for (int e = tid; e < P.E; e += nt) {
         eoff[e] = off[e];
         toff[e] = tof[e];
         const int c = cnt[e];
-        for (int j = 0; j * PF_RB < c; ++j) {
-            tile_e[tof[e] + j] = e;
-            tile_r0[tof[e] + j] = off[e] + j * PF_RB;
-            tile_n[tof[e] + j] = min(PF_RB, c - j * PF_RB);
+        int k = tof[e];
+        auto entry = [&](int r0, int n, int w) {
+            tile_e[k] = e;
+            tile_r0[k] = r0;
+            tile_n[k] = n;
+            tile_w[k] = w;
+            ++k;
+        };
+        if (c <= PF_RB) {
+            if (c > 0) entry(off[e], c, -1);
+        } else {
+            // wide tiles of PF_RB_WIDE rows, two entries each (column-block
+            // halves); a remainder of at most PF_RB rows in a narrow tile
+            for (int r = 0; r < c; r += PF_RB_WIDE) {
+                const int n = min(PF_RB_WIDE, c - r);
+                if (n > PF_RB) {
+                    entry(off[e] + r, n, 0);
+                    entry(off[e] + r, n, 1);
+                } else {
+                    entry(off[e] + r, n, -1);
+                }
+            }
         }
     }
     if (tid == 0) {

@@ -1,6 +1,7 @@
 """GPU parity of the routed-MoE prefill path (grouped GEMMs, exl3_moe_prefill)
 through the C ABI: against the oracle on small layers, with uniform and
-Zipf-skewed routing (experts with several 32-row tiles), invalid and duplicate
+Zipf-skewed routing (experts with several tiles, narrow and wide), wide tiles
+bitwise against narrow ones, invalid and duplicate
 ids, dtypes, a shared expert as an extra slot; against the decode kernel
 (itself checked against the oracle) at the full 256-expert shape, row by row.
 Tolerance: max-abs 2e-2, rel-L2 1e-3 against the oracle; decode vs prefill
@@ -78,6 +79,34 @@ def test_prefill_hot_expert_many_tiles(small):
     x = synth.activations(T, 512, seed=805)
     got = run_prefill(small, x, ids, w).cpu().numpy()
     assert_close(got, small.ref(x, ids, w), what="hot expert")
+
+
+def test_prefill_wide_tiles_bitwise_narrow(small):
+    """Experts with more than 32 rows run wide tiles (up to 64 rows, each
+    decoded step applied to four 16-row blocks, half of each tile's columns per
+    lane): expert 3 (3-bit) gets 300 rows (four full wide tiles and a 44-row
+    one), expert 5 (2-bit) 150 (two full ones and a 22-row narrow tile),
+    expert 7 (4-bit) about 40 (one partial wide tile).  The same tokens in
+    5-token calls give no expert more than 10 rows, so only narrow tiles run;
+    every output row is bitwise the same either way, and both meet the oracle
+    bar."""
+    import torch
+
+    T = 150
+    rng = np.random.default_rng(14)
+    others = np.array([0, 1, 2, 4, 6, 8, 9, 10, 11, 12, 13, 14, 15])
+    ids = np.zeros((T, 4), np.int32)
+    ids[:, 0], ids[:, 1], ids[:, 2] = 3, 5, 3
+    ids[:, 3] = np.where(np.arange(T) < 40, 7, others[rng.integers(0, len(others), T)])
+    w = rng.random((T, 4)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    x = synth.activations(T, 512, seed=815)
+    print("prefill wide tiles vs 5-token slices", flush=True)
+    whole = run_prefill(small, x, ids, w)
+    sliced = torch.cat([run_prefill(small, x[i:i + 5], ids[i:i + 5], w[i:i + 5]) for i in range(0, T, 5)])
+    torch.cuda.synchronize()
+    assert torch.equal(whole, sliced), "wide tiles changed a row's result"
+    assert_close(whole.cpu().numpy(), small.ref(x, ids, w), what="wide tiles")
 
 
 def test_prefill_invalid_ids_and_zero_rows(small):
