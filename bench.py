@@ -738,6 +738,54 @@ def time_row_blocks(dev, iters: int = 256, reps: int = 3) -> dict:
     return {"unit": "SIMD cycles", "iters": iters, **out}
 
 
+GEMM_STEPS = ("narrow_1_row_block", "narrow_2_row_blocks", "wide_4_row_blocks")
+
+
+def time_gemm_steps(dev, iters: int = 256, reps: int = 3) -> dict:
+    """The prefill GEMM's own step functions (csrc/exl3_probe.hip
+    probe_gemm_step_kernel: mma_tile2 with one or two row blocks, mma_tile_wide
+    with four) on register-resident tile and A words, single-wave workgroups,
+    two per SIMD.  Returns SIMD cycles per 64 decoded weights (one per lane)
+    and per 64 weight-rows, at 2 and 3 bits."""
+    import ctypes
+
+    import torch
+    from dsv4_carve_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_LIB)
+    lib.exl3_probe_gemm_step.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.exl3_probe_gemm_step.restype = ctypes.c_int
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    simds = 4 * cus
+    blocks = 2 * simds
+    g = torch.Generator().manual_seed(11)
+    words = torch.randint(0, 2 ** 31 - 1, (64 * 8 * 3,), generator=g, dtype=torch.int64).to(torch.int32).to(dev)
+    sink = torch.empty(blocks * 64, dtype=torch.float32, device=dev)
+    clk = torch.zeros(2 * blocks, dtype=torch.int64, device=dev)
+    stream = int(torch.cuda.current_stream(dev).cuda_stream)
+    out = {}
+    for bits in (2, 3):
+        for kind, (name, rows) in enumerate(zip(GEMM_STEPS, (16, 32, 64))):
+            times = []
+            for _ in range(reps + 1):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                assert lib.exl3_probe_gemm_step(bits, kind, blocks, iters, words.data_ptr(), sink.data_ptr(),
+                                                clk.data_ptr(), stream) == 0
+                b.record()
+                torch.cuda.synchronize()
+                times.append(a.elapsed_time(b) * 1e-3)
+            t = sorted(times[1:])[reps // 2]
+            c = clk[:2 * blocks].view(blocks, 2).double().sum(0).tolist()
+            ghz = c[0] / c[1] * 0.1
+            weights = blocks * iters * (8192.0 if rows == 64 else 16384.0)
+            cyc = t * ghz * 1e9 * simds / (weights / 64.0)
+            out[f"K{bits}_{name}"] = {"per_64_weights": round(cyc, 2), "per_64_weight_rows": round(cyc / rows, 3)}
+    del words, sink, clk
+    return {"unit": "SIMD cycles", "iters": iters, **out}
+
+
 ISA_OPS = ("v_and_b32", "v_xor_b32", "v_lshrrev_b32", "v_bitop3_b32", "v_mul_lo_u16", "v_add_u32",
            "v_bfe_u32", "v_alignbit_b32", "v_perm_b32", "v_mul_lo_u32", "v_lshlrev_b32", "v_add3_u32",
            "v_mad_u32_u16", "v_mad_u32_u16 op_sel hi", "v_pk_mad_u16", "v_pk_mul_lo_u16",
@@ -914,6 +962,8 @@ def main() -> int:
         print(f"[bench] instruction issue rates: {extra['isa_issue_rates']}", file=sys.stderr, flush=True)
         extra["row_block_rates"] = time_row_blocks(dev)
         print(f"[bench] row-block rates: {extra['row_block_rates']}", file=sys.stderr, flush=True)
+        extra["gemm_step_rates"] = time_gemm_steps(dev)
+        print(f"[bench] prefill step rates: {extra['gemm_step_rates']}", file=sys.stderr, flush=True)
     if "null" in legs:
         # The same workloads on the timing-only twin library (each decoded
         # weight replaced by a loaded tile word): the skeleton of loads, MFMAs,

@@ -382,6 +382,35 @@ __device__ __forceinline__ void fwht128_x2(float& v0, float& v1) {
     }
 }
 
+// Same transform for four independent 128-blocks, 8 consecutive elements per
+// lane: lanes 16 b .. 16 b + 15 hold block b (element 8 j + e in lane j of the
+// 16).  Stages h = 1, 2, 4 run in registers, h = 8 .. 64 between lanes by DPP
+// moves within each row of 16 lanes (no LDS traffic); every stage pairs the
+// same elements with the same operands as fwht128_x2, so the results are
+// bitwise the same.
+__device__ __forceinline__ void fwht128_x8(float (&v)[8]) {
+    const int c = threadIdx.x & 15;
+#pragma unroll
+    for (int h = 1; h < 8; h <<= 1)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int a = (q / h) * 2 * h + (q % h);
+            const float x0 = v[a], x1 = v[a + h];
+            v[a] = x0 + x1;
+            v[a + h] = x0 - x1;
+        }
+    const float s1 = (c & 1) ? -1.f : 1.f, s2 = (c & 2) ? -1.f : 1.f;
+    const float s4 = (c & 4) ? -1.f : 1.f, s8 = (c & 8) ? -1.f : 1.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bfly(v[e], dpp_xor<1>(v[e]), s1);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bfly(v[e], dpp_xor<2>(v[e]), s2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bfly(v[e], dpp_xor<4>(v[e]), s4);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bfly(v[e], dpp_xor<8>(v[e]), s8);
+}
+
 // Same transform for two independent 128-blocks, 4 consecutive elements per
 // lane: lanes 0-31 hold block 0, lanes 32-63 block 1 (element 4j+e of the block
 // in lane j of the half-wave).

@@ -131,12 +131,36 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
 
 // ---------------------------------------------------------------- 2. input rotation (one wave per pair and 512 columns, both projections)
 //
-// Every wave issues all of its loads before any arithmetic: one wave looping
-// over the 32 blocks of a 4096-wide row waited for each block's loads in
-// turn (50 us per layer at 512 tokens).  The pair's expert comes from the
-// plan (no route lookup), and one wave rotates the gate and the up input of
-// its columns, so the chain of dependent loads (pair -> scale pointers ->
-// x and scales) is paid once for both.
+// Each lane holds 8 consecutive columns (16-byte loads and stores): lanes
+// 16 b .. 16 b + 15 cover 128-block b, so the block's Hadamard runs in
+// registers and DPP moves (fwht128_x8).  The pair's expert comes from the plan
+// (no route lookup), and one wave rotates the gate and the up input of its
+// columns, so the chain of dependent loads (pair -> scale pointers -> x and
+// scales) is paid once for both.
+
+// half(x * s) of 8 packed inputs (fp16 or bf16 x, fp16 s), as fp32.
+__device__ __forceinline__ void pf_scaled8(const u32x4_t& xv, const u32x4_t& sv, int x_kind, float (&v)[8]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint16_t xb = (uint16_t)(h ? xv[i] >> 16 : xv[i] & 0xffffu);
+            const uint16_t x16 = x_kind != 0 ? f32_to_f16_bits(bf16_to_f32(xb)) : xb;
+            const uint16_t s16 = (uint16_t)(h ? sv[i] >> 16 : sv[i] & 0xffffu);
+            // the fp32 product of two halves is exact, so one RNE cast = half mul
+            v[2 * i + h] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(x16) * f16_bits_to_f32(s16)));
+        }
+    }
+}
+
+__device__ __forceinline__ u32x4_t pf_rotated8(float (&v)[8]) {
+    fwht128_x8(v);
+    u32x4_t o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)f32_to_f16_bits(v[2 * i] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(v[2 * i + 1] * HAD_NORM) << 16);
+    return o;
+}
 
 __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     const PfLayout& L = P.L;
@@ -146,31 +170,23 @@ __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     const int s = pat<int>(P.scratch, L.pair_slot)[p];
     const int e = pat<int>(P.scratch, L.pair_e)[p];
     const int tok = s / P.topk;
-    const int k0 = ch * 512, nblocks = min(HAD_MAX_BLOCKS, (P.H - k0) / 128);
-    const uint16_t* gsu = reinterpret_cast<const uint16_t*>(P.gsu[e]) + k0;
-    const uint16_t* usu = reinterpret_cast<const uint16_t*>(P.usu[e]) + k0;
-    RowIn g, u;
-    had_in_load(P.x, (size_t)tok * P.H + k0, gsu, nblocks, g);
-    {
-        const int lane = threadIdx.x & (WAVE - 1);
-        gptr_t<uint32_t> sp = as_global(reinterpret_cast<const uint32_t*>(usu) + lane);
-#pragma unroll
-        for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
-            if (b < nblocks) {
-                u.x[b] = g.x[b];
-                u.s[b] = sp[64 * b];
-            }
-    }
     const int lane = threadIdx.x;
+    // H is a multiple of 256: a lane whose 128-block is past H has no columns
+    const int col = ch * 512 + 8 * lane;
+    const bool live = col < P.H;
+    const int cl = live ? col : ch * 512;
+    const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(P.x) + (size_t)tok * P.H + cl);
+    const u32x4_t gs = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(P.gsu[e]) + cl);
+    const u32x4_t us = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(P.usu[e]) + cl);
+    float vg[8], vu[8];
+    pf_scaled8(xv, gs, P.x_kind, vg);
+    pf_scaled8(xv, us, P.x_kind, vu);
+    const u32x4_t og = pf_rotated8(vg), ou = pf_rotated8(vu);
     uint16_t* xh = pat<uint16_t>(P.scratch, L.Xh);
-    uint32_t* dg = reinterpret_cast<uint32_t*>(xh + (size_t)p * P.H + k0);
-    uint32_t* du = reinterpret_cast<uint32_t*>(xh + ((size_t)P.P + p) * P.H + k0);
-#pragma unroll
-    for (int b = 0; b < HAD_MAX_BLOCKS; ++b)
-        if (b < nblocks) {
-            dg[64 * b + lane] = had_in_pair(g.x[b], g.s[b], P.x_kind);
-            du[64 * b + lane] = had_in_pair(u.x[b], u.s[b], P.x_kind);
-        }
+    if (live) {
+        *reinterpret_cast<u32x4_t*>(xh + (size_t)p * P.H + col) = og;
+        *reinterpret_cast<u32x4_t*>(xh + ((size_t)P.P + p) * P.H + col) = ou;
+    }
 }
 
 // ---------------------------------------------------------------- 4. activation + down input rotation (one wave per pair and 256 columns)
@@ -328,6 +344,7 @@ static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, 
         !down_suh || !down_svh)
         return fail("null pointer table");
     if (x_kind != 0 && x_kind != 1) return fail("x must be fp16 or bf16");
+    if (reinterpret_cast<uintptr_t>(x) % 16) return fail("x must be 16-byte aligned (the input rotation reads 16-byte rows)");
     if (out_kind < OUT_F16 || out_kind > OUT_F32) return fail("out must be fp16, bf16 or fp32");
     const int64_t need = exl3_moe_prefill_scratch_bytes(tokens, hidden, intermediate, topk, n_experts);
     if (need < 0) return (int)need;

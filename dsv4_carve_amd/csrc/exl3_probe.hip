@@ -34,6 +34,7 @@
 #include <stdint.h>
 
 #include "exl3_gemv.hpp"
+#include "exl3_prefill.hpp"
 
 using exl3::u32x4_t;
 
@@ -284,6 +285,86 @@ static void probe_rows_dispatch(int cfg, int blocks, int iters, const uint32_t* 
     ((cfg == C ? launch_probe_rows<BITS, C>(blocks, iters, words, sink, clk, st) : void()), ...);
 }
 
+// Grouped-GEMM step probe: the prefill kernels' own step functions
+// (exl3_prefill.hpp mma_tile2 for a narrow tile of one or two 16-row blocks,
+// mma_tile_wide for a wide tile's four) on tile words and raw A words held in
+// registers and made opaque every iteration, so each iteration builds the A
+// operands, decodes every window the step decodes and issues its MFMAs, with
+// no memory traffic and no item overheads.  Rates are per decoded weight.
+enum ProbeGemmStep : int { STEP_NARROW_1 = 0, STEP_NARROW_2 = 1, STEP_WIDE_4 = 2, STEP_KINDS = 3 };
+
+template <int BITS, int KIND>
+__global__ __launch_bounds__(64, 2) void probe_gemm_step_kernel(const uint32_t* __restrict__ words, int iters,
+                                                               float* __restrict__ sink,
+                                                               uint64_t* __restrict__ clk) {
+    using namespace exl3;
+    using namespace exl3::prefill;
+    const int lane = threadIdx.x;
+    uint32_t W[8 * BITS];
+#pragma unroll
+    for (int i = 0; i < 8 * BITS; ++i) W[i] = words[lane * 8 * BITS + i];
+    constexpr int RB = KIND == STEP_WIDE_4 ? 4 : 2;
+    u32x4_t a[RB][2];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) a[rb][h][j] = 0x3c003c00u ^ (uint32_t)(lane + 7 * rb + 3 * h + j);
+    constexpr int NC = KIND == STEP_WIDE_4 ? 8 : 16;
+    float4_t acc[RB][NC];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < NC; ++i) acc[rb][i] = float4_t{0.f, 0.f, 0.f, 0.f};
+    const uint64_t c0 = __builtin_amdgcn_s_memtime(), t0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 8 * BITS; ++i) asm volatile("" : "+v"(W[i]));
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) asm volatile("" : "+v"(a[rb][0]), "+v"(a[rb][1]));
+        if constexpr (KIND == STEP_WIDE_4) {
+            mma_tile_wide<BITS, CB_MCG>(W, a, acc);
+        } else {
+            const u32x4_t(&a2)[2][2] = reinterpret_cast<const u32x4_t(&)[2][2]>(a);
+            float4_t(&acc2)[2][16] = reinterpret_cast<float4_t(&)[2][16]>(acc);
+            mma_tile2<BITS, CB_MCG, KIND == STEP_NARROW_2>(W, a2, acc2);
+        }
+    }
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), t1 = __builtin_amdgcn_s_memrealtime();
+    float sum = 0.f;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+        for (int i = 0; i < NC; ++i) sum += acc[rb][i][0] + acc[rb][i][1] + acc[rb][i][2] + acc[rb][i][3];
+    sink[blockIdx.x * 64 + lane] = sum;
+    if (lane == 0) {
+        clk[2 * blockIdx.x] = c1 - c0;
+        clk[2 * blockIdx.x + 1] = t1 - t0;
+    }
+}
+
+template <int BITS>
+static int launch_probe_gemm_step(int kind, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                                  hipStream_t st) {
+    switch (kind) {
+        case STEP_NARROW_1:
+            hipLaunchKernelGGL((probe_gemm_step_kernel<BITS, STEP_NARROW_1>), dim3(blocks), dim3(64), 0, st, words,
+                               iters, sink, clk);
+            break;
+        case STEP_NARROW_2:
+            hipLaunchKernelGGL((probe_gemm_step_kernel<BITS, STEP_NARROW_2>), dim3(blocks), dim3(64), 0, st, words,
+                               iters, sink, clk);
+            break;
+        case STEP_WIDE_4:
+            hipLaunchKernelGGL((probe_gemm_step_kernel<BITS, STEP_WIDE_4>), dim3(blocks), dim3(64), 0, st, words,
+                               iters, sink, clk);
+            break;
+        default: return -1;
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // The instruction kinds of the issue-rate probe (exl3_probe_isa's `op`).
 enum ProbeIsaOp : int {
     ISA_AND = 0, ISA_XOR, ISA_LSHRREV, ISA_BITOP3, ISA_MUL_LO_U16, ISA_ADD_U32,
@@ -501,6 +582,20 @@ int exl3_probe_rows(int bits, int cfg, int blocks, int iters, const uint32_t* wo
     else
         return -1;
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Launches `blocks` single-wave workgroups of the grouped-GEMM step probe at
+// `bits` (2 or 3; MCG) for step `kind` (0 narrow tile, one row block; 1 narrow
+// tile, two; 2 wide tile, four), each iteration one step (16384 decoded
+// weights narrow, 8192 wide); buffers and clocks as exl3_probe_decode_mode.
+// Returns 0, or -1 on a bad argument or launch error.
+int exl3_probe_gemm_step(int bits, int kind, int blocks, int iters, const uint32_t* words, float* sink,
+                         uint64_t* clk, void* stream) {
+    if (!words || !sink || !clk || blocks < 1 || iters < 1) return -1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (bits == 2) return launch_probe_gemm_step<2>(kind, blocks, iters, words, sink, clk, st);
+    if (bits == 3) return launch_probe_gemm_step<3>(kind, blocks, iters, words, sink, clk, st);
+    return -1;
 }
 
 // The decode kernels' loop (mode 0) at `bits`.
