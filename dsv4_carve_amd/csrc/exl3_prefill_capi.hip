@@ -189,54 +189,63 @@ __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     }
 }
 
-// ---------------------------------------------------------------- 4. activation + down input rotation (one wave per pair and 256 columns)
+// ---------------------------------------------------------------- 4. activation + down input rotation (one wave per pair and 512 columns)
+//
+// Lane l holds 8 consecutive columns, lanes 16 b .. 16 b + 15 one 128-block of
+// the down input (fwht128_x8), as in the input rotation.
 
 __global__ __launch_bounds__(64) void pf_act_kernel(PfParams P) {
     const PfLayout& L = P.L;
-    const int ncb = P.I / COLS;
-    const int p = blockIdx.x / ncb, c0 = (blockIdx.x - p * ncb) * COLS;
+    const int nch = (P.I + 511) / 512;
+    const int p = blockIdx.x / nch, ch = blockIdx.x - p * nch;
     if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
     const int lane = threadIdx.x;
     const int e = pat<int>(P.scratch, L.pair_e)[p];
-    const int col = c0 + 128 * (lane >> 5) + 4 * (lane & 31);
-    const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I + col;
-    const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I + col;
+    // I is a multiple of 256: a lane whose 128-block is past I has no columns
+    const int col = ch * 512 + 8 * lane;
+    const bool live = col < P.I;
+    const int cl = live ? col : ch * 512;
+    const float* G = pat<float>(P.scratch, L.GU) + (size_t)p * P.I + cl;
+    const float* U = pat<float>(P.scratch, L.GU) + ((size_t)P.P + p) * P.I + cl;
     const size_t kstride = (size_t)2 * P.P * P.I;     // between k-parts
-    uint16_t dsu[4];
-    {
-        const uint2 d = *reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(P.dsu[e]) + col);
-        dsu[0] = (uint16_t)d.x; dsu[1] = (uint16_t)(d.x >> 16); dsu[2] = (uint16_t)d.y; dsu[3] = (uint16_t)(d.y >> 16);
-    }
+    const u32x4_t ds = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(P.dsu[e]) + cl);
     // every k-part's loads first, then the sums in k-part order
-    float4_t gp[4], up[4];
+    float4_t gp[2][2], up[2][2];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < 2; ++ks)
         if (ks < L.ks_up) {
-            gp[ks] = *reinterpret_cast<const float4_t*>(G + ks * kstride);
-            up[ks] = *reinterpret_cast<const float4_t*>(U + ks * kstride);
-        }
-    float4_t g4 = gp[0], u4 = up[0];
 #pragma unroll
-    for (int ks = 1; ks < 4; ++ks)
-        if (ks < L.ks_up) {
-            g4 += gp[ks];
-            u4 += up[ks];
+            for (int h = 0; h < 2; ++h) {
+                gp[ks][h] = *reinterpret_cast<const float4_t*>(G + ks * kstride + 4 * h);
+                up[ks][h] = *reinterpret_cast<const float4_t*>(U + ks * kstride + 4 * h);
+            }
         }
-    float dv[4];
+    float dv[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        float gg = g4[i], uu = u4[i];
-        if (gg > P.limit) gg = P.limit;
-        if (uu < -P.limit) uu = -P.limit;
-        if (uu > P.limit) uu = P.limit;
-        const uint16_t act = f32_to_f16_bits((gg / (1.0f + expf(-gg))) * uu);
-        dv[i] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(dsu[i])));
+    for (int h = 0; h < 2; ++h) {
+        float4_t g4 = gp[0][h], u4 = up[0][h];
+        if (L.ks_up > 1) {
+            g4 += gp[1][h];
+            u4 += up[1][h];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float gg = g4[i], uu = u4[i];
+            if (gg > P.limit) gg = P.limit;
+            if (uu < -P.limit) uu = -P.limit;
+            if (uu > P.limit) uu = P.limit;
+            const uint16_t act = f32_to_f16_bits((gg / (1.0f + expf(-gg))) * uu);
+            const int j = 4 * h + i;
+            const uint16_t s16 = (uint16_t)((j & 1) ? ds[j >> 1] >> 16 : ds[j >> 1] & 0xffffu);
+            dv[j] = f16_bits_to_f32(f32_to_f16_bits(f16_bits_to_f32(act) * f16_bits_to_f32(s16)));
+        }
     }
-    fwht128_x4(dv);
-    uint2 packed;
-    packed.x = (uint32_t)f32_to_f16_bits(dv[0] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[1] * HAD_NORM) << 16);
-    packed.y = (uint32_t)f32_to_f16_bits(dv[2] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[3] * HAD_NORM) << 16);
-    *reinterpret_cast<uint2*>(pat<uint16_t>(P.scratch, L.AD) + (size_t)p * P.I + col) = packed;
+    fwht128_x8(dv);
+    u32x4_t packed;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        packed[i] = (uint32_t)f32_to_f16_bits(dv[2 * i] * HAD_NORM) | ((uint32_t)f32_to_f16_bits(dv[2 * i + 1] * HAD_NORM) << 16);
+    if (live) *reinterpret_cast<u32x4_t*>(pat<uint16_t>(P.scratch, L.AD) + (size_t)p * P.I + col) = packed;
 }
 
 // ---------------------------------------------------------------- 6. gather (one wave per token and 256-column block)
@@ -382,7 +391,7 @@ static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, 
     if ((rc = launch_widths(P, mask, codebook, false,
                             (int)pf_gemm_grid(tiles, 2 * P.L.ks_up, (int)(intermediate / COLS)), s)))
         return rc;
-    hipLaunchKernelGGL(pf_act_kernel, dim3(P.P * (intermediate / COLS)), dim3(WAVE), 0, s, P);
+    hipLaunchKernelGGL(pf_act_kernel, dim3(P.P * ((intermediate + 511) / 512)), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
     if ((rc = launch_widths(P, mask, codebook, true, (int)pf_gemm_grid(tiles, P.L.ks_down, (int)(hidden / COLS)), s)))
         return rc;

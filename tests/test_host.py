@@ -138,6 +138,12 @@ def test_moe_routed_argument_errors_without_device(entry, kw, msg):
     assert msg in _err()
 
 
+def test_prefill_input_alignment_without_device():
+    """The prefill path reads 16-byte pieces of the input rows."""
+    assert _routed_call("exl3_moe_prefill_routed", x=ctypes.c_void_p(18)) == -1
+    assert "16-byte aligned" in _err()
+
+
 @pytest.mark.parametrize("k,n,cb,kind,msg", [
     (100, 256, 1, 2, "k must be a positive multiple of 128"),
     (256, 100, 1, 2, "n must be a positive multiple of 128"),
