@@ -738,14 +738,15 @@ def time_row_blocks(dev, iters: int = 256, reps: int = 3) -> dict:
     return {"unit": "SIMD cycles", "iters": iters, **out}
 
 
-GEMM_STEPS = ("narrow_1_row_block", "narrow_2_row_blocks", "wide_4_row_blocks")
+GEMM_STEPS = ("narrow_1_row_block", "narrow_2_row_blocks", "wide_4_row_blocks", "wide_4_row_blocks_addends_summed")
 
 
 def time_gemm_steps(dev, iters: int = 256, reps: int = 3) -> dict:
     """The prefill GEMM's own step functions (csrc/exl3_probe.hip
     probe_gemm_step_kernel: mma_tile2 with one or two row blocks, mma_tile_wide
-    with four) on register-resident tile and A words, single-wave workgroups,
-    two per SIMD.  Returns SIMD cycles per 64 decoded weights (one per lane)
+    with four, and a wide step with each weight's addends summed on the VALU
+    so half the MFMAs run) on register-resident tile and A words, single-wave
+    workgroups, two per SIMD.  Returns SIMD cycles per 64 decoded weights (one per lane)
     and per 64 weight-rows, at 2 and 3 bits."""
     import ctypes
 
@@ -766,7 +767,7 @@ def time_gemm_steps(dev, iters: int = 256, reps: int = 3) -> dict:
     stream = int(torch.cuda.current_stream(dev).cuda_stream)
     out = {}
     for bits in (2, 3):
-        for kind, (name, rows) in enumerate(zip(GEMM_STEPS, (16, 32, 64))):
+        for kind, (name, rows) in enumerate(zip(GEMM_STEPS, (16, 32, 64, 64))):
             times = []
             for _ in range(reps + 1):
                 a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

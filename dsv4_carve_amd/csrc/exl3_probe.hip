@@ -291,7 +291,52 @@ static void probe_rows_dispatch(int cfg, int blocks, int iters, const uint32_t* 
 // registers and made opaque every iteration, so each iteration builds the A
 // operands, decodes every window the step decodes and issues its MFMAs, with
 // no memory traffic and no item overheads.  Rates are per decoded weight.
-enum ProbeGemmStep : int { STEP_NARROW_1 = 0, STEP_NARROW_2 = 1, STEP_WIDE_4 = 2, STEP_KINDS = 3 };
+enum ProbeGemmStep : int { STEP_NARROW_1 = 0, STEP_NARROW_2 = 1, STEP_WIDE_4 = 2, STEP_WIDE_4_SUMMED = 3, STEP_KINDS = 4 };
+
+// A wide step with each weight's two addends summed on the VALU (two byte
+// permutes gather the low and the high addends of two weights, one packed f16
+// add sums them), so an MFMA takes eight weights per lane: half the MFMAs,
+// and the A operand of two k-groups is the lane's raw activation words (no
+// duplication, no permutes).  Timing only: it rounds each weight to fp16 as
+// the dequantized weight is, where the kernels' duplicated-A MFMA sums the
+// addends exactly.
+template <int BITS>
+__device__ __forceinline__ void mma_tile_wide_summed(const uint32_t* W, const exl3::u32x4_t (&a)[4][2],
+                                                     exl3::float4_t (&acc)[4][8]) {
+    using namespace exl3;
+    typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+    static_for<2>([&](auto RI) {
+        constexpr int r2 = decltype(RI)::value;          // k-groups 2 r2, 2 r2 + 1
+        __builtin_amdgcn_sched_barrier(0);
+        half8_t Ar[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            u32x4_t w;
+            w[0] = a[rb][0][2 * r2]; w[1] = a[rb][1][2 * r2];
+            w[2] = a[rb][0][2 * r2 + 1]; w[3] = a[rb][1][2 * r2 + 1];
+            Ar[rb] = __builtin_bit_cast(half8_t, w);
+        }
+        static_for<8>([&](auto II) {
+            constexpr int i = decltype(II)::value;
+            constexpr int n = 2 * (i >> 1) + 8 * (i & 1), m = n / 2;
+            u32x4_t b;
+            static_for<4>([&](auto JI) {
+                constexpr int j = decltype(JI)::value;
+                constexpr int r = 2 * r2 + j / 2, q0 = 2 * (j & 1);
+                constexpr int T0 = 32 * (n & 7) + 8 * r + 4 * (n >> 3) + q0;
+                const uint32_t xa = decode_pair<BITS, CB_MCG, T0>(W);
+                const uint32_t xb = decode_pair<BITS, CB_MCG, T0 + 1>(W);
+                const h2_t lo = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(xb, xa, 0x01000504u));
+                const h2_t hi = __builtin_bit_cast(h2_t, __builtin_amdgcn_perm(xb, xa, 0x03020706u));
+                b[j] = __builtin_bit_cast(uint32_t, lo + hi);
+            });
+            const half8_t B = __builtin_bit_cast(half8_t, b);
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+                acc[rb][m] = __builtin_amdgcn_mfma_f32_16x16x32_f16(Ar[rb], B, acc[rb][m], 0, 0, 0);
+        });
+    });
+}
 
 template <int BITS, int KIND>
 __global__ __launch_bounds__(64, 2) void probe_gemm_step_kernel(const uint32_t* __restrict__ words, int iters,
@@ -303,7 +348,8 @@ __global__ __launch_bounds__(64, 2) void probe_gemm_step_kernel(const uint32_t* 
     uint32_t W[8 * BITS];
 #pragma unroll
     for (int i = 0; i < 8 * BITS; ++i) W[i] = words[lane * 8 * BITS + i];
-    constexpr int RB = KIND == STEP_WIDE_4 ? 4 : 2;
+    constexpr bool WIDE = KIND == STEP_WIDE_4 || KIND == STEP_WIDE_4_SUMMED;
+    constexpr int RB = WIDE ? 4 : 2;
     u32x4_t a[RB][2];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
@@ -311,7 +357,7 @@ __global__ __launch_bounds__(64, 2) void probe_gemm_step_kernel(const uint32_t* 
         for (int h = 0; h < 2; ++h)
 #pragma unroll
             for (int j = 0; j < 4; ++j) a[rb][h][j] = 0x3c003c00u ^ (uint32_t)(lane + 7 * rb + 3 * h + j);
-    constexpr int NC = KIND == STEP_WIDE_4 ? 8 : 16;
+    constexpr int NC = WIDE ? 8 : 16;
     float4_t acc[RB][NC];
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
@@ -325,6 +371,8 @@ __global__ __launch_bounds__(64, 2) void probe_gemm_step_kernel(const uint32_t* 
         for (int rb = 0; rb < RB; ++rb) asm volatile("" : "+v"(a[rb][0]), "+v"(a[rb][1]));
         if constexpr (KIND == STEP_WIDE_4) {
             mma_tile_wide<BITS, CB_MCG>(W, a, acc);
+        } else if constexpr (KIND == STEP_WIDE_4_SUMMED) {
+            mma_tile_wide_summed<BITS>(W, a, acc);
         } else {
             const u32x4_t(&a2)[2][2] = reinterpret_cast<const u32x4_t(&)[2][2]>(a);
             float4_t(&acc2)[2][16] = reinterpret_cast<float4_t(&)[2][16]>(acc);
@@ -359,6 +407,10 @@ static int launch_probe_gemm_step(int kind, int blocks, int iters, const uint32_
         case STEP_WIDE_4:
             hipLaunchKernelGGL((probe_gemm_step_kernel<BITS, STEP_WIDE_4>), dim3(blocks), dim3(64), 0, st, words,
                                iters, sink, clk);
+            break;
+        case STEP_WIDE_4_SUMMED:
+            hipLaunchKernelGGL((probe_gemm_step_kernel<BITS, STEP_WIDE_4_SUMMED>), dim3(blocks), dim3(64), 0, st,
+                               words, iters, sink, clk);
             break;
         default: return -1;
     }
@@ -586,8 +638,9 @@ int exl3_probe_rows(int bits, int cfg, int blocks, int iters, const uint32_t* wo
 
 // Launches `blocks` single-wave workgroups of the grouped-GEMM step probe at
 // `bits` (2 or 3; MCG) for step `kind` (0 narrow tile, one row block; 1 narrow
-// tile, two; 2 wide tile, four), each iteration one step (16384 decoded
-// weights narrow, 8192 wide); buffers and clocks as exl3_probe_decode_mode.
+// tile, two; 2 wide tile, four; 3 wide tile with the addends summed on the
+// VALU), each iteration one step (16384 decoded weights narrow, 8192 wide);
+// buffers and clocks as exl3_probe_decode_mode.
 // Returns 0, or -1 on a bad argument or launch error.
 int exl3_probe_gemm_step(int bits, int kind, int blocks, int iters, const uint32_t* words, float* sink,
                          uint64_t* clk, void* stream) {
