@@ -421,10 +421,12 @@ def time_linear(dev, k, n, bits, rows_list, steps=20):
 MFMA_PEAK_F16 = 2.5e15
 
 
-def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True, lib=None):
+def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True, lib=None, hot8=False):
     """Prefill-shaped layer (grouped GEMMs): us per layer over `tokens` tokens
     with Zipf(1.1) top-k routing (`zipf`; otherwise the decode benchmark's
-    N(0,1)-logit routing), fresh routing each step from a pool of 4.
+    N(0,1)-logit routing), fresh routing each step from a pool of 4.  `hot8`:
+    every token on the same 8 experts (8i .. 8i + 7 for pool entry i, all
+    3-bit here), so every expert runs wide tiles only.
     Returns (us, algorithmic flops, algorithmic bytes, mean distinct experts).
     `lib`: call that library's C ABI instead of the ops (the null-decode twin)."""
     import torch
@@ -433,6 +435,8 @@ def time_prefill(layer, dev, tokens, topk, steps, warmup, seed, zipf=True, lib=N
     n_exp = len(layer.bits)
     route = synth.zipf_routing if zipf else synth.routing
     pool = [route(tokens, n_exp, topk, seed=seed + i) for i in range(4)]
+    if hot8:
+        pool = [(np.tile(np.arange(topk, dtype=p[0].dtype) + 8 * i, (tokens, 1)), p[1]) for i, p in enumerate(pool)]
     ids = [torch.from_numpy(p[0]).to(dev) for p in pool]
     wts = [torch.from_numpy(p[1]).to(dev) for p in pool]
     x = torch.from_numpy(synth.activations(tokens, layer.hidden, seed=seed)).to(dev)
@@ -918,6 +922,8 @@ def main() -> int:
                     help="dense leg: comma-separated KxN shapes")
     ap.add_argument("--dense-bits", default=",".join(str(b) for b in DENSE_BITS), help="dense leg: bit widths")
     ap.add_argument("--dense-rows", default=",".join(str(r) for r in DENSE_ROWS), help="dense leg: row counts")
+    ap.add_argument("--prefill-routing", default="zipf,hot8",
+                    help="prefill leg: zipf (Zipf(1.1) over 256 experts), hot8 (every token on 8 experts), or both")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="end with one device-to-device copy of this many MiB (HBM counter calibration)")
     a = ap.parse_args()
@@ -1028,7 +1034,15 @@ def main() -> int:
             torch.cuda.empty_cache()
         extra["tp8_slice_h4096_i256_top6"] = tp
 
-    if "prefill" in legs:
+    if "prefill" in legs and "hot8" in a.prefill_routing:
+        ush, flh, _, _ = time_prefill(layer, dev, 512, TOPK, 10, 2, seed=4242, hot8=True)
+        extra["prefill_512_tokens_hot8"] = {"us_per_layer": round(ush, 1), "tokens_per_s": round(512 / (ush * 1e-6), 0),
+                                            "tflops": round(flh / (ush * 1e-6) / 1e12, 2),
+                                            "mfma_frac_fp16": round(flh / (ush * 1e-6) / MFMA_PEAK_F16, 4),
+                                            "decoded_gweights": round(8 * 8 * 3.0 * HIDDEN * INTER / 1e9, 2)}
+        print(f"[bench] prefill 512 tokens, 8 hot experts: {extra['prefill_512_tokens_hot8']}", file=sys.stderr,
+              flush=True)
+    if "prefill" in legs and "zipf" in a.prefill_routing:
         usp, fl, bp, dist = time_prefill(layer, dev, 512, TOPK, 10, 2, seed=4242)
         extra["prefill_512_tokens_zipf1.1"] = {
             "us_per_layer": round(usp, 1), "tokens_per_s": round(512 / (usp * 1e-6), 0),
