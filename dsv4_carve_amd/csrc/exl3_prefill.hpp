@@ -63,12 +63,16 @@ __host__ __device__ inline int pf_tile_entries(int c) {
 }
 
 // k-splits of the gate/up (K = hidden) and down (K = intermediate) GEMMs: as
-// many as keep an even number of 64-row steps per part, up to 2 each (on the
-// 512-token layer 2/2 measured faster than 4/2, 1/2 and 2/1: fewer parts halve
-// the partials the activation reads, more parts shorten the launches' last
-// round).  Each part writes its own fp32 output (the output Hadamard and svh
-// are linear, so they apply per part); the activation and gather kernels add
-// the parts in order, so results do not depend on scheduling.
+// many as keep an even number of 64-row steps per part, up to the cap.  More
+// parts give more, shorter items, so a launch's last round leaves less of the
+// GPU idle; fewer parts halve the partials written and read again.  With many
+// (token, slot) pairs the launches run several rounds anyway, so the caps drop
+// to 1 there: the down GEMM from 4096 pairs, the gate/up GEMM (twice the items
+// per tile) from 8192.  Each part writes its own fp32 output (the output
+// Hadamard and svh are linear, so they apply per part); the activation and
+// gather kernels add the parts in order, so results do not depend on
+// scheduling (they do depend on the pair count through the split).
+constexpr int64_t PF_KS_DOWN_ONE_PAIRS = 4096, PF_KS_UP_ONE_PAIRS = 8192;
 inline int pf_ksplit(int64_t K, int cap) {
     int ks = cap;
     while (ks > 1 && K % (2 * STEP_K * ks)) ks /= 2;
@@ -77,8 +81,8 @@ inline int pf_ksplit(int64_t K, int cap) {
 
 inline PfLayout pf_layout(int64_t pairs, int64_t H, int64_t I, int64_t E) {
     PfLayout L;
-    L.ks_up = pf_ksplit(H, 2);
-    L.ks_down = pf_ksplit(I, 2);
+    L.ks_up = pf_ksplit(H, pairs >= PF_KS_UP_ONE_PAIRS ? 1 : 2);
+    L.ks_down = pf_ksplit(I, pairs >= PF_KS_DOWN_ONE_PAIRS ? 1 : 2);
     // An expert with c rows has at most ceil(c / PF_RB) tile entries (a wide
     // tile is two entries, one per half of the column blocks).
     L.max_tiles = E + (pairs + PF_RB - 1) / PF_RB;

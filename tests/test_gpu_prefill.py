@@ -109,6 +109,18 @@ def test_prefill_wide_tiles_bitwise_narrow(small):
     assert_close(whole.cpu().numpy(), small.ref(x, ids, w), what="wide tiles")
 
 
+@pytest.mark.parametrize("tokens", [700, 1400])
+def test_prefill_k_split_by_pair_count(small, tokens):
+    """The GEMMs split K in two parts below 4096 (down) and 8192 (gate/up)
+    (token, slot) pairs and run it whole above: 700 tokens x top-6 (4200 pairs)
+    splits only the gate/up GEMM, 1400 tokens (8400 pairs) neither."""
+    print(f"prefill k-split tokens={tokens}", flush=True)
+    ids, w = synth.zipf_routing(tokens, 16, 6, seed=850 + tokens)
+    x = synth.activations(tokens, 512, seed=851 + tokens)
+    got = run_prefill(small, x, ids, w).cpu().numpy()
+    assert_close(got, small.ref(x, ids, w), what=f"prefill T={tokens}")
+
+
 def test_prefill_invalid_ids_and_zero_rows(small):
     T = 33
     rng = np.random.default_rng(6)
