@@ -216,27 +216,29 @@ __device__ __forceinline__ void pf_tile(bool valid, const uint16_t* A, int row0,
 
     // nsteps (64 k-rows each, from k0) is even
     TileRegs<BITS> t0, t1;
-    u32x4_t ac[2][2];
-    // Each step's A loads are issued before the next step's tile loads: the
-    // wait for A (needed at once) then leaves the tile prefetch in flight
-    // (loads complete in issue order, so A issued after it would wait for it).
     // A tile of at most 16 rows (most tiles under skewed routing) runs a loop
     // without row block 1's A loads and MFMAs; its rows are the same.
     auto steps = [&](auto two) {
         constexpr bool TWO = decltype(two)::value;
-        auto load_a = [&](int s) {
+        // A and the tile of step s + 1 are both requested before step s's
+        // MFMAs: the wait for step s's operands (loads complete in issue
+        // order) leaves both prefetches in flight.
+        u32x4_t ac0[2][2], ac1[2][2];
+        auto load_a = [&](u32x4_t (&ac)[2][2], int s) {
             ac[0][0] = a0[s * astep]; ac[0][1] = a0[s * astep + 1];
             if constexpr (TWO) { ac[1][0] = a1[s * astep]; ac[1][1] = a1[s * astep + 1]; }
         };
         load_tile<BITS>(t0, tp);
+        load_a(ac0, 0);
         for (int s = 0; s < nsteps; s += 2) {
-            load_a(s);
             load_tile<BITS>(t1, tp + (s + 1) * tstep);
-            mma_tile2<BITS, CB, TWO>(t0.words(), ac, acc);
-            load_a(s + 1);
-            // the last iteration reloads its own step (a valid address, unused)
-            load_tile<BITS>(t0, tp + min(s + 2, nsteps - 1) * tstep);
-            mma_tile2<BITS, CB, TWO>(t1.words(), ac, acc);
+            load_a(ac1, s + 1);
+            mma_tile2<BITS, CB, TWO>(t0.words(), ac0, acc);
+            // the last iteration reloads its own step (valid addresses, unused)
+            const int sn = min(s + 2, nsteps - 1);
+            load_tile<BITS>(t0, tp + sn * tstep);
+            load_a(ac0, sn);
+            mma_tile2<BITS, CB, TWO>(t1.words(), ac1, acc);
         }
     };
     if (nrows > 16) steps(std::true_type{});

@@ -32,16 +32,30 @@ __device__ __forceinline__ void wave0_scan(int* v, int n, int* total) {
     if (lane == 0) *total = carry;
 }
 
-// Local expert of slot s, or -1.  An expert whose width is outside the
-// call's bits_mask (no GEMM launch covers it) is routed nowhere, so it
-// contributes nothing, and sets `bad`.
-__device__ __forceinline__ int pf_local(const PfParams& P, int s, int* bad) {
-    const int e = P.rt.local(s, P.E);
-    if (e >= 0 && P.ebits && !((P.mask >> (P.ebits[e] & 31)) & 1u)) {
-        *bad = 1;
-        return -1;
+// Local experts of PF_PLAN_N slots per thread (s0, s0 + nt, ...), -1 for
+// none.  An expert whose width is outside the call's bits_mask (no GEMM
+// launch covers it) is routed nowhere, so it contributes nothing, and sets
+// `bad`.  Every slot's id loads, then its map and width loads, are in flight
+// together, so a round pays one chain of dependent loads instead of one per
+// slot.
+constexpr int PF_PLAN_N = 8;
+
+__device__ __forceinline__ void pf_local_n(const PfParams& P, int s0, int nt, int (&e)[PF_PLAN_N], int* bad) {
+    int s[PF_PLAN_N];
+#pragma unroll
+    for (int i = 0; i < PF_PLAN_N; ++i) s[i] = s0 + i * nt;
+    P.rt.local_n(s, P.P, P.E, e);
+    if (P.ebits) {
+        int b[PF_PLAN_N];
+#pragma unroll
+        for (int i = 0; i < PF_PLAN_N; ++i) b[i] = P.ebits[e[i] >= 0 ? e[i] : 0];
+#pragma unroll
+        for (int i = 0; i < PF_PLAN_N; ++i)
+            if (e[i] >= 0 && !((P.mask >> (b[i] & 31)) & 1u)) {
+                *bad = 1;
+                e[i] = -1;
+            }
     }
-    return e;
 }
 
 __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
@@ -52,12 +66,19 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     __shared__ int bad;
     const PfLayout& L = P.L;
     const int tid = threadIdx.x, nt = blockDim.x;
+    const int round = nt * PF_PLAN_N;
+    // up to `round` pairs, each thread's experts stay in registers for the
+    // placement pass; beyond that the placement pass looks them up again
+    const bool one_round = P.P <= round;
+    int ev[PF_PLAN_N];
     for (int e = tid; e < P.E; e += nt) cnt[e] = 0;
     if (tid == 0) bad = 0;
     __syncthreads();
-    for (int s = tid; s < P.P; s += nt) {
-        const int e = pf_local(P, s, &bad);
-        if (e >= 0) atomicAdd(&cnt[e], 1);
+    for (int s0 = tid; s0 < P.P; s0 += round) {
+        pf_local_n(P, s0, nt, ev, &bad);
+#pragma unroll
+        for (int i = 0; i < PF_PLAN_N; ++i)
+            if (ev[i] >= 0) atomicAdd(&cnt[ev[i]], 1);
     }
     __syncthreads();
     for (int e = tid; e < P.E; e += nt) {
@@ -117,15 +138,20 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     int* pair_slot = pat<int>(P.scratch, L.pair_slot);
     int* pair_e = pat<int>(P.scratch, L.pair_e);
     int* pos = pat<int>(P.scratch, L.pos);
-    for (int s = tid; s < P.P; s += nt) {
-        const int e = pf_local(P, s, &bad);
-        int p = -1;
-        if (e >= 0) {
-            p = atomicAdd(&cnt[e], 1);
-            pair_slot[p] = s;
-            pair_e[p] = e;
+    for (int s0 = tid; s0 < P.P; s0 += round) {
+        if (!one_round) pf_local_n(P, s0, nt, ev, &bad);
+#pragma unroll
+        for (int i = 0; i < PF_PLAN_N; ++i) {
+            const int s = s0 + i * nt;
+            if (s >= P.P) break;
+            int p = -1;
+            if (ev[i] >= 0) {
+                p = atomicAdd(&cnt[ev[i]], 1);
+                pair_slot[p] = s;
+                pair_e[p] = ev[i];
+            }
+            pos[s] = p;
         }
-        pos[s] = p;
     }
 }
 
