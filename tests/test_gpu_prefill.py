@@ -68,6 +68,20 @@ def test_prefill_other_widths(dev, tokens):
     assert_close(got, layer.ref(x, ids, w), what=f"prefill widths 1/5/6/7/8 T={tokens}")
 
 
+@pytest.mark.parametrize("hidden", [1280, 2304])
+def test_prefill_hidden_past_whole_chunks(dev, hidden):
+    """A hidden size that is a multiple of 256 but not of 512: the input
+    rotation's last 512-column chunk is half full (1280: in the only group of
+    chunks; 2304: alone in the second group, whose other chunks lie past the
+    row)."""
+    print(f"prefill hidden={hidden}", flush=True)
+    layer = Layer(dev, 6, hidden, 256, [3, 2, 3, 2, 4, 3], seed=36)
+    ids, w = synth.zipf_routing(21, 6, 4, seed=840)
+    x = synth.activations(21, hidden, seed=841)
+    got = run_prefill(layer, x, ids, w).cpu().numpy()
+    assert_close(got, layer.ref(x, ids, w), what=f"prefill hidden {hidden}")
+
+
 def test_prefill_hot_expert_many_tiles(small):
     """Every token routes to expert 3 (4 tiles of 32 rows + a partial one) and
     to one other expert; duplicate ids within a row count twice."""
