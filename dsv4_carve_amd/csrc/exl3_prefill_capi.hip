@@ -155,15 +155,14 @@ __global__ __launch_bounds__(1024) void pf_plan_kernel(PfParams P) {
     }
 }
 
-// ---------------------------------------------------------------- 2. input rotation (one wave per pair and 2048 columns, both projections)
+// ---------------------------------------------------------------- 2. input rotation (one wave per pair and 512 columns, both projections)
 //
-// Each lane holds 8 consecutive columns of a 512-column chunk (16-byte loads
-// and stores): lanes 16 b .. 16 b + 15 cover 128-block b, so the block's
-// Hadamard runs in registers and DPP moves (fwht128_x8).  The pair's expert
-// comes from the plan (no route lookup), and one wave rotates the gate and
-// the up input of PF_ROT_CHUNKS chunks, every chunk's loads issued before any
-// arithmetic, so the chain of dependent loads (pair -> scale pointers -> x
-// and scales) is paid once for both projections and all its chunks.
+// Each lane holds 8 consecutive columns (16-byte loads and stores): lanes
+// 16 b .. 16 b + 15 cover 128-block b, so the block's Hadamard runs in
+// registers and DPP moves (fwht128_x8).  The pair's expert comes from the plan
+// (no route lookup), and one wave rotates the gate and the up input of its
+// columns, so the chain of dependent loads (pair -> scale pointers -> x and
+// scales) is paid once for both.
 
 // half(x * s) of 8 packed inputs (fp16 or bf16 x, fp16 s), as fp32.
 __device__ __forceinline__ void pf_scaled8(const u32x4_t& xv, const u32x4_t& sv, int x_kind, float (&v)[8]) {
@@ -189,52 +188,30 @@ __device__ __forceinline__ u32x4_t pf_rotated8(float (&v)[8]) {
     return o;
 }
 
-constexpr int PF_ROT_CHUNKS = 4;          // 512-column chunks per wave
-
-__host__ __device__ inline int pf_rot_groups(int H) { return ((H + 511) / 512 + PF_ROT_CHUNKS - 1) / PF_ROT_CHUNKS; }
-
 __global__ __launch_bounds__(64) void pf_rotate_kernel(PfParams P) {
     const PfLayout& L = P.L;
-    const int ng = pf_rot_groups(P.H);
-    const int p = blockIdx.x / ng, grp = blockIdx.x - p * ng;
-    // p < P.P, so the plan's entries for p are readable whether or not p is
-    // one of this call's pairs: all three loads go out together
-    const int pairs = pat<int>(P.scratch, L.meta)[PF_META_PAIRS];
+    const int nch = (P.H + 511) / 512;
+    const int p = blockIdx.x / nch, ch = blockIdx.x - p * nch;
+    if (p >= pat<int>(P.scratch, L.meta)[PF_META_PAIRS]) return;
     const int s = pat<int>(P.scratch, L.pair_slot)[p];
     const int e = pat<int>(P.scratch, L.pair_e)[p];
-    if (p >= pairs) return;
     const int tok = s / P.topk;
     const int lane = threadIdx.x;
-    const uint16_t* xr = reinterpret_cast<const uint16_t*>(P.x) + (size_t)tok * P.H;
-    const uint16_t* gsu = reinterpret_cast<const uint16_t*>(P.gsu[e]);
-    const uint16_t* usu = reinterpret_cast<const uint16_t*>(P.usu[e]);
     // H is a multiple of 256: a lane whose 128-block is past H has no columns
-    // (it reads column 0's values, valid memory, and stores nothing)
-    int col[PF_ROT_CHUNKS];
-    u32x4_t xv[PF_ROT_CHUNKS], gs[PF_ROT_CHUNKS], us[PF_ROT_CHUNKS];
-#pragma unroll
-    for (int c = 0; c < PF_ROT_CHUNKS; ++c) {
-        col[c] = (grp * PF_ROT_CHUNKS + c) * 512 + 8 * lane;
-        const int cl = col[c] < P.H ? col[c] : 0;
-        xv[c] = *reinterpret_cast<const u32x4_t*>(xr + cl);
-        gs[c] = *reinterpret_cast<const u32x4_t*>(gsu + cl);
-        us[c] = *reinterpret_cast<const u32x4_t*>(usu + cl);
-    }
-    uint16_t* xg = pat<uint16_t>(P.scratch, L.Xh) + (size_t)p * P.H;
-    uint16_t* xu = pat<uint16_t>(P.scratch, L.Xh) + ((size_t)P.P + p) * P.H;
-#pragma unroll
-    for (int c = 0; c < PF_ROT_CHUNKS; ++c) {
-        // a chunk past H is past it for the whole wave (H is a multiple of
-        // 256, chunks are 512 wide): no lane's DPP partner is missing
-        if ((grp * PF_ROT_CHUNKS + c) * 512 >= P.H) break;
-        float vg[8], vu[8];
-        pf_scaled8(xv[c], gs[c], P.x_kind, vg);
-        pf_scaled8(xv[c], us[c], P.x_kind, vu);
-        const u32x4_t og = pf_rotated8(vg), ou = pf_rotated8(vu);
-        if (col[c] < P.H) {
-            *reinterpret_cast<u32x4_t*>(xg + col[c]) = og;
-            *reinterpret_cast<u32x4_t*>(xu + col[c]) = ou;
-        }
+    const int col = ch * 512 + 8 * lane;
+    const bool live = col < P.H;
+    const int cl = live ? col : ch * 512;
+    const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(P.x) + (size_t)tok * P.H + cl);
+    const u32x4_t gs = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(P.gsu[e]) + cl);
+    const u32x4_t us = *reinterpret_cast<const u32x4_t*>(reinterpret_cast<const uint16_t*>(P.usu[e]) + cl);
+    float vg[8], vu[8];
+    pf_scaled8(xv, gs, P.x_kind, vg);
+    pf_scaled8(xv, us, P.x_kind, vu);
+    const u32x4_t og = pf_rotated8(vg), ou = pf_rotated8(vu);
+    uint16_t* xh = pat<uint16_t>(P.scratch, L.Xh);
+    if (live) {
+        *reinterpret_cast<u32x4_t*>(xh + (size_t)p * P.H + col) = og;
+        *reinterpret_cast<u32x4_t*>(xh + ((size_t)P.P + p) * P.H + col) = ou;
     }
 }
 
@@ -434,7 +411,7 @@ static int moe_prefill_impl(const void* x, int x_kind, void* out, int out_kind, 
     int rc;
     hipLaunchKernelGGL(pf_plan_kernel, dim3(1), dim3(1024), 0, s, P);
     if ((rc = check_launch())) return rc;
-    hipLaunchKernelGGL(pf_rotate_kernel, dim3(P.P * pf_rot_groups((int)hidden)), dim3(WAVE), 0, s, P);
+    hipLaunchKernelGGL(pf_rotate_kernel, dim3(P.P * ((hidden + 511) / 512)), dim3(WAVE), 0, s, P);
     if ((rc = check_launch())) return rc;
     const int64_t tiles = P.L.max_tiles;
     if ((rc = launch_widths(P, mask, codebook, false,

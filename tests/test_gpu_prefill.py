@@ -69,11 +69,11 @@ def test_prefill_other_widths(dev, tokens):
 
 
 @pytest.mark.parametrize("hidden", [1280, 2304])
-def test_prefill_hidden_past_whole_chunks(dev, hidden):
+def test_prefill_hidden_not_a_multiple_of_512(dev, hidden):
     """A hidden size that is a multiple of 256 but not of 512: the input
-    rotation's last 512-column chunk is half full (1280: in the only group of
-    chunks; 2304: alone in the second group, whose other chunks lie past the
-    row)."""
+    rotation's last 512-column wave is half full (its lanes past the row
+    store nothing), and the down GEMM has an odd number of 256-column
+    blocks."""
     print(f"prefill hidden={hidden}", flush=True)
     layer = Layer(dev, 6, hidden, 256, [3, 2, 3, 2, 4, 3], seed=36)
     ids, w = synth.zipf_routing(21, 6, 4, seed=840)
