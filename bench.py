@@ -688,9 +688,56 @@ def time_decode_ceiling(dev, iters: int = 512, reps: int = 5) -> dict:
             "full_agpr_acc": run(bits, 3, 2, iters // 4, 3)["simd_cycles_per_64_weights"],
             "full_agpr_acc_4_waves_per_simd": run(bits, 3, 4, iters // 4, 3)["simd_cycles_per_64_weights"],
             "addends_summed_half_mfmas": run(bits, 4, 2, iters // 4, 3)["simd_cycles_per_64_weights"]}
-    del words, sink, clk
+    # Wave roles (exl3_probe_roles): one workgroup per CU with two or three
+    # waves per SIMD, each running the whole loop, or some decoding only and
+    # others running only the MFMAs of the same work.  Cycles are per 64
+    # weights of complete work (decoded and multiplied); `mixed` is the share of
+    # SIMDs whose waves had both roles (read back from HW_ID).
+    lib.exl3_probe_roles.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    lib.exl3_probe_roles.restype = ctypes.c_int
+    rsink = torch.empty(cus * 768, dtype=torch.float32, device=dev)
+    rclk = torch.zeros(3 * 12 * cus, dtype=torch.int64, device=dev)
+    role_of = {1: [0, 0, 0, 0, 1, 1, 1, 1], 2: [0, 1, 0, 1, 0, 1, 0, 1], 3: [0] * 8 + [1] * 4}
+
+    def run_roles(bits, mode, n_iter, n_reps):
+        times = []
+        for _ in range(n_reps + 1):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            assert lib.exl3_probe_roles(bits, mode, cus, n_iter, words.data_ptr(), rsink.data_ptr(), rclk.data_ptr(),
+                                        stream) == 0
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) * 1e-3)
+        t = sorted(times[1:])[n_reps // 2]
+        nw = 12 if mode >= 3 else 8
+        c = rclk.view(cus, 12, 3)[:, :nw].double().cpu()
+        ghz = float(c[:, :, 0].sum() / c[:, :, 1].sum()) * 0.1
+        units = cus * {0: 8, 1: 4, 2: 4, 3: 8, 4: 12}[mode] * n_iter * 16384.0
+        out = {"simd_cycles_per_64_weights": round(t * ghz * 1e9 * simds / (units / 64.0), 2)}
+        if mode in role_of:
+            simd_of = c[:, :, 2].long().tolist()
+            mixed = total = 0
+            for wg in simd_of:
+                for sm in range(4):
+                    r = {role_of[mode][w] for w in range(nw) if wg[w] == sm}
+                    total += 1
+                    mixed += len(r) == 2
+            out["mixed"] = round(mixed / total, 3)
+        return out
+
+    roles = {}
+    for bits in (2, 3):
+        roles[f"K{bits}"] = {
+            "both_waves_whole_loop": run_roles(bits, 0, iters // 4, 3)["simd_cycles_per_64_weights"],
+            "waves_0_3_decode_4_7_mfma": run_roles(bits, 1, iters // 4, 3),
+            "even_waves_decode_odd_mfma": run_roles(bits, 2, iters // 4, 3),
+            "three_waves_whole_loop": run_roles(bits, 4, iters // 4, 3)["simd_cycles_per_64_weights"],
+            "two_decode_waves_one_mfma_wave": run_roles(bits, 3, iters // 4, 3)}
+    del words, sink, clk, rsink, rclk
     return {"workgroups": 2 * simds, "iters": iters, "codebook": "MCG", **res,
-            "split_simd_cycles_per_64_weights": split}
+            "split_simd_cycles_per_64_weights": split, "wave_roles_simd_cycles_per_64_weights": roles}
 
 
 ROWS_CFG = ((1, 1), (2, 1), (2, 2), (3, 2), (4, 2), (4, 4), (6, 4), (8, 4))

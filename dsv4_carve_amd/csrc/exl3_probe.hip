@@ -185,6 +185,63 @@ static int launch_probe_decode(int mode, int blocks, int iters, const uint32_t* 
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+// Wave-role probe: one workgroup per CU.  Modes 0-2 use eight waves (two per
+// SIMD), modes 3-4 twelve (three per SIMD).  mode 0: every wave runs the
+// decode loop (decode + MFMA); mode 1: waves 0-3 decode only and waves 4-7 run
+// the MFMAs only; mode 2: even waves decode only and odd waves run the MFMAs
+// only; mode 3: waves 0-7 decode only and waves 8-11 run the MFMAs of two
+// iterations per iteration (two decoding waves and one multiplying wave per
+// SIMD, the same work); mode 4: every one of the twelve waves runs the decode
+// loop.  Each wave also records the SIMD it ran on (HW_ID bits 5:4), so which
+// roles shared a SIMD is read back, not assumed.
+constexpr int PROBE_ROLES_MAX_WAVES = 12;
+
+template <int BITS>
+__global__ __launch_bounds__(64 * PROBE_ROLES_MAX_WAVES, 1) void probe_roles_kernel(
+    const uint32_t* __restrict__ words, int iters, int mode, float* __restrict__ sink, uint64_t* __restrict__ clk) {
+    using namespace exl3;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    uint32_t W[8 * BITS];
+#pragma unroll
+    for (int i = 0; i < 8 * BITS; ++i) W[i] = words[lane * 8 * BITS + i];
+    half8_t A[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) A[r][j] = (_Float16)((float)((lane + 3 * r + j) & 7) * 0.125f - 0.4375f);
+    float4_t acc[16];
+    zero_acc(acc);
+    const int role = (mode == 0 || mode == 4) ? PROBE_FULL
+                   : mode == 1 ? (w < 4 ? PROBE_DECODE_ONLY : PROBE_MFMA_ONLY)
+                   : mode == 2 ? ((w & 1) ? PROBE_MFMA_ONLY : PROBE_DECODE_ONLY)
+                               : (w < 8 ? PROBE_DECODE_ONLY : PROBE_MFMA_ONLY);
+    const int n_it = (mode == 3 && role == PROBE_MFMA_ONLY) ? 2 * iters : iters;
+    auto loop = [&](auto M) {
+        for (int it = 0; it < n_it; ++it) {
+#pragma unroll
+            for (int i = 0; i < 8 * BITS; ++i) asm volatile("" : "+v"(W[i]));
+            probe_tile<BITS, decltype(M)::value>(W, A, acc);
+        }
+    };
+    const uint64_t c0 = __builtin_amdgcn_s_memtime(), t0 = __builtin_amdgcn_s_memrealtime();
+    if (role == PROBE_FULL) loop(std::integral_constant<int, PROBE_FULL>{});
+    else if (role == PROBE_DECODE_ONLY) loop(std::integral_constant<int, PROBE_DECODE_ONLY>{});
+    else loop(std::integral_constant<int, PROBE_MFMA_ONLY>{});
+    const uint64_t c1 = __builtin_amdgcn_s_memtime(), t1 = __builtin_amdgcn_s_memrealtime();
+    // HW_ID (hardware register 4), all 32 bits: SIMD_ID is bits 5:4
+    const uint32_t hw = __builtin_amdgcn_s_getreg((31 << 11) | (0 << 6) | 4);
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sum += acc[i][0] + acc[i][1] + acc[i][2] + acc[i][3];
+    sink[blockIdx.x * 64 * PROBE_ROLES_MAX_WAVES + threadIdx.x] = sum;
+    if (lane == 0) {
+        const size_t o = 3 * ((size_t)blockIdx.x * PROBE_ROLES_MAX_WAVES + w);
+        clk[o] = c1 - c0;
+        clk[o + 1] = t1 - t0;
+        clk[o + 2] = (hw >> 4) & 3u;
+    }
+}
+
 // Row-block probe: the grouped GEMM's inner loop with each decoded B operand
 // applied to RB row blocks (16 rows each), the lane decoding the 16 / D
 // columns n = D m + p of its tile (D = 1: all 16).  A lane whose tile words are
@@ -601,6 +658,30 @@ int exl3_probe_decode_mode(int bits, int mode, int blocks, int iters, const uint
         case 6: return launch_probe_decode<6>(mode, blocks, iters, words, sink, clk, st);
         default: return -1;
     }
+}
+
+// Launches `blocks` workgroups of the wave-role probe at `bits` (2 or 3;
+// MCG) in `mode` (0-2: eight waves; 0 every wave decode + MFMA, 1 waves 0-3
+// decode only and 4-7 MFMA only, 2 even waves decode only and odd MFMA only;
+// 3-4: twelve waves; 3 waves 0-7 decode only and 8-11 the MFMAs of two
+// iterations per iteration, 4 every wave decode + MFMA), each wave covering
+// 16384 weights per iteration for `iters` iterations.  words as
+// exl3_probe_decode_mode; sink: blocks * 768 floats; clk: 3 * 12 * blocks
+// uint64, per wave slot (12 per workgroup; eight-wave modes leave the last four
+// unwritten) its loop's shader clock cycles, 100 MHz reference ticks and the
+// SIMD (0-3) it ran on.  Returns 0, or -1 on a bad argument or launch error.
+int exl3_probe_roles(int bits, int mode, int blocks, int iters, const uint32_t* words, float* sink, uint64_t* clk,
+                     void* stream) {
+    if (!words || !sink || !clk || blocks < 1 || iters < 1 || mode < 0 || mode > 4) return -1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const dim3 threads(mode >= 3 ? 64 * PROBE_ROLES_MAX_WAVES : 512);
+    if (bits == 2)
+        hipLaunchKernelGGL(probe_roles_kernel<2>, dim3(blocks), threads, 0, st, words, iters, mode, sink, clk);
+    else if (bits == 3)
+        hipLaunchKernelGGL(probe_roles_kernel<3>, dim3(blocks), threads, 0, st, words, iters, mode, sink, clk);
+    else
+        return -1;
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // Instruction issue-rate probe: `blocks` four-wave workgroups, each wave
