@@ -212,7 +212,9 @@ def test_apply_experts_large_batches_use_prefill(dev, experts, monkeypatch):
 def test_apply_experts_long_batches_run_in_token_slices(dev, experts, monkeypatch):
     """Batches past the prefill kernel's pair limit run in token slices (the
     reference's fat-chunk slicing); a row's result does not depend on which
-    slice it is in, so the output is bitwise the one-call output."""
+    slice it is in as long as the slices split K alike (here every call is
+    below 4096 (token, slot) pairs), so the output is bitwise the one-call
+    output."""
     import torch
     from dsv4_carve_amd import vllm_exl3 as V
 
