@@ -144,6 +144,23 @@ def test_prefill_input_alignment_without_device():
     assert "16-byte aligned" in _err()
 
 
+def test_prefill_scratch_drops_where_k_stops_splitting():
+    """The prefill GEMMs split K in two below 4096 (down) and 8192 (gate/up)
+    (token, slot) pairs and keep it whole from there, so the scratch, which
+    holds one fp32 partial per part, shrinks as a call crosses each count
+    although the call grows (hidden 4096, intermediate 2048, top-8, 256
+    experts: 511 -> 512 tokens crosses 4096 pairs, 1023 -> 1024 crosses 8192).
+    Away from the two counts it grows with the tokens."""
+    lib = _lib.load()
+    size = lambda t: _lib.check(lib.exl3_moe_prefill_scratch_bytes(t, 4096, 2048, 8, 256))
+    # the second down part ([pairs][hidden] fp32) goes away at 4096 pairs
+    assert size(511) - size(512) > 0.9 * (511 * 8) * 4096 * 4
+    # the second gate/up part ([2][pairs][intermediate] fp32) at 8192
+    assert size(1023) - size(1024) > 0.9 * 2 * (1023 * 8) * 2048 * 4
+    for t in (100, 600, 2000):
+        assert size(t + 1) > size(t)
+
+
 @pytest.mark.parametrize("k,n,cb,kind,msg", [
     (100, 256, 1, 2, "k must be a positive multiple of 128"),
     (256, 100, 1, 2, "n must be a positive multiple of 128"),
