@@ -8,7 +8,8 @@
   block's output (RMS-normalised, fp16) feeding the second.
 * The prefill path on the 256-expert layer at 512 tokens with Zipf(1.1)
   routing, every token checked against the oracle (the hottest expert's rows
-  span many 32-row tiles).
+  span many 32-row tiles); and at 2048 tokens (both GEMMs keep K whole)
+  against the same tokens in four 512-token calls.
 
 Bars: max-abs 2e-2 and rel-L2 1e-3 on the raw outputs (no rescaling), and the
 kernels' error word must stay zero."""
@@ -144,4 +145,32 @@ def test_prefill_512_tokens_zipf(c2, dev):
     mae, rel = assert_close(got, ref, what="prefill 512 tokens")
     print(f"prefill 512: hot expert {hot} on {len(hot_rows)} tokens, {int((counts > 0).sum())} experts; "
           f"max-abs {mae:.3e} rel-L2 {rel:.3e}", flush=True)
+    _no_errors(dev)
+
+
+def test_prefill_2048_tokens_against_512_token_calls(c2, dev):
+    """2048 Zipf(1.1) tokens in one call (16384 pairs: both GEMMs keep K
+    whole, hot experts in many wide tiles) against the same tokens in four
+    512-token calls (4096 pairs each: the gate/up GEMM splits K in two; that
+    case is checked against the oracle above).  Only the split's fp32
+    reassociation differs, which can flip an fp16 rounding of the activation
+    by one ulp before the down projection: rel-L2 5e-4 per row, half the
+    oracle bar, as for prefill against decode."""
+    import torch
+    from tests.helpers import rel_l2
+    from tests.test_gpu_prefill import run_prefill
+
+    print("prefill 2048 tokens vs four 512-token calls", flush=True)
+    T = 2048
+    ids, w = synth.zipf_routing(T, E, 8, seed=42048)
+    x = synth.activations(T, H, seed=42048)
+    whole = run_prefill(c2, x, ids, w)
+    parts = torch.cat([run_prefill(c2, x[i:i + 512], ids[i:i + 512], w[i:i + 512]) for i in range(0, T, 512)])
+    torch.cuda.synchronize()
+    a, b = whole.cpu().numpy(), parts.cpu().numpy()
+    assert np.isfinite(a).all()
+    worst = max(rel_l2(a[r], b[r]) for r in range(T))
+    counts = np.bincount(ids.reshape(-1), minlength=E)
+    print(f"prefill 2048: hottest expert {int(counts.max())} rows; worst row rel-L2 {worst:.2e}", flush=True)
+    assert worst < 5e-4
     _no_errors(dev)
