@@ -532,6 +532,43 @@ def test_width_outside_mask_rejected_before_launch(small, dev):
         ops.moe_prefill(x, out, small.tables, ids, w, intermediate=256, expert_bits=small.ebits, bits_mask=bad_mask)
 
 
+@pytest.mark.parametrize("cb", [O.CB_3INST, O.CB_MUL1])
+def test_other_codebooks(dev, small, cb):
+    """The routed kernels with the 3INST and MUL1 codebooks (their instances
+    cover every width 1-8): both decode schedules at 5 and 16 rows, and the
+    prefill GEMMs with narrow and wide tiles (experts 3 and 5 take every one of
+    60 tokens), against the oracle evaluated with the same codebook."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    cache = {}
+    for m, profile in ((5, "zipf"), (16, "unique")):
+        ids, w = route_ids(m, profile), route_weights(m, "normal")
+        x = synth.activations(m, 512, seed=870 + m)
+        ref = O.moe(x, ids, w, small.experts, LIMIT, cb=cb, cache=cache)
+        for path in ("phased", "ticket"):
+            print(f"codebook {cb} decode {path} m={m}", flush=True)
+            out = torch.empty((m, 512), dtype=torch.float32, device=dev)
+            with moe_path(path):
+                ops.moe_decode(to_dev(x, dev), out, small.tables, to_dev(ids, dev), to_dev(w, dev), intermediate=256,
+                               expert_bits=small.ebits, bits_mask=small.mask, codebook=cb)
+            assert ops.moe_error(ops.SCRATCH.current(dev, "moe")) == 0
+            assert_close(out.cpu().numpy(), ref, what=f"codebook {cb} {path} m={m}")
+    T = 60
+    rng = np.random.default_rng(871)
+    ids = np.stack([np.array([3, 5, rng.integers(0, 16), rng.integers(0, 16)]) for _ in range(T)]).astype(np.int32)
+    w = rng.random((T, 4)).astype(np.float32)
+    w /= w.sum(axis=1, keepdims=True)
+    x = synth.activations(T, 512, seed=872)
+    print(f"codebook {cb} prefill T={T}", flush=True)
+    out = torch.empty((T, 512), dtype=torch.float32, device=dev)
+    ops.moe_prefill(to_dev(x, dev), out, small.tables, to_dev(ids, dev), to_dev(w, dev), intermediate=256,
+                    expert_bits=small.ebits, bits_mask=small.mask, codebook=cb)
+    assert ops.moe_error(ops.SCRATCH.current(dev, "moe_prefill")) == 0
+    assert_close(out.cpu().numpy(), O.moe(x, ids, w, small.experts, LIMIT, cb=cb, cache=cache),
+                 what=f"codebook {cb} prefill")
+
+
 @pytest.mark.parametrize("path", ["phased", "ticket", "prefill"])
 def test_unlisted_width_sets_error_word(dev, path):
     """Through the C ABI with the host check bypassed: experts of a width the
