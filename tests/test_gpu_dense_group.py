@@ -62,6 +62,29 @@ def test_mixed_fan_against_oracle_and_solo(dev, rows):
         assert rel_l2(got, solo) < 1e-5, f"member {j}: fan and solo call differ beyond fp32 reassociation"
 
 
+@pytest.mark.parametrize("cb", [O.CB_3INST, O.CB_MUL1])
+def test_fan_other_codebooks(dev, cb):
+    """The fan with the 3INST and MUL1 codebooks (mixed widths, 1 and 16 rows),
+    against the oracle with the same codebook and against each member's solo
+    call."""
+    import torch
+    from dsv4_carve_amd import ops
+
+    fan = Fan(dev, 512, [256, 128, 512], [4, 2, 6], seed=33)
+    for rows in (1, 16):
+        print(f"fan codebook {cb} rows={rows}", flush=True)
+        x = synth.activations(rows, 512, seed=960 + rows)
+        xd = to_dev(x, dev)
+        outs = ops.gemm_group(xd, fan.dev, cb, torch.float32)
+        for j, out in enumerate(outs):
+            L = fan.host[j]
+            got = out.cpu().numpy()
+            assert_close(got, O.linear(x, L["trellis"], L["suh"], L["svh"], L["bits"], cb),
+                         what=f"codebook {cb} member {j} rows={rows}")
+            solo = ops.gemm(xd, *fan.dev[j], cb, torch.float32).cpu().numpy()
+            assert rel_l2(got, solo) < 1e-5
+
+
 def test_fan_bitwise_repeat_and_dtypes(dev):
     import torch
 
