@@ -135,6 +135,18 @@ def test_prefill_k_split_by_pair_count(small, tokens):
     assert_close(got, small.ref(x, ids, w), what=f"prefill T={tokens}")
 
 
+def test_prefill_at_the_pair_limit(small):
+    """The largest call one prefill launch sequence takes: 8192 tokens at
+    top-8, 65536 (token, slot) pairs, about 4096 rows per expert (64 wide tiles
+    each), K whole in both GEMMs."""
+    T = 8192
+    print(f"prefill at the pair limit T={T} top-8", flush=True)
+    ids, w = synth.routing(T, 16, 8, seed=860)
+    x = synth.activations(T, 512, seed=861)
+    got = run_prefill(small, x, ids, w).cpu().numpy()
+    assert_close(got, small.ref(x, ids, w), what="prefill 65536 pairs")
+
+
 def test_prefill_invalid_ids_and_zero_rows(small):
     T = 33
     rng = np.random.default_rng(6)

@@ -144,6 +144,16 @@ def test_prefill_input_alignment_without_device():
     assert "16-byte aligned" in _err()
 
 
+def test_prefill_pair_limit_without_device():
+    """One prefill call takes up to 65536 (token, slot) pairs: 8192 tokens at
+    top-8 are accepted, one more token is refused by the sizing function and
+    by the entry itself."""
+    lib = _lib.load()
+    assert lib.exl3_moe_prefill_scratch_bytes(8192, 4096, 2048, 8, 256) > 0
+    assert lib.exl3_moe_prefill_scratch_bytes(8193, 4096, 2048, 8, 256) == -1 and "65536" in _err()
+    assert _routed_call("exl3_moe_prefill_routed", m=32769, topk=2) == -1 and "65536" in _err()
+
+
 def test_prefill_scratch_drops_where_k_stops_splitting():
     """The prefill GEMMs split K in two below 4096 (down) and 8192 (gate/up)
     (token, slot) pairs and keep it whole from there, so the scratch, which
