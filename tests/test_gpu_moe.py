@@ -445,10 +445,12 @@ def test_tp_slice_against_oracle(tp_slice, kb, m, uniform):
 # ---------------------------------------------------------------- shared expert fused as one more slot
 
 
-@pytest.mark.parametrize("m", [1, 7, 16])
+@pytest.mark.parametrize("m", [1, 7, 16, 24, 32])
 def test_shared_expert_as_extra_slot(dev, m):
     """Routed top-8 plus a 6-bit shared expert appended to every row with
-    weight 1: out = sum of the routed experts + the shared expert, in one launch."""
+    weight 1: out = sum of the routed experts + the shared expert, in one launch.
+    32 rows x 9 slots is the decode kernels' largest call (288 slots); past 16
+    rows the shared expert's group runs in 16-row passes."""
     print(f"shared expert slot m={m}", flush=True)
     if not hasattr(test_shared_expert_as_extra_slot, "layer"):
         test_shared_expert_as_extra_slot.layer = Layer(dev, 13, 512, 256, [3, 2] * 6 + [6], seed=33)
