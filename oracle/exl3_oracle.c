@@ -87,13 +87,12 @@ uint16_t ora_window(const uint16_t* tile, int bits, int t) {
 #define ORA_MCG_MULT 0xCBAC1FEDu
 #define ORA_MUL1_MULT 0x83DCD12Du
 
-static uint16_t half_add_rne(uint16_t a, uint16_t b) {
-    /* the double sum of two binary16 values is exact */
-    return ora_double_to_half((double)ora_half_to_float(a) + (double)ora_half_to_float(b));
-}
-
-/* cb: 0 = 3INST, 1 = MCG, 2 = MUL1 (exl3_gemm.cu.lna:186-189 numbering) */
-uint16_t ora_codebook(uint16_t window, int cb) {
+/* The codebook's value before its one rounding to binary16, exact in a
+ * double: for 3INST and MCG the sum of the two binary16 addends, for MUL1 the
+ * half FMA's exact result.  (The GPU GEMV and MoE kernels feed the two addends
+ * to the matrix core separately, so they use this value, not the rounded one.)
+ * cb: 0 = 3INST, 1 = MCG, 2 = MUL1 (exl3_gemm.cu.lna:186-189 numbering) */
+double ora_codebook_exact(uint16_t window, int cb) {
     uint32_t x = window;
     if (cb == 2) {
         x *= ORA_MUL1_MULT;
@@ -101,19 +100,26 @@ uint16_t ora_codebook(uint16_t window, int cb) {
                            ((x >> 16) & 0xffu) + ((x >> 24) & 0xffu);
         /* single-rounded half FMA: s*h(0x1eee) + h(0xc931); the double
          * product of two halves is exact and so is the sum here */
-        const double v = (double)ora_half_to_float((uint16_t)s) *
-                             (double)ora_half_to_float(0x1eee) +
-                         (double)ora_half_to_float(0xc931);
-        return ora_double_to_half(v);
+        return (double)ora_half_to_float((uint16_t)s) * (double)ora_half_to_float(0x1eee) +
+               (double)ora_half_to_float(0xc931);
     }
     if (cb == 0) x = x * 89226354u + 64248484u;
     else x = x * ORA_MCG_MULT;
     x = (x & 0x8fff8fffu) ^ 0x3b603b60u;   /* lop3 0x6a */
-    return half_add_rne((uint16_t)(x & 0xffffu), (uint16_t)(x >> 16));
+    /* the double sum of two binary16 values is exact */
+    return (double)ora_half_to_float((uint16_t)(x & 0xffffu)) + (double)ora_half_to_float((uint16_t)(x >> 16));
+}
+
+uint16_t ora_codebook(uint16_t window, int cb) {
+    return ora_double_to_half(ora_codebook_exact(window, cb));
 }
 
 void ora_codebook_lut(int cb, uint16_t* lut /* [65536] */) {
     for (uint32_t w = 0; w < 65536u; ++w) lut[w] = ora_codebook((uint16_t)w, cb);
+}
+
+void ora_codebook_exact_lut(int cb, double* lut /* [65536] */) {
+    for (uint32_t w = 0; w < 65536u; ++w) lut[w] = ora_codebook_exact((uint16_t)w, cb);
 }
 
 /* ---------------- A.4 tile permutation ---------------- */

@@ -110,6 +110,45 @@ def test_codebook_mul1_vs_numpy():
     assert np.array_equal(O.codebook_lut(O.CB_MUL1), expect)
 
 
+@pytest.mark.parametrize("cb", [O.CB_MCG, O.CB_3INST])
+def test_codebook_exact_mcg_3inst_vs_numpy(cb):
+    """Before rounding, the MCG / 3INST value is the exact sum of its two
+    binary16 addends (the GPU kernels add them in the matrix core)."""
+    lo, hi = _mcg_parts(cb)
+    assert np.array_equal(O.codebook_exact_lut(cb), lo.astype(np.float64) + hi.astype(np.float64))
+
+
+def test_codebook_exact_mul1_vs_numpy():
+    w = np.arange(65536, dtype=np.uint64)
+    x = (w * 0x83DCD12D) & 0xFFFFFFFF
+    s = 0x6400 + (x & 0xFF) + ((x >> 8) & 0xFF) + ((x >> 16) & 0xFF) + ((x >> 24) & 0xFF)
+    sh = s.astype(np.uint16).view(np.float16).astype(np.float64)
+    a = np.array([0x1EEE], np.uint16).view(np.float16).astype(np.float64)[0]
+    c = np.array([0xC931], np.uint16).view(np.float16).astype(np.float64)[0]
+    assert np.array_equal(O.codebook_exact_lut(O.CB_MUL1), sh * a + c)
+
+
+@pytest.mark.parametrize("cb", [O.CB_MCG, O.CB_3INST, O.CB_MUL1])
+def test_codebook_is_the_exact_value_rounded(cb):
+    """The binary16 codebook is its exact value rounded to nearest even, and
+    the rounding changes a large share of the values (so weights with and
+    without it differ measurably)."""
+    ex = O.codebook_exact_lut(cb)
+    assert np.array_equal(ex.astype(np.float16).view(np.uint16), O.codebook_lut(cb))
+    assert np.mean(ex != ex.astype(np.float16).astype(np.float64)) > 0.3
+
+
+@pytest.mark.parametrize("bits,cb", [(2, O.CB_MCG), (3, O.CB_MCG), (6, O.CB_3INST), (4, O.CB_MUL1)])
+def test_reconstruct_exact_rounds_to_reconstruct(bits, cb):
+    """Every element of the exact-addend reconstruct rounds to the binary16
+    reconstruct: the two read the same window for every element."""
+    rng = np.random.default_rng(bits)
+    tr = rng.integers(-32768, 32768, size=(8, 6, 16 * bits), dtype=np.int64).astype(np.int16)
+    e = O.reconstruct_exact(tr, bits, cb)
+    assert e.dtype == np.float64 and e.shape == (128, 96)
+    assert np.array_equal(e.astype(np.float16).view(np.uint16), O.reconstruct_fast(tr, bits, cb).view(np.uint16))
+
+
 @pytest.mark.parametrize("cb", [O.CB_MCG, O.CB_3INST, O.CB_MUL1])
 def test_codebook_vs_reference_truncating_helper(cb):
     """The reference host helper truncates (exl3_dequant.cuh:40-53); the canon
