@@ -85,8 +85,11 @@ class Layer:
         assert ops.moe_error(used) == 0, "MoE decode set its error word"
         return out
 
-    def ref(self, x16, ids, w, limit=LIMIT):
-        return O.moe(x16, ids, w, self.experts, limit, cache=self.cache)
+    def ref(self, x16, ids, w, limit=LIMIT, exact_addends=False):
+        # the exact-addend weights are float64: not kept (a full-shape layer's
+        # would take tens of GB)
+        return O.moe(x16, ids, w, self.experts, limit, cache=None if exact_addends else self.cache,
+                     exact_addends=exact_addends)
 
 
 @pytest.fixture(scope="module")
