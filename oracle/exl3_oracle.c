@@ -87,22 +87,25 @@ uint16_t ora_window(const uint16_t* tile, int bits, int t) {
 #define ORA_MCG_MULT 0xCBAC1FEDu
 #define ORA_MUL1_MULT 0x83DCD12Du
 
-/* The codebook's value before its one rounding to binary16, exact in a
- * double: for 3INST and MCG the sum of the two binary16 addends, for MUL1 the
- * half FMA's exact result.  (The GPU GEMV and MoE kernels feed the two addends
- * to the matrix core separately, so they use this value, not the rounded one.)
+/* MUL1's value: a single-rounded half FMA s*h(0x1eee) + h(0xc931); the double
+ * product of two halves is exact and so is the sum here, so this is the FMA's
+ * exact result before its one rounding. */
+static double mul1_fma_exact(uint16_t window) {
+    const uint32_t x = (uint32_t)window * ORA_MUL1_MULT;
+    const uint32_t s = 0x6400u + (x & 0xffu) + ((x >> 8) & 0xffu) + ((x >> 16) & 0xffu) + ((x >> 24) & 0xffu);
+    return (double)ora_half_to_float((uint16_t)s) * (double)ora_half_to_float(0x1eee) +
+           (double)ora_half_to_float(0xc931);
+}
+
+/* The exact sum, in a double, of the binary16 addends whose rounded sum is
+ * the codebook value: for 3INST and MCG the two masked halves; MUL1 is one
+ * single-rounded half FMA, so its one addend is the binary16 value itself.
+ * (The GPU GEMV and MoE kernels hand these addends to the matrix core, which
+ * adds them exactly, so this is the weight they use.)
  * cb: 0 = 3INST, 1 = MCG, 2 = MUL1 (exl3_gemm.cu.lna:186-189 numbering) */
-double ora_codebook_exact(uint16_t window, int cb) {
+double ora_codebook_addend_sum(uint16_t window, int cb) {
+    if (cb == 2) return (double)ora_half_to_float(ora_double_to_half(mul1_fma_exact(window)));
     uint32_t x = window;
-    if (cb == 2) {
-        x *= ORA_MUL1_MULT;
-        const uint32_t s = 0x6400u + (x & 0xffu) + ((x >> 8) & 0xffu) +
-                           ((x >> 16) & 0xffu) + ((x >> 24) & 0xffu);
-        /* single-rounded half FMA: s*h(0x1eee) + h(0xc931); the double
-         * product of two halves is exact and so is the sum here */
-        return (double)ora_half_to_float((uint16_t)s) * (double)ora_half_to_float(0x1eee) +
-               (double)ora_half_to_float(0xc931);
-    }
     if (cb == 0) x = x * 89226354u + 64248484u;
     else x = x * ORA_MCG_MULT;
     x = (x & 0x8fff8fffu) ^ 0x3b603b60u;   /* lop3 0x6a */
@@ -110,16 +113,18 @@ double ora_codebook_exact(uint16_t window, int cb) {
     return (double)ora_half_to_float((uint16_t)(x & 0xffffu)) + (double)ora_half_to_float((uint16_t)(x >> 16));
 }
 
+/* The codebook value: that sum rounded to nearest even (a binary16 addend of
+ * MUL1 is unchanged by it). */
 uint16_t ora_codebook(uint16_t window, int cb) {
-    return ora_double_to_half(ora_codebook_exact(window, cb));
+    return ora_double_to_half(ora_codebook_addend_sum(window, cb));
 }
 
 void ora_codebook_lut(int cb, uint16_t* lut /* [65536] */) {
     for (uint32_t w = 0; w < 65536u; ++w) lut[w] = ora_codebook((uint16_t)w, cb);
 }
 
-void ora_codebook_exact_lut(int cb, double* lut /* [65536] */) {
-    for (uint32_t w = 0; w < 65536u; ++w) lut[w] = ora_codebook_exact((uint16_t)w, cb);
+void ora_codebook_addend_sum_lut(int cb, double* lut /* [65536] */) {
+    for (uint32_t w = 0; w < 65536u; ++w) lut[w] = ora_codebook_addend_sum((uint16_t)w, cb);
 }
 
 /* ---------------- A.4 tile permutation ---------------- */

@@ -31,13 +31,13 @@ Reference rounding points reproduced (file:line in the reference tree):
   top-k slot order).
 
 The weights of that path are the codebook values rounded to binary16.  The
-same layer on the values before that rounding (``codebook_exact_lut``,
-``reconstruct_exact``, ``moe(..., exact_addends=True)``: the exact sum of the
-two binary16 addends, or MUL1's exact half FMA) is what the GPU kernels
-compute, since their matrix cores add the two addends themselves; the tests
-use it beside the rounded-weight oracle.  Its codebook values are pinned
-against the numpy restatement of the addends and by rounding back to the
-binary16 codebook.
+same layer on the exact sums of each value's binary16 addends
+(``codebook_addend_sum_lut``, ``reconstruct_exact``,
+``moe(..., exact_addends=True)``: the two masked halves of 3INST and MCG; MUL1
+has one addend, its binary16 value) is what the GPU kernels compute, since
+their matrix cores add the addends themselves; the tests use it beside the
+rounded-weight oracle.  Its values are pinned against the numpy restatement
+of the addends and by rounding back to the binary16 codebook.
 """
 
 from __future__ import annotations
@@ -79,7 +79,7 @@ def lib() -> ctypes.CDLL:
     L.ora_codebook.argtypes = [ctypes.c_uint16, ctypes.c_int]
     L.ora_codebook.restype = ctypes.c_uint16
     L.ora_codebook_lut.argtypes = [ctypes.c_int, u16p]
-    L.ora_codebook_exact_lut.argtypes = [ctypes.c_int, np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]
+    L.ora_codebook_addend_sum_lut.argtypes = [ctypes.c_int, np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")]
     L.ora_tile_t.argtypes = [ctypes.c_int, ctypes.c_int]
     L.ora_tile_t.restype = ctypes.c_int
     L.ora_reconstruct.argtypes = [u16p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, u16p]
@@ -166,19 +166,20 @@ def reconstruct_fast(trellis: np.ndarray, bits: int, cb: int = CB_MCG) -> np.nda
 
 
 @lru_cache(maxsize=3)
-def codebook_exact_lut(cb: int = CB_MCG) -> np.ndarray:
-    """All 65536 codebook values before their rounding to binary16 (float64):
-    the exact sum of the two binary16 addends (3INST, MCG) or the exact half
-    FMA (MUL1).  codebook_lut(cb) is this rounded to nearest even."""
+def codebook_addend_sum_lut(cb: int = CB_MCG) -> np.ndarray:
+    """All 65536 exact sums (float64) of the binary16 addends whose rounded sum
+    is the codebook value: the two masked halves for 3INST and MCG; MUL1 is a
+    single-rounded half FMA, one addend, so its entry is the binary16 value.
+    codebook_lut(cb) is this rounded to nearest even."""
     out = np.empty(65536, np.float64)
-    lib().ora_codebook_exact_lut(cb, out)
+    lib().ora_codebook_addend_sum_lut(cb, out)
     out.setflags(write=False)
     return out
 
 
 def reconstruct_exact(trellis: np.ndarray, bits: int, cb: int = CB_MCG) -> np.ndarray:
-    """Each element's codebook value before its binary16 rounding, float64
-    [K, N]: the weight the GPU kernels use, which hand the two addends to the
+    """Each element's exact addend sum (codebook_addend_sum_lut), float64
+    [K, N]: the weight the GPU kernels use, which hand the addends to the
     matrix core and add them there in fp32.  The windows come from the same
     reconstruct as reconstruct_fast, run with the identity table."""
     kt, nt, tw = trellis.shape
@@ -186,7 +187,7 @@ def reconstruct_exact(trellis: np.ndarray, bits: int, cb: int = CB_MCG) -> np.nd
     win = np.empty((kt * 16, nt * 16), np.uint16)
     lib().ora_reconstruct_fast(_u16(trellis).reshape(-1), kt * 16, nt * 16, bits,
                                np.arange(65536, dtype=np.uint16), win.reshape(-1))
-    return codebook_exact_lut(cb)[win]
+    return codebook_addend_sum_lut(cb)[win]
 
 
 def dequant_full_c(trellis, suh, svh, bits, cb=CB_MCG) -> np.ndarray:
@@ -326,9 +327,9 @@ def moe(x16: np.ndarray, ids: np.ndarray, weights: np.ndarray, experts: list[dic
     ids int [m, topk]; ids outside [0, len(experts)) contribute nothing.  Each
     distinct (expert, row) pair is computed once; the expert sum walks the
     top-k slots of each row in order, in fp32.  exact_addends: the weights are
-    the codebook values before their binary16 rounding (reconstruct_exact),
-    as the GPU kernels use them; otherwise the rounded weights of the
-    reference's CPU path."""
+    the exact sums of the codebook addends (reconstruct_exact), as the GPU
+    kernels use them; otherwise the rounded weights of the reference's CPU
+    path."""
     m, H = x16.shape
     topk = ids.shape[1]
     n_exp = len(experts)

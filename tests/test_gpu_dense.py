@@ -104,12 +104,23 @@ def test_gemm_baseline_shapes(ops, dev, k, n, bits):
         assert_close(y.cpu().numpy(), ref, what=f"{k}x{n} K{bits} rows={rows}")
 
 
-def test_gemm_c0_config(ops, dev):
-    """K=N=4096, 6 bits, 1 row: the CPU-reference configuration."""
+@pytest.mark.parametrize("bits,cb", [(6, O.CB_MCG), (2, O.CB_MCG), (3, O.CB_3INST), (4, O.CB_MUL1)])
+def test_gemm_c0_config(ops, dev, bits, cb):
+    """K=N=4096, 1 row (6 bits: the CPU-reference configuration).  Against the
+    oracle of the reference's CPU path (weights rounded to binary16) at the
+    standard bar, and against the oracle on the weights the kernel uses (the
+    exact sum of each weight's binary16 codebook addends, which the matrix
+    core adds itself; for MUL1, one addend, the two oracles coincide) at fp32
+    rounding: rel-L2 2e-6 (measured 1.7e-7)."""
     import torch
 
-    got, ref = _gemm_case(ops, dev, 4096, 4096, 6, 1, torch.float32, seed=2026)
+    got, ref = _gemm_case(ops, dev, 4096, 4096, bits, 1, torch.float32, seed=2026, cb=cb)
     assert_close(got, ref, what="C0")
+    L = synth.dense(4096, 4096, bits, seed=2026 + bits)
+    x = synth.activations(1, 4096, seed=2026 + 1)
+    exact = O.linear(x, L["trellis"], L["suh"], L["svh"], bits, cb, w=O.reconstruct_exact(L["trellis"], bits, cb))
+    mae, rel = assert_close(got, exact, max_abs=2e-5, rel=2e-6, what="C0 (exact addends)")
+    print(f"C0 K{bits} cb={cb}: against exact addends max-abs {mae:.3e} rel-L2 {rel:.3e}", flush=True)
 
 
 @pytest.mark.parametrize("rows", [17, 31, 32, 33, 40, 64, 100, 144])

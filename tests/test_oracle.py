@@ -111,31 +111,23 @@ def test_codebook_mul1_vs_numpy():
 
 
 @pytest.mark.parametrize("cb", [O.CB_MCG, O.CB_3INST])
-def test_codebook_exact_mcg_3inst_vs_numpy(cb):
-    """Before rounding, the MCG / 3INST value is the exact sum of its two
-    binary16 addends (the GPU kernels add them in the matrix core)."""
+def test_codebook_addend_sum_mcg_3inst_vs_numpy(cb):
+    """The MCG / 3INST addend sum is the exact sum of the two masked binary16
+    halves (the GPU kernels add them in the matrix core); rounded, it is the
+    codebook, and the rounding changes a large share of the values (so weights
+    with and without it differ measurably)."""
     lo, hi = _mcg_parts(cb)
-    assert np.array_equal(O.codebook_exact_lut(cb), lo.astype(np.float64) + hi.astype(np.float64))
+    s = O.codebook_addend_sum_lut(cb)
+    assert np.array_equal(s, lo.astype(np.float64) + hi.astype(np.float64))
+    assert np.array_equal(s.astype(np.float16).view(np.uint16), O.codebook_lut(cb))
+    assert np.mean(s != s.astype(np.float16).astype(np.float64)) > 0.3
 
 
-def test_codebook_exact_mul1_vs_numpy():
-    w = np.arange(65536, dtype=np.uint64)
-    x = (w * 0x83DCD12D) & 0xFFFFFFFF
-    s = 0x6400 + (x & 0xFF) + ((x >> 8) & 0xFF) + ((x >> 16) & 0xFF) + ((x >> 24) & 0xFF)
-    sh = s.astype(np.uint16).view(np.float16).astype(np.float64)
-    a = np.array([0x1EEE], np.uint16).view(np.float16).astype(np.float64)[0]
-    c = np.array([0xC931], np.uint16).view(np.float16).astype(np.float64)[0]
-    assert np.array_equal(O.codebook_exact_lut(O.CB_MUL1), sh * a + c)
-
-
-@pytest.mark.parametrize("cb", [O.CB_MCG, O.CB_3INST, O.CB_MUL1])
-def test_codebook_is_the_exact_value_rounded(cb):
-    """The binary16 codebook is its exact value rounded to nearest even, and
-    the rounding changes a large share of the values (so weights with and
-    without it differ measurably)."""
-    ex = O.codebook_exact_lut(cb)
-    assert np.array_equal(ex.astype(np.float16).view(np.uint16), O.codebook_lut(cb))
-    assert np.mean(ex != ex.astype(np.float16).astype(np.float64)) > 0.3
+def test_codebook_addend_sum_mul1_is_its_value():
+    """MUL1 is one single-rounded half FMA: its one addend is the codebook
+    value itself (the kernels hand it to the matrix core with a zero)."""
+    s = O.codebook_addend_sum_lut(O.CB_MUL1)
+    assert np.array_equal(s, O.codebook_lut(O.CB_MUL1).view(np.float16).astype(np.float64))
 
 
 @pytest.mark.parametrize("bits,cb", [(2, O.CB_MCG), (3, O.CB_MCG), (6, O.CB_3INST), (4, O.CB_MUL1)])
