@@ -121,6 +121,10 @@ def test_prefill_wide_tiles_bitwise_narrow(small):
     torch.cuda.synchronize()
     assert torch.equal(whole, sliced), "wide tiles changed a row's result"
     assert_close(whole.cpu().numpy(), small.ref(x, ids, w), what="wide tiles")
+    # against the weights the kernels use (exact sums of the codebook addends)
+    mae, rel = assert_close(whole.cpu().numpy(), small.ref(x, ids, w, exact_addends=True), max_abs=4e-3, rel=1e-4,
+                            what="wide tiles (exact addends)")
+    print(f"wide tiles against exact addends: max-abs {mae:.3e} rel-L2 {rel:.3e}", flush=True)
 
 
 @pytest.mark.parametrize("tokens", [700, 1400])
