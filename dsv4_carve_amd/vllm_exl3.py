@@ -19,6 +19,10 @@ error behaviour, so the plugin's dispatch code can switch to this package:
     of a module that read the same input, by LNA_EXL3_DENSE_GROUP
     (recipe-lna/vllm_exl3_exl3.py.lna:62-802), and the cross-module T1 fans
     whose later members read the fused call's cached outputs.
+  * LNA_EXL3_VRAM_TRACE=1 logs the torch allocator's bytes before and after
+    each allocating phase (group and fan registration, their scratch, each
+    group's first call, the MoE tables and scratch), as the reference's trace
+    does (recipe-lna/vllm_exl3_exl3.py.lna:92-118).
   * ``Exl3MoEMethod`` / ``Exl3LinearMethod`` -- create_weights /
     process_weights_after_loading / apply (recipe-lna/vllm_exl3_exl3.py.lna:2045-2307,
     2310-2853), importable without vLLM.
@@ -304,7 +308,52 @@ def reset_dense_group_state() -> None:
         _DENSE_GROUP_STATS[key] = 0
     _DENSE_GROUP_FALLBACK_COUNTS.clear()
     _DENSE_GROUP_ACTIVE_LOGGED.clear()
+    _VRAM_FIRST_CALL_TRACED.clear()
     _DENSE_GROUP_CALL_COUNTS.update({1: 0, 2: 0})
+
+
+# ---------------------------------------------------------------- VRAM trace
+
+_VRAM_FIRST_CALL_TRACED: set = set()
+
+
+def _vram_mark(device) -> int | None:
+    """Bytes the torch allocator holds on `device` after a synchronize, or None
+    unless LNA_EXL3_VRAM_TRACE=1 (the reference's opt-in trace of allocation
+    deltas per phase, recipe-lna/vllm_exl3_exl3.py.lna:92-118).  The library's
+    own static arrays (the no-alloc entry's fixed scratch) are not torch
+    allocations and never show here."""
+    if os.environ.get("LNA_EXL3_VRAM_TRACE") != "1" or device is None:
+        return None
+    device = torch.device(device)
+    if device.type != "cuda":
+        return None
+    torch.cuda.synchronize(device)
+    return int(torch.cuda.memory_allocated(device))
+
+
+def _vram_report(phase: str, group_id: str, before: int | None, after: int | None) -> None:
+    """One log line per traced phase, in the reference's format (log scrapers
+    read it): phase, layer, allocated MiB before and after, and the delta."""
+    if before is None or after is None:
+        return
+    mib = 1024.0 * 1024.0
+    logger.info("F2 VRAM phase=%s layer=%s before_mib=%.3f after_mib=%.3f delta_mib=%+.3f",
+                phase, group_id, before / mib, after / mib, (after - before) / mib)
+
+
+def _vram_first_call(group_id: str, device):
+    """Mark before a group's first call (None when traced already or off)."""
+    if group_id in _VRAM_FIRST_CALL_TRACED:
+        return None
+    return _vram_mark(device)
+
+
+def _vram_first_call_done(group_id: str, device, before) -> None:
+    if before is None:
+        return
+    _vram_report("first_call", group_id, before, _vram_mark(device))
+    _VRAM_FIRST_CALL_TRACED.add(group_id)
 
 
 def _dense_group_members(linears: list, group_id: str) -> dict:
@@ -387,11 +436,13 @@ def build_exl3_dense_group(module) -> None:
         module._exl3_dense_group = None            # a one-shard module may still join a fan
     else:
         group_id = f"local:{getattr(module, 'prefix', '?')}:{id(module)}"
+        before = _vram_mark(linears[0].trellis.device)
         try:
             module._exl3_dense_group = _dense_group_members(linears, group_id)
         except ValueError as exc:
             module._exl3_dense_group = None
             _dense_group_fallback("registration", str(exc), group_id)
+        _vram_report("registration.local_tables", group_id, before, _vram_mark(linears[0].trellis.device))
     if dense_group_mode() == 2:
         _register_dense_fan(module)
 
@@ -400,7 +451,9 @@ def prewarm_exl3_dense_group(module) -> None:
     """Reserve the fused call's scratch for the prewarm row counts."""
     group = getattr(module, "_exl3_dense_group", None)
     if group:
+        before = _vram_mark(group["device"])
         _prewarm_group(group)
+        _vram_report("registration.local_scratch", group["group_id"], before, _vram_mark(group["device"]))
 
 
 # ---------------------------------------------------------------- T1 fans
@@ -465,6 +518,7 @@ def _publish_dense_fan(group_id: str, kind: str) -> None:
             return
         positions[id(module)] = tuple(range(len(flat), len(flat) + len(members)))
         flat.extend(members)
+    tables_before = _vram_mark(flat[0].trellis.device)
     try:
         fan = _dense_group_members(flat, group_id)
     except ValueError as exc:
@@ -479,8 +533,11 @@ def _publish_dense_fan(group_id: str, kind: str) -> None:
                 "member_refs": tuple(weakref.ref(m) for m in modules), "cache": None, "last_completed": None,
                 "generation": 0, "prewarm_failed": True,
                 "outbuf": torch.empty(DENSE_GROUP_MAX_ROWS * sum(fan["ns"]), dtype=torch.float32, device=device)})
+    _vram_report("registration.fan_tables", group_id, tables_before, _vram_mark(device))
     if device.type == "cuda":
+        scratch_before = _vram_mark(device)
         fan["prewarm_failed"] = not _prewarm_group(fan, lambda rows: _fan_outputs(fan, rows))
+        _vram_report("registration.fan_scratch", group_id, scratch_before, _vram_mark(device))
     for m in modules:
         m._exl3_dense_fan = fan
 
@@ -536,11 +593,13 @@ def _run_fan(module, fan: dict, x_fp16: torch.Tensor, source: torch.Tensor, m: i
                               "previous one", group_id)
         fan["cache"] = None
     outs = _fan_outputs(fan, m)
+    first = None if torch.cuda.is_current_stream_capturing() else _vram_first_call(group_id, x_fp16.device)
     try:
         ops.gemm_group(x_fp16, fan["members"], fan["codebook"], torch.float32, outs=outs)
     except Exception as exc:
         _dense_group_fallback("error", repr(exc), group_id)
         return None
+    _vram_first_call_done(group_id, x_fp16.device, first)
     fan["generation"] += 1
     fan["cache"] = {"key": key, "m": m, "stream": stream, "used": {id(module)}, "outs": outs,
                     "source_ref": source}
@@ -601,11 +660,13 @@ def run_exl3_group(module, x_fp16: torch.Tensor, out_dtype: torch.dtype = torch.
     if int(x_fp16.shape[1]) != group["k"]:
         _dense_group_fallback("input", f"group k={group['k']} got {x_fp16.shape[1]}", group["group_id"])
         return solo()
+    first = None if torch.cuda.is_current_stream_capturing() else _vram_first_call(group["group_id"], x_fp16.device)
     try:
         outs = ops.gemm_group(x_fp16, group["members"], group["codebook"], out_dtype)
     except Exception as exc:
         _dense_group_fallback("error", repr(exc), group["group_id"])
         return solo()
+    _vram_first_call_done(group["group_id"], x_fp16.device, first)
     _dense_group_active(1, group["group_id"])
     return outs
 
@@ -827,6 +888,8 @@ def build_exl3_fused_state(layer, inners: list[dict[str, Any]]) -> None:
     (recipe-lna/vllm_exl3_exl3.py.lna:1543-1594).  The weights must stay alive
     and must not move while the tables are in use."""
     device = inners[0]["gate"].trellis.device
+    layer_id = getattr(layer, "prefix", "?")
+    before = _vram_mark(device)
     tables = {}
     for key in MOE_TABLE_KEYS:
         which, attr = key.split("_", 1)
@@ -840,8 +903,11 @@ def build_exl3_fused_state(layer, inners: list[dict[str, Any]]) -> None:
     layer._exl3_ptr_sources = [(p["gate"].trellis, p["down"].trellis) for p in inners]
     if len(set(bits)) == 1:
         layer._exl3_k = bits[0]
+    _vram_report("moe.tables", layer_id, before, _vram_mark(device))
     if get_moe_kernel_backend() == "lna2":
+        before = _vram_mark(device)
         _prepare_lna_state(layer, inners)
+        _vram_report("moe.scratch", layer_id, before, _vram_mark(device))
 
 
 def _ptrs_stale(layer, inners) -> bool:
@@ -1453,8 +1519,10 @@ class Exl3LinearMethod:
             return
         dev = lins[0].trellis.device
         try:
+            before = _vram_mark(dev)
             for lin in lins:
                 ops.prepare_gemm(dev, AUTO_RECONSTRUCT_THRESHOLD, int(lin.in_features), int(lin.out_features))
+            _vram_report("registration.gemv_scratch", getattr(layer, "prefix", "?"), before, _vram_mark(dev))
             prewarm_exl3_dense_group(layer)
         except Exception as exc:
             logger.warning("EXL3 prewarm skipped for %s: %s", getattr(layer, "prefix", "?"), exc)

@@ -165,3 +165,58 @@ def test_decode_scratch_serves_a_layer_like_the_checked_ones(dev, monkeypatch):
                                    LIMIT)
     torch.cuda.synchronize()
     assert_close(y.float().cpu().numpy(), ref.cpu().numpy(), max_abs=2e-2 + 8e-3)
+
+
+def test_vram_trace_phases_match_the_scratch_sizes(dev, monkeypatch, caplog):
+    """LNA_EXL3_VRAM_TRACE=1 (recipe-lna/vllm_exl3_exl3.py.lna:92-118) on a fresh
+    scratch pool: one routed layer and one two-shard dense module log each
+    allocating phase, and every delta is what that phase keeps: the MoE
+    pointer and width tables, the decode scratch, the dense GEMV scratch, no
+    device tables for a T0 group, and the first call's two fp32 outputs."""
+    import logging
+    import re
+
+    import torch
+    from dsv4_carve_amd import ops
+    from dsv4_carve_amd import vllm_exl3 as V
+
+    monkeypatch.setenv("LNA_EXL3_VRAM_TRACE", "1")
+    monkeypatch.setenv("VLLM_EXL3_MOE_KERNEL", "lna2")
+    monkeypatch.setenv("VLLM_EXL3_MOE_STRICT", "2")
+    monkeypatch.setenv("LNA_EXL3_DENSE_GROUP", "1")
+    monkeypatch.setattr(ops, "SCRATCH", ops._ScratchPool())
+    V.reset_dense_group_state()
+    host_experts = []
+    for e in range(E):
+        ex = synth.expert(e, H, I, BITS, seed=570)
+        host_experts.append({p: {k: torch.from_numpy(ex[p][k]) for k in ("trellis", "suh", "svh")}
+                             for p in ("gate", "up", "down")})
+    gu_host = [synth.dense(H, I, SHARED_BITS, seed=575 + j) for j in range(2)]
+    gu_dev = [{k: to_dev(h[k], dev) for k in ("trellis", "suh", "svh")} for h in gu_host]
+    m = 4
+    with caplog.at_level(logging.INFO, logger=V.logger.name):
+        _moe_layer(dev, host_experts, 0)
+        gu, gu_meth = _dense_module(dev, "model.layers.0.ffn.shared_experts.gate_up_proj", H, [I, I], gu_dev)
+        gu_meth.apply(gu, to_dev(synth.activations(m, H, seed=576), dev))
+        torch.cuda.synchronize()
+    pat = re.compile(r"F2 VRAM phase=(\S+) layer=(\S+) before_mib=([\d.]+) after_mib=([\d.]+) delta_mib=([+-][\d.]+)")
+    delta = {}                                        # MiB, as logged (three decimals)
+    for r in caplog.records:
+        hit = pat.fullmatch(r.getMessage())
+        if hit:
+            assert hit.group(1) not in delta, f"phase {hit.group(1)} logged twice"
+            delta[hit.group(1)] = float(hit.group(5))
+    print("traced deltas (MiB):", delta, flush=True)
+    blocks = lambda b: -(-b // 512) * 512             # the caching allocator's 512-byte rounding
+    near = lambda phase, nbytes: abs(delta[phase] - nbytes / 2 ** 20) <= 5e-4 + 1e-9   # the log's rounding
+    assert set(delta) == {"moe.tables", "moe.scratch", "registration.gemv_scratch", "registration.local_tables",
+                          "registration.local_scratch", "first_call"}, delta
+    # one int64 entry per expert in each pointer table, one int8 width per expert
+    assert near("moe.tables", len(V.MOE_TABLE_KEYS) * blocks(E * 8) + blocks(E))
+    assert near("moe.scratch", blocks(ops.moe_scratch_bytes(H, I, V.LNA2_MAX_TOPK, rows=V.lna2_max_rows())))
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    held = {purpose: int(buf.numel()) for (d, purpose), buf in ops.SCRATCH._bufs.items() if d == idx}
+    assert near("registration.gemv_scratch", blocks(held["gemm"]))
+    assert delta["registration.local_tables"] == 0.0
+    assert near("registration.local_scratch", blocks(held["gemm_group"]))
+    assert near("first_call", 2 * blocks(m * I * 4))

@@ -546,3 +546,26 @@ def test_scratch_pool_frees_replaced_buffers_unless_captured(monkeypatch):
     c = pool.get(cpu, "moe", 8000)
     assert pool.resident_bytes() == 8000 + 4000             # `b` retired, kept alive
     assert pool.get(cpu, "moe", 16000) is not c and pool.resident_bytes() == 16000 + 4000
+
+
+def test_vram_trace_is_opt_in_and_logs_the_reference_format(monkeypatch, caplog):
+    """LNA_EXL3_VRAM_TRACE=1 (recipe-lna/vllm_exl3_exl3.py.lna:92-118): no mark
+    unless it is set, none for a CPU device, and one line per phase with the
+    before / after MiB and the signed delta."""
+    import logging
+
+    monkeypatch.delenv("LNA_EXL3_VRAM_TRACE", raising=False)
+    assert V._vram_mark(torch.device("cpu")) is None
+    monkeypatch.setenv("LNA_EXL3_VRAM_TRACE", "1")
+    assert V._vram_mark(torch.device("cpu")) is None
+    assert V._vram_mark(None) is None
+    with caplog.at_level(logging.INFO, logger=V.logger.name):
+        V._vram_report("registration.fan_scratch", "layers.3:hfan", 3 << 20, (3 << 20) + (1 << 19))
+        V._vram_report("first_call", "g", None, 5)           # no mark, no line
+        V._vram_report("moe.scratch", "x", 2 << 20, 1 << 20)
+    lines = [r.getMessage() for r in caplog.records]
+    assert lines == [
+        "F2 VRAM phase=registration.fan_scratch layer=layers.3:hfan before_mib=3.000 after_mib=3.500 "
+        "delta_mib=+0.500",
+        "F2 VRAM phase=moe.scratch layer=x before_mib=2.000 after_mib=1.000 delta_mib=-1.000",
+    ]
