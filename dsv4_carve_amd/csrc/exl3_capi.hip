@@ -114,7 +114,7 @@ int exl3_gemm(const uint16_t* a, int64_t m, int64_t k, const int16_t* b, int64_t
         if (rc) return rc;
         if (p.split_reduce) {
             hipLaunchKernelGGL(gemv_reduce_kernel<RED_BATCH>, dim3((int)(n / 128) * R), dim3(64), 0, s, partials, svh, cr,
-                               c_kind, R, (int)n, p.n_kc);
+                               c_kind, R, (int)n, p.n_kc, p.xcd ? 1 : 0);
             if ((rc = check_launch())) return rc;
         }
     }
@@ -182,6 +182,7 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
         P.x = a + r0 * k;
         P.R = R; P.K = (int)k; P.nsteps = p.nsteps; P.n_kc = p.n_kc; P.count = (int)count; P.out_kind = c_kind;
         int blocks = 0, rblocks = 0;
+        bool whole = true;
         for (int64_t j = 0; j < count; ++j) {
             const int n_cb = (int)((n_list[j] + COLS - 1) / COLS);
             P.trellis[j] = trellis[j]; P.suh[j] = suh[j]; P.svh[j] = svh[j];
@@ -193,9 +194,11 @@ int exl3_gemm_group(const uint16_t* a, int64_t m, int64_t k, int64_t count, cons
             P.rblock0[j] = rblocks;
             blocks += n_cb * p.n_kc;
             rblocks += (int)(n_list[j] / 128) * R;
+            whole = whole && n_list[j] % COLS == 0;
         }
         P.block0[count] = blocks;
         P.rblock0[count] = rblocks;
+        P.xcd = xcd_order_allowed() && whole && (blocks / p.n_kc) % N_XCD == 0 ? 1 : 0;
         for (int b = 1; b <= 8; ++b) {
             if (!(widths & (1u << b))) continue;
             int rc = 0;

@@ -293,6 +293,7 @@ struct GemvPlan {
     int n_cb;           // 256-column blocks
     int waves;          // waves per item (column groups), 1, 2 or 4
     bool split_reduce;  // partial sums finished by gemv_reduce_kernel
+    bool xcd = false;   // items and finish keyed by column block (xcd_split)
 };
 
 // Rows of x per call of the kernels: up to 16 rows one MFMA row block, 17 and
@@ -346,8 +347,22 @@ inline GemvPlan gemv_plan_cb(int64_t rows, int64_t k, int64_t total_cb, int cus)
     return p;
 }
 
+// The partial-sum items of a column block and that block's finish run on one
+// XCD (xcd_split), so the finish reads the partials from its own L2, when the
+// column blocks (of a matrix, or of all members of a fan) are whole and a
+// multiple of 8.  EXL3_XCD_ORDER=0 turns it off.
+inline bool xcd_order_allowed() {
+    static const bool off = [] {
+        const char* v = getenv("EXL3_XCD_ORDER");
+        return v && *v && atoi(v) == 0;
+    }();
+    return !off;
+}
+
 inline GemvPlan gemv_plan(int64_t rows, int64_t k, int64_t n, int cus) {
-    return gemv_plan_cb(rows, k, (n + COLS - 1) / COLS, cus);
+    GemvPlan p = gemv_plan_cb(rows, k, (n + COLS - 1) / COLS, cus);
+    p.xcd = xcd_order_allowed() && n % COLS == 0 && p.n_cb % N_XCD == 0;
+    return p;
 }
 
 // Split-K partials of a matrix: [column block][row][k-chunk][256] fp32, so
@@ -565,9 +580,11 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ suh,
                                                       const uint16_t* __restrict__ svh, void* __restrict__ out,
                                                       int out_kind, int R, int K, int N, int nsteps, int n_kc,
-                                                      int* __restrict__ counters, float* __restrict__ partials) {
+                                                      int xcd, int* __restrict__ counters,
+                                                      float* __restrict__ partials) {
     __shared__ uint16_t xa[MAX_ROWS * RB * GEMV_NSTEP_CAP * STEP_K];
-    const int cb = blockIdx.x / n_kc, kc = blockIdx.x - cb * n_kc;
+    int cb, kc;
+    xcd_split(blockIdx.x, n_kc, xcd, cb, kc);      // group: column block
     gemv_item<BITS, CB, W, RB, !SPLIT>(x, trellis, suh, R, K, N, nsteps, cb, kc, partials, xa);
     if constexpr (SPLIT) return;
     publish_fence();
@@ -638,8 +655,12 @@ __device__ __forceinline__ void gemv_reduce_block(const float* __restrict__ part
 template <int BATCH>
 __global__ __launch_bounds__(64) void gemv_reduce_kernel(const float* __restrict__ partials,
                                                          const uint16_t* __restrict__ svh, void* __restrict__ out,
-                                                         int out_kind, int R, int N, int n_kc) {
-    const int hb = blockIdx.x / R, m = blockIdx.x - (blockIdx.x / R) * R;
+                                                         int out_kind, int R, int N, int n_kc, int xcd) {
+    // group: the 256-column block (two 128-blocks) whose partials gemv_kernel wrote on this XCD
+    int cb, j;
+    xcd_split(blockIdx.x, 2 * R, xcd, cb, j);
+    const int hi = j >= R ? 1 : 0;
+    const int hb = 2 * cb + hi, m = j - hi * R;
     gemv_reduce_block<BATCH>(partials, svh, out, out_kind, R, N, n_kc, hb, m);
 }
 
@@ -664,6 +685,7 @@ struct FanParams {
     float* partials[MAX_FAN];
     int N[MAX_FAN];
     int bits[MAX_FAN];
+    int xcd;                    // items and finish keyed by the fan's column block (xcd_split)
     int block0[MAX_FAN + 1];    // partial-sum items: member j owns [block0[j], block0[j+1])
     int rblock0[MAX_FAN + 1];   // finish items (128 columns x row): member j owns [rblock0[j], rblock0[j+1])
 };
@@ -679,17 +701,24 @@ __device__ __forceinline__ int fan_member(const int (&first)[MAX_FAN + 1], int c
 template <int BITS, int CB, int W, int RB>
 __global__ __launch_bounds__(64 * W) void gemv_fan_kernel(FanParams P) {
     __shared__ uint16_t xa[MAX_ROWS * RB * GEMV_NSTEP_CAP * STEP_K];
-    const int j = fan_member(P.block0, P.count, blockIdx.x);
+    // the members' column blocks in order are the fan's column blocks
+    int g, jj;
+    xcd_split(blockIdx.x, P.n_kc, P.xcd, g, jj);
+    const int i = g * P.n_kc + jj;
+    const int j = fan_member(P.block0, P.count, i);
     if (P.bits[j] != BITS) return;
-    const int local = blockIdx.x - P.block0[j];
+    const int local = i - P.block0[j];
     const int cb = local / P.n_kc, kc = local - (local / P.n_kc) * P.n_kc;
     gemv_item<BITS, CB, W, RB, false>(P.x, P.trellis[j], P.suh[j], P.R, P.K, P.N[j], P.nsteps, cb, kc, P.partials[j], xa);
 }
 
 template <int BATCH>
 __global__ __launch_bounds__(64) void gemv_fan_reduce_kernel(FanParams P) {
-    const int j = fan_member(P.rblock0, P.count, blockIdx.x);
-    const int local = blockIdx.x - P.rblock0[j];
+    int g, jj;
+    xcd_split(blockIdx.x, 2 * P.R, P.xcd, g, jj);
+    const int i = g * 2 * P.R + jj;
+    const int j = fan_member(P.rblock0, P.count, i);
+    const int local = i - P.rblock0[j];
     const int hb = local / P.R, m = local - (local / P.R) * P.R;
     gemv_reduce_block<BATCH>(P.partials[j], P.svh[j], P.out[j], P.out_kind, P.R, P.N[j], P.n_kc, hb, m);
 }

@@ -43,12 +43,12 @@ static void launch_gemv_w(const GemvArgs& a) {
     const dim3 grid(a.plan.n_cb * a.plan.n_kc), block(64 * W);
     if (a.plan.split_reduce)
         hipLaunchKernelGGL((gemv_kernel<B, C, W, RB, true>), grid, block, 0, a.stream, a.x, a.trellis, a.suh,
-                           a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps, a.plan.n_kc, a.counters,
-                           a.partials);
+                           a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps, a.plan.n_kc, a.plan.xcd ? 1 : 0,
+                           a.counters, a.partials);
     else
         hipLaunchKernelGGL((gemv_kernel<B, C, W, RB, false>), grid, block, 0, a.stream, a.x, a.trellis, a.suh,
-                           a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps, a.plan.n_kc, a.counters,
-                           a.partials);
+                           a.svh, a.out, a.out_kind, a.R, a.K, a.N, a.plan.nsteps, a.plan.n_kc, a.plan.xcd ? 1 : 0,
+                           a.counters, a.partials);
 }
 
 // Up to 16 rows: one MFMA row block, 1, 2 or 4 column groups; 17-32 rows:

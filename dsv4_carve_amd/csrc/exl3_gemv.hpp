@@ -105,6 +105,35 @@ __device__ __forceinline__ uint16_t decode_half(const uint32_t* W) {
     return codebook_half<CB, WinSel<BITS, T>::HI>(win_src<BITS, T>(W));
 }
 
+// ---------------------------------------------------------------- XCD-keyed item order
+//
+// A launch's workgroups go to the 8 XCDs in turn (workgroup b runs on XCD
+// b % 8), and what a launch writes stays in that XCD's L2 for the launches
+// after it, while a read from another XCD goes to memory: writing 8 MB and
+// reading it back in the next launch took 4.9 us per pair from the writing
+// XCDs and 8.3 us from the others.  A launch whose output the next launch
+// reads can therefore order its items by a group key the reader shares: every
+// item of group g runs on XCD g % 8, and so does the reader's item for g.
+// Item j of group g is workgroup 8 (per_group (g / 8) + j) + g % 8, a
+// bijection onto the same grid when the group count is a multiple of 8.
+// The dense GEMV and its split-K finish use it (16 rows of 4096x4096: 14.0
+// against 16.0 us); in the routed-MoE phased launches the same keys (gate/up
+// by column block of I, down and finish by column block of H) measured the
+// same as the slot-major order at 1-16 rows, so they keep that order.
+constexpr int N_XCD = 8;
+
+// Item (g, j) of workgroup b: with `on` (0 or 1) the XCD-keyed order above,
+// otherwise g = b / per_group, j = b % per_group.  One division and no branch
+// on `on`: a branch on a kernel argument makes the kernel wait for that
+// argument before it requests the others.
+__device__ __forceinline__ void xcd_split(int b, int per_group, int on, int& g, int& j) {
+    const unsigned ub = (unsigned)b, t = ub / N_XCD, x = ub % N_XCD;
+    const unsigned d = on ? t : ub;
+    const unsigned q = d / (unsigned)per_group;
+    g = (int)(on ? x + N_XCD * q : q);
+    j = (int)(d - q * (unsigned)per_group);
+}
+
 // ---------------------------------------------------------------- tile loads
 
 // Register buffer for one tile.  CAP (16-byte vectors) may exceed the 2*BITS a
