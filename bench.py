@@ -633,6 +633,43 @@ def time_read_ceiling(dev, gib: int = 2, reps: int = 10) -> dict:
             **res}
 
 
+def time_handoff(dev, blocks: int = 2048, pairs: int = 100, reps: int = 3) -> dict:
+    """Cross-launch hand-off through the XCDs' L2s (csrc/exl3_probe.hip
+    probe_handoff_*): a launch writes 4 KB per workgroup (8 MB over 2048
+    workgroups), the next reads it back; us per (write, read) pair, in a
+    captured graph of `pairs` pairs, when each reading workgroup reads a
+    region written on its own XCD (shift a multiple of 8) or on another one.
+    This is what the dense GEMV's XCD-keyed item order relies on."""
+    import ctypes
+
+    import torch
+    from dsv4_carve_amd import build as B
+
+    lib = ctypes.CDLL(B.PROBE_LIB)
+    lib.exl3_probe_handoff.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_void_p]
+    lib.exl3_probe_handoff.restype = ctypes.c_int
+    buf = torch.empty(blocks * 256 * 4, dtype=torch.int32, device=dev)
+    sink = torch.empty(blocks * 256, dtype=torch.int32, device=dev)
+    res = {}
+    for shift in (0, 8, 1, 3):
+        s = torch.cuda.Stream(dev)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            assert lib.exl3_probe_handoff(buf.data_ptr(), sink.data_ptr(), blocks, shift, 1, s.cuda_stream) == 0
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                assert lib.exl3_probe_handoff(buf.data_ptr(), sink.data_ptr(), blocks, shift, pairs,
+                                              s.cuda_stream) == 0
+        times = []
+        for _ in range(reps + 1):
+            times.append(_replay_timed(g) * 1e3 / pairs)
+        res[f"shift_{shift}"] = round(sorted(times[1:])[len(times[1:]) // 2], 3)
+        del g
+    return {"unit": "us per (write, read) pair", "bytes": blocks * 256 * 16, "own_xcd": [res["shift_0"], res["shift_8"]],
+            "other_xcd": [res["shift_1"], res["shift_3"]], **res}
+
+
 def time_decode_ceiling(dev, iters: int = 512, reps: int = 5) -> dict:
     """Decode-rate ceiling: the decode kernels' inner loop (decode + MFMA on
     tiles held in registers, csrc/exl3_probe.hip) at their residency of two
@@ -1005,6 +1042,8 @@ def main() -> int:
     if "ceiling" in legs:
         extra["hbm_read_ceiling"] = time_read_ceiling(dev)
         print(f"[bench] read ceiling: {extra['hbm_read_ceiling']}", file=sys.stderr, flush=True)
+        extra["xcd_handoff"] = time_handoff(dev)
+        print(f"[bench] cross-launch hand-off: {extra['xcd_handoff']}", file=sys.stderr, flush=True)
         dc = time_decode_ceiling(dev)
         floor = decode_floor_us(dc, a.rows, layer.bits, HIDDEN, INTER, TOPK, seed=a.rows)
         mem = nbytes / (extra["hbm_read_ceiling"]["best_p50_GBps"] * 1e9) * 1e6

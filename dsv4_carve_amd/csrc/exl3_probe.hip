@@ -625,6 +625,27 @@ static void isa_dispatch(int op, int blocks, int iters, uint32_t* sink, uint64_t
     ((op == OPS ? launch_isa<OPS>(blocks, iters, sink, clk, st) : void()), ...);
 }
 
+// ---------------------------------------------------------------- cross-launch hand-off
+//
+// Does what one launch writes stay in the writing XCD's L2 for the next?
+// probe_handoff_write: workgroup b writes 256 16-byte vectors at region b.
+// probe_handoff_read: workgroup b reads region (b + shift) % blocks.
+// Workgroups go to the XCDs in turn, so a shift that is a multiple of 8 reads
+// data written on the reading workgroup's own XCD.
+constexpr int HANDOFF_THREADS = 256;
+
+__global__ __launch_bounds__(HANDOFF_THREADS) void probe_handoff_write(u32x4_t* buf, uint32_t salt) {
+    const uint32_t i = blockIdx.x * HANDOFF_THREADS + threadIdx.x;
+    buf[i] = u32x4_t{i + salt, 2u * i, 3u * i, 4u * i};
+}
+
+__global__ __launch_bounds__(HANDOFF_THREADS) void probe_handoff_read(const u32x4_t* buf, uint32_t* sink,
+                                                                      int shift) {
+    const uint32_t src = (blockIdx.x + (uint32_t)shift) % gridDim.x;
+    const u32x4_t v = buf[src * HANDOFF_THREADS + threadIdx.x];
+    sink[blockIdx.x * HANDOFF_THREADS + threadIdx.x] = v[0] ^ v[1] ^ v[2] ^ v[3];
+}
+
 extern "C" {
 
 // Launches the probe over bytes (a multiple of 16) at buf; sink holds one
@@ -638,6 +659,21 @@ int exl3_probe_read(const void* buf, int64_t bytes, uint32_t* sink, int blocks, 
 }
 
 int exl3_probe_threads(void) { return PROBE_THREADS; }
+
+// `pairs` (write, read) launch pairs over `blocks` workgroups: buf holds
+// blocks * 256 16-byte vectors, sink blocks * 256 uint32.  The read launch of
+// each pair reads the region written `shift` workgroups on (0 <= shift).
+int exl3_probe_handoff(void* buf, uint32_t* sink, int blocks, int shift, int pairs, void* stream) {
+    if (!buf || !sink || blocks < 1 || shift < 0 || pairs < 1) return -1;
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    for (int k = 0; k < pairs; ++k) {
+        hipLaunchKernelGGL(probe_handoff_write, dim3(blocks), dim3(HANDOFF_THREADS), 0, st,
+                           reinterpret_cast<u32x4_t*>(buf), (uint32_t)k);
+        hipLaunchKernelGGL(probe_handoff_read, dim3(blocks), dim3(HANDOFF_THREADS), 0, st,
+                           reinterpret_cast<const u32x4_t*>(buf), sink, shift);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 // Launches `blocks` single-wave workgroups of the decode-rate probe at `bits`
 // (2, 3, 4 or 6; MCG codebook) in `mode` (0 decode + MFMA, 1 decode only, 2
