@@ -348,9 +348,9 @@ inline GemvPlan gemv_plan_cb(int64_t rows, int64_t k, int64_t total_cb, int cus)
 }
 
 // The partial-sum items of a column block and that block's finish run on one
-// XCD (xcd_split), so the finish reads the partials from its own L2, when the
-// column blocks (of a matrix, or of all members of a fan) are whole and a
-// multiple of 8.  EXL3_XCD_ORDER=0 turns it off.
+// XCD (xcd_split) when the column blocks (of a matrix, or of all members of a
+// fan) are whole and a multiple of 8: 16 rows of 4096x4096 14.0 against 16.0
+// us, the gain in the partial-sum launch.  EXL3_XCD_ORDER=0 turns it off.
 inline bool xcd_order_allowed() {
     static const bool off = [] {
         const char* v = getenv("EXL3_XCD_ORDER");
