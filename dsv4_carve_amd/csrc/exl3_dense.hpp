@@ -350,13 +350,11 @@ inline GemvPlan gemv_plan_cb(int64_t rows, int64_t k, int64_t total_cb, int cus)
 // The partial-sum items of a column block and that block's finish run on one
 // XCD (xcd_split) when the column blocks (of a matrix, or of all members of a
 // fan) are whole and a multiple of 8: 16 rows of 4096x4096 14.0 against 16.0
-// us, the gain in the partial-sum launch.  EXL3_XCD_ORDER=0 turns it off.
+// us, the gain in the partial-sum launch.  EXL3_XCD_ORDER=0 turns it off (read
+// at every call, so one process can compare both orders).
 inline bool xcd_order_allowed() {
-    static const bool off = [] {
-        const char* v = getenv("EXL3_XCD_ORDER");
-        return v && *v && atoi(v) == 0;
-    }();
-    return !off;
+    const char* v = getenv("EXL3_XCD_ORDER");
+    return !(v && *v && atoi(v) == 0);
 }
 
 inline GemvPlan gemv_plan(int64_t rows, int64_t k, int64_t n, int cus) {

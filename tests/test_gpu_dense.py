@@ -275,3 +275,36 @@ def test_dequant_nk_is_the_transpose(ops, dev, bits, cb):
     w_t = ops.dequant_trellis_nk(tr, su, sv, bits, mcg=cb == O.CB_MCG, mul1=cb == O.CB_MUL1).cpu().numpy()
     ref = O.dequant_full_c(L["trellis"], L["suh"], L["svh"], bits, cb)
     assert np.array_equal(w_t.view(np.uint16).T, ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("rows", [1, 16, 32])
+def test_xcd_keyed_order_is_bitwise_the_plain_order(ops, dev, monkeypatch, rows):
+    """The XCD-keyed item order (a column block's split-K items and its finish
+    on one XCD) only moves items between workgroups: a 4096x4096 call and a fan
+    whose column blocks are a multiple of 8 give bitwise the outputs of the
+    plain order (EXL3_XCD_ORDER=0), and match the oracle."""
+    import torch
+
+    k, n, bits = 4096, 4096, 3
+    L = synth.dense(k, n, bits, seed=910)
+    t, u, v = (to_dev(L[key], dev) for key in ("trellis", "suh", "svh"))
+    x_np = synth.activations(rows, k, seed=911)
+    x = to_dev(x_np, dev)
+    fan_ns = (1024, 512, 1024, 1024, 256, 256)          # 16 column blocks
+    fan = [synth.dense(k, fn, 6, seed=920 + i) for i, fn in enumerate(fan_ns)]
+    members = [tuple(to_dev(f[key], dev) for key in ("trellis", "suh", "svh")) for f in fan]
+
+    def run():
+        y = ops.gemm(x, t, u, v, ops.CB_MCG, torch.float32)
+        ys = ops.gemm_group(x, members, ops.CB_MCG, torch.float32) if rows <= 16 else []
+        torch.cuda.synchronize()
+        return [y.cpu().numpy()] + [z.cpu().numpy() for z in ys]
+
+    monkeypatch.setenv("EXL3_XCD_ORDER", "0")
+    plain = run()
+    monkeypatch.delenv("EXL3_XCD_ORDER")
+    keyed = run()
+    for a, b in zip(plain, keyed):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    ref = O.linear(x_np, L["trellis"], L["suh"], L["svh"], bits, O.CB_MCG)
+    assert_close(keyed[0], ref, what=f"keyed order rows={rows}")
